@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Benchmark of the shape-aware GEMM path on one MI355X.
+
+Headline: the BF16 prefill projection C[2048,4096] = A[2048,1024] W[4096,1024]^T
+(bf16 out, fp32 accumulate) on the kernel the selection table picks.  A step
+is one GEMM over resident inputs; K steps are captured back to back in one
+HIP graph (launch gaps of the host excluded, as the reference's adaptive
+repeat loop of cuda_kernels/gemm/src/gemm_bench.cu:198-223 excludes them)
+and timed with HIP events on the stream they run on.
+
+Alongside (extra keys of the same JSON line): the decode GEMMs M in
+{1,4,8,16,32} x N=6144 x K=1024 with W rotated over more than twice the
+256 MB Infinity Cache, the FP32 1024^3 GEMM, the FP16 down projection, the
+BF16 LM head, torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
+for comparison only, and the CPU baseline (host F.linear, multi-threaded).
+
+Prints ONE JSON line on stdout; a readable table goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+PEAK_MFMA_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # MI355X dense
+PEAK_HBM_GBS = 8000.0
+INFINITY_CACHE_BYTES = 256 * 2 ** 20
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_bf16_prefill_2048x4096x1024.md"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=100)
+    p.add_argument("--no-extras", action="store_true", help="headline only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-vendor", action="store_true", help="skip the torch GPU GEMM comparison")
+    p.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
+    return p.parse_args()
+
+
+class GraphTimer:
+    """Captures a list of launches into one HIP graph and times a replay."""
+
+    def __init__(self, torch, launches):
+        self.torch = torch
+        self.graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            launches[0]()   # first launch outside capture
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(self.graph):
+            for f in launches:
+                f()
+        torch.cuda.synchronize()
+
+    def time_ms(self) -> float:
+        t = self.torch
+        start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        t.cuda.synchronize()
+        start.record()
+        self.graph.replay()
+        end.record()
+        t.cuda.synchronize()
+        return start.elapsed_time(end)
+
+
+def median_graph_ms(torch, launches, trials=5) -> float:
+    """Median over trials of (graph replay time / launches), in ms."""
+    timer = GraphTimer(torch, launches)
+    timer.time_ms()
+    samples = sorted(timer.time_ms() / len(launches) for _ in range(trials))
+    return samples[len(samples) // 2]
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 PMC summary, or None."""
+    if not TRAFFIC_FILE.is_file():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this GEMM path runs on one MI355X per process and has no "
+              "multi-GPU mode (run with --gpus 1).", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    L = pkg._lib
+    L.load()                      # raises if the HIP library is not built
+    W = pkg.workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    code = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16}
+    dname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+    def launcher(a, b, c, m, n, k, layout, din, dout):
+        ldb = k if layout == L.B_NK else n
+        args_ = (a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, k, ldb, n, layout, code[din], code[dout])
+
+        def f():
+            L.gemm_raw(*args_, torch.cuda.current_stream().cuda_stream)
+        return f
+
+    # ---------------------------------------------------------------- headline
+    name = W.HEADLINE
+    wl = W.WORKLOADS[name]
+    m, n, k = wl.ms[0], wl.n, wl.k
+    a, w = W.make_inputs(name, m, device=dev)
+    out = torch.empty(m, n, dtype=wl.dtype_out, device=dev)
+    kid = L.select(m, n, k, k, k, n, wl.b_layout, code[wl.dtype_in], code[wl.dtype_out], True)
+    kernel = L.kernel_name(kid)
+    flops = W.problem_flops(m, n, k)
+    launch = launcher(a, w, out, m, n, k, wl.b_layout, wl.dtype_in, wl.dtype_out)
+    log(f"headline {name}: kernel {kernel}, warmup {args.warmup}, steps {args.steps}")
+    if args.warmup > 0:
+        GraphTimer(torch, [launch] * args.warmup).time_ms()
+    timer = GraphTimer(torch, [launch] * args.steps)
+    torch.cuda.synchronize()
+    elapsed_ms = timer.time_ms()
+    torch.cuda.synchronize()
+    ms_per_step = elapsed_ms / args.steps
+    tflops = flops / (ms_per_step * 1e-3) / 1e12
+    peak = PEAK_MFMA_TFLOPS[dname[wl.dtype_in]]
+    log(f"  {ms_per_step * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  {100 * tflops / peak:.1f}% of {peak} TFLOP/s")
+
+    result = {
+        "metric": "TFLOP/s & % MFMA peak (prefill GEMM); HBM GB/s & % peak (decode M<=32)",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, rounded to bf16)",
+        "config": {"workload": name, "m": m, "n": n, "k": k, "b_layout": "W[N,K]", "out_dtype": "bf16",
+                   "kernel": kernel, "timing": "K launches back to back in one HIP graph, HIP events"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": read_traffic(),
+                     "algorithmic_flops_per_launch": flops,
+                     "algorithmic_bytes_per_launch": W.problem_bytes(m, n, k, wl.dtype_in, wl.dtype_out)},
+    }
+
+    # ------------------------------------------------------------ decode rows
+    extras = {}
+    if not args.no_extras:
+        dname_ = "bf16_decode_n6144_k1024"
+        dw = W.WORKLOADS[dname_]
+        w_bytes = dw.n * dw.k * 2
+        copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / w_bytes) + 1)
+        _, w0 = W.make_inputs(dname_, 1, device=dev)
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        rows = []
+        for dm in dw.ms:
+            a_d, _ = W.make_inputs(dname_, dm, device=dev)
+            o_d = torch.empty(dm, dw.n, dtype=dw.dtype_out, device=dev)
+            launches = [launcher(a_d, ws[i % copies], o_d, dm, dw.n, dw.k, L.B_NK, dw.dtype_in, dw.dtype_out)
+                        for i in range(copies * 10)]
+            t_ms = median_graph_ms(torch, launches)
+            byts = W.problem_bytes(dm, dw.n, dw.k, dw.dtype_in, dw.dtype_out)
+            gbs = byts / (t_ms * 1e-3) / 1e9
+            kd = L.kernel_name(L.select(dm, dw.n, dw.k, dw.k, dw.k, dw.n, L.B_NK, L.BF16, L.BF16, True))
+            rows.append({"m": dm, "us": round(t_ms * 1e3, 3), "GB/s": round(gbs, 1),
+                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": kd, "w_buffers": copies})
+            log(f"decode M={dm:2d}: {t_ms * 1e3:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM ({kd})")
+        extras["decode_bf16_n6144_k1024"] = rows
+        del ws
+
+        # ------------------------------------------------ other workloads
+        other = []
+        for oname in ("fp32_square_1024", "fp16_down_4096x1024x3584", "bf16_lm_head_n151936_k1024"):
+            ow = W.WORKLOADS[oname]
+            for om in ow.ms:
+                a_o, b_o = W.make_inputs(oname, om, device=dev)
+                o_o = torch.empty(om, ow.n, dtype=ow.dtype_out, device=dev)
+                b_bytes = b_o.numel() * b_o.element_size()
+                nbuf = 2 if ow.bound == "hbm" else 1
+                bs = [b_o] + [b_o.clone() for _ in range(nbuf - 1)]
+                reps = 20 if b_bytes > 2 ** 27 else 100
+                launches = [launcher(a_o, bs[i % nbuf], o_o, om, ow.n, ow.k, ow.b_layout, ow.dtype_in,
+                                     ow.dtype_out) for i in range(reps)]
+                t_ms = median_graph_ms(torch, launches, trials=3)
+                fl = W.problem_flops(om, ow.n, ow.k)
+                byts = W.problem_bytes(om, ow.n, ow.k, ow.dtype_in, ow.dtype_out)
+                tf = fl / (t_ms * 1e-3) / 1e12
+                gbs = byts / (t_ms * 1e-3) / 1e9
+                pk = PEAK_MFMA_TFLOPS[dname[ow.dtype_in]]
+                ldb = ow.k if ow.b_layout == L.B_NK else ow.n
+                ko = L.kernel_name(L.select(om, ow.n, ow.k, ow.k, ldb, ow.n, ow.b_layout, code[ow.dtype_in],
+                                            code[ow.dtype_out], True))
+                other.append({"workload": oname, "m": om, "us": round(t_ms * 1e3, 3), "TFLOP/s": round(tf, 2),
+                              "frac_mfma": round(tf / pk, 4), "GB/s": round(gbs, 1),
+                              "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": ko})
+                log(f"{oname} M={om}: {t_ms * 1e3:.1f} us  {tf:.1f} TFLOP/s ({100 * tf / pk:.1f}%)  "
+                    f"{gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)  [{ko}]")
+                del bs, a_o, b_o, o_o
+        extras["other_workloads"] = other
+
+    # ------------------------------------------ vendor comparison (not used)
+    if not args.no_vendor:
+        F = torch.nn.functional
+
+        def vendor(aa, ww):
+            def f():
+                F.linear(aa, ww)
+            return f
+        try:
+            t_ms = median_graph_ms(torch, [vendor(a, w)] * 200)
+            vt = flops / (t_ms * 1e-3) / 1e12
+            extras["vendor_torch_linear_prefill"] = {"us": round(t_ms * 1e3, 3), "TFLOP/s": round(vt, 2),
+                                                     "note": "torch.matmul on the GPU (hipBLASLt/rocBLAS), "
+                                                             "comparison only, never dispatched to"}
+            log(f"vendor torch.matmul prefill: {t_ms * 1e3:.2f} us  {vt:.1f} TFLOP/s")
+        except Exception as exc:  # comparison only; never fails the bench
+            extras["vendor_torch_linear_prefill"] = {"error": str(exc)[:200]}
+
+    # ------------------------------------------------------------ CPU baseline
+    if not args.no_cpu:
+        from oracle import cpu_baseline
+
+        a_cpu, w_cpu = W.make_inputs(name, m)
+        cb = cpu_baseline.time_cpu_gemm(a_cpu, w_cpu, True, wl.dtype_out, budget_s=args.cpu_budget)
+        cpu_tf = flops / cb["seconds"] / 1e12
+        result["cpu_baseline"] = {
+            "value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
+            "sample": f"full {m}x{n}x{k} bf16 F.linear on the host CPU ({cb['cpu_model']}, "
+                      f"{cb['threads']} threads of {cb['cpu_count']}), median of {cb['samples']} calls",
+        }
+        log(f"cpu baseline: {cb['seconds'] * 1e3:.1f} ms/call  {cpu_tf:.3f} TFLOP/s on {cb['threads']} threads")
+
+    result.update(extras)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,147 @@
+/*
+ * nanovllm_gemm.h — C ABI of the MI355X (gfx950) shape-aware GEMM library.
+ *
+ * One library, libnanovllm_gemm.so, built by hipcc for gfx950.  Every entry
+ * point takes plain device pointers, sizes and an opaque HIP stream; there
+ * are no torch types in any signature and no C++ exception crosses the
+ * boundary.  Errors come back as negative return codes, with a thread-local
+ * message from nanovllm_gemm_last_error().
+ *
+ * Problem computed by every GEMM entry point (row-major, fp32 accumulate):
+ *
+ *     C[m, n] = sum_k A[m, k] * B(k, n)
+ *
+ *   A  : [M, K] row-major, element (m, k) at a[m * lda + k]
+ *   B  : b_layout == NANOVLLM_GEMM_B_NK: W[N, K] row-major (the nn.Linear
+ *        weight layout), B(k, n) = b[n * ldb + k]
+ *        b_layout == NANOVLLM_GEMM_B_KN: B[K, N] row-major,
+ *        B(k, n) = b[k * ldb + n]
+ *   C  : [M, N] row-major, element (m, n) at c[m * ldc + n]
+ *
+ * Supported dtype pairs (in -> out): f32->f32, f16->{f16,f32},
+ * bf16->{bf16,f32}.  A and B share the input dtype.  Narrow outputs are the
+ * round-to-nearest-even image of the fp32 accumulator.
+ *
+ * Reference interfaces these replace (paths relative to the reference repo):
+ *   - cuda_kernels/gemm/src/gemm_bench.cu:80-196   wmma_direct_kernel / wmma_staged_kernel
+ *     launched at :349-369 with B[K,N] and FP32 output;
+ *   - cuda_kernels/gemm/src/gemm_wmma.cu:34-207    scalar / WMMA / staged kernels, B = W[N,K];
+ *   - cuda_kernels/gemm/src/gemm_tiled.cu:36-202   FP32 naive / tiled / register-tiled kernels;
+ *   - cuda_kernels/gemm/src/gemm.cu:7-15           FP32 one-thread-per-output kernel;
+ *   - cuda_kernels/gemm/src/gemm_bench.cu:252-282  supports_wmma / choose_path / path_name;
+ *   - nanovllm/layers/linear.py:51,73,153 and nanovllm/layers/embed_head.py:61
+ *     F.linear(x, W) call sites (W[N,K], the NK layout here).
+ */
+#ifndef NANOVLLM_GEMM_H
+#define NANOVLLM_GEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types.  Values are part of the ABI. */
+enum {
+    NANOVLLM_GEMM_F32 = 0,
+    NANOVLLM_GEMM_F16 = 1,
+    NANOVLLM_GEMM_BF16 = 2
+};
+
+/* Layout of the second operand.  Values are part of the ABI. */
+enum {
+    NANOVLLM_GEMM_B_NK = 0, /* W[N, K] row-major (nn.Linear weight)   */
+    NANOVLLM_GEMM_B_KN = 1  /* B[K, N] row-major (gemm_bench.cu:103)  */
+};
+
+/* Kernel identifiers returned by nanovllm_gemm_select().  The ladder
+ * mirrors the reference's rungs; none of them is a vendor-library call.
+ *   FP32_NAIVE     one thread per output            (gemm.cu:7-15, gemm_tiled.cu:36-51)
+ *   FP32_TILED     LDS-tiled fp32 MFMA kernel       (gemm_tiled.cu:56-202)
+ *   MFMA_DIRECT    one wave per 32x32 C tile, operands straight from
+ *                  global memory, any shape          (gemm_bench.cu:80-115, gemm_wmma.cu:56-104)
+ *   MFMA_STAGED    LDS multi-buffered macro-tile MFMA kernel for
+ *                  prefill-shaped problems           (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
+ *   SPLITK_DECODE  split-K wavefront-reduction kernel for M <= 32 that
+ *                  streams W once                    (replaces the cuBLAS fallback of
+ *                                                     gemm_bench.cu:260-273 for decode shapes)
+ */
+enum {
+    NANOVLLM_GEMM_KERNEL_FP32_NAIVE = 0,
+    NANOVLLM_GEMM_KERNEL_FP32_TILED = 1,
+    NANOVLLM_GEMM_KERNEL_MFMA_DIRECT = 2,
+    NANOVLLM_GEMM_KERNEL_MFMA_STAGED = 3,
+    NANOVLLM_GEMM_KERNEL_SPLITK_DECODE = 4,
+    NANOVLLM_GEMM_KERNEL_COUNT = 5
+};
+
+/* Return codes. */
+enum {
+    NANOVLLM_GEMM_OK = 0,
+    NANOVLLM_GEMM_EINVAL = -1,      /* bad size, stride, pointer or enum  */
+    NANOVLLM_GEMM_EUNSUPPORTED = -2, /* dtype pair / kernel cannot run it  */
+    NANOVLLM_GEMM_ELAUNCH = -3      /* HIP reported an error at launch    */
+};
+
+/*
+ * Shape-aware GEMM.  Picks the kernel with nanovllm_gemm_select() and
+ * enqueues it on `stream` (a hipStream_t; NULL is the default stream).
+ * Asynchronous: no host synchronisation, no allocation, capturable into a
+ * HIP graph.  Replaces choose_path + the launch lambdas of
+ * gemm_bench.cu:260-273, 349-369 and the F.linear call of linear.py:51.
+ * Returns NANOVLLM_GEMM_OK or a negative code.
+ */
+int nanovllm_gemm(const void* a, const void* b, void* c,
+                  int64_t m, int64_t n, int64_t k,
+                  int64_t lda, int64_t ldb, int64_t ldc,
+                  int b_layout, int dtype_in, int dtype_out,
+                  void* stream);
+
+/*
+ * Same problem, forced onto one kernel of the ladder (for parity tests of
+ * every rung and for the benchmark ladder, like gemm_bench.cu:396-416
+ * timing direct and staged side by side).  Returns
+ * NANOVLLM_GEMM_EUNSUPPORTED when that kernel cannot run the problem
+ * (checked by nanovllm_gemm_kernel_supports()).
+ */
+int nanovllm_gemm_with_kernel(int kernel_id,
+                              const void* a, const void* b, void* c,
+                              int64_t m, int64_t n, int64_t k,
+                              int64_t lda, int64_t ldb, int64_t ldc,
+                              int b_layout, int dtype_in, int dtype_out,
+                              void* stream);
+
+/*
+ * Shape-selection table: the kernel nanovllm_gemm() would launch for this
+ * problem, given that the pointers are 16-byte aligned when `aligned16` is
+ * non-zero.  Pure host function; callable without a GPU.  Replaces
+ * supports_wmma + choose_path (gemm_bench.cu:252-273).  Returns a kernel id
+ * or a negative code for an invalid problem.
+ */
+int nanovllm_gemm_select(int64_t m, int64_t n, int64_t k,
+                         int64_t lda, int64_t ldb, int64_t ldc,
+                         int b_layout, int dtype_in, int dtype_out,
+                         int aligned16);
+
+/* 1 when `kernel_id` can run the problem, else 0.  Pure host function. */
+int nanovllm_gemm_kernel_supports(int kernel_id,
+                                  int64_t m, int64_t n, int64_t k,
+                                  int64_t lda, int64_t ldb, int64_t ldc,
+                                  int b_layout, int dtype_in, int dtype_out,
+                                  int aligned16);
+
+/* Stable name of a kernel id ("fp32_tiled", "mfma_staged", ...), or
+ * "unknown".  Mirrors path_name (gemm_bench.cu:275-282). */
+const char* nanovllm_gemm_kernel_name(int kernel_id);
+
+/* Message describing the last error on the calling thread ("" if none). */
+const char* nanovllm_gemm_last_error(void);
+
+/* Library version, (major << 16) | minor. */
+int nanovllm_gemm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOVLLM_GEMM_H */

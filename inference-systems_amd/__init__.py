@@ -1,0 +1,14 @@
+"""MI355X-native shape-aware GEMM for nano-vLLM linear layers.
+
+Importable as ``inference_systems_amd`` (the directory name carries a
+hyphen, so it is registered under that name by the loaders in
+``__graft_entry__.py`` and ``tests/conftest.py``).
+
+  _lib      ctypes binding of libnanovllm_gemm.so (the C ABI)
+  kernels   the ``nanovllm::gemm`` / ``nanovllm::gemm_kn`` torch ops
+  build     hipcc recipe for the library
+"""
+from . import _lib, workloads
+from .kernels import gemm, gemm_kn, gemm_with_kernel, linear, selected_kernel
+
+__all__ = ["_lib", "workloads", "gemm", "gemm_kn", "gemm_with_kernel", "linear", "selected_kernel"]

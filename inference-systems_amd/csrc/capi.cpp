@@ -1,0 +1,193 @@
+// C ABI of libnanovllm_gemm.so: argument validation, the shape-selection
+// table, dispatch to the kernel launchers, and thread-local error text.
+// Declarations and their reference counterparts: include/nanovllm_gemm.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "gemm_common.hpp"
+
+namespace nvg {
+
+namespace {
+thread_local std::string g_last_error;
+
+bool dtype_pair_ok(int din, int dout) {
+    switch (din) {
+        case NANOVLLM_GEMM_F32: return dout == NANOVLLM_GEMM_F32;
+        case NANOVLLM_GEMM_F16: return dout == NANOVLLM_GEMM_F16 || dout == NANOVLLM_GEMM_F32;
+        case NANOVLLM_GEMM_BF16: return dout == NANOVLLM_GEMM_BF16 || dout == NANOVLLM_GEMM_F32;
+        default: return false;
+    }
+}
+
+bool is_half(int dt) { return dt == NANOVLLM_GEMM_F16 || dt == NANOVLLM_GEMM_BF16; }
+
+// Checks sizes, strides and enums; records the reason on failure.
+int validate(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int b_layout, int din,
+             int dout) {
+    if (b_layout != NANOVLLM_GEMM_B_NK && b_layout != NANOVLLM_GEMM_B_KN)
+        return set_error(NANOVLLM_GEMM_EINVAL, "b_layout must be NANOVLLM_GEMM_B_NK (0) or NANOVLLM_GEMM_B_KN (1), got %d",
+                         b_layout);
+    if (din < NANOVLLM_GEMM_F32 || din > NANOVLLM_GEMM_BF16 || dout < NANOVLLM_GEMM_F32 || dout > NANOVLLM_GEMM_BF16)
+        return set_error(NANOVLLM_GEMM_EINVAL, "unknown dtype code (in %d, out %d)", din, dout);
+    if (!dtype_pair_ok(din, dout))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "unsupported dtype pair (in %d, out %d): supported are f32->f32, f16->{f16,f32}, "
+                         "bf16->{bf16,f32}",
+                         din, dout);
+    if (m < 0 || n < 0) return set_error(NANOVLLM_GEMM_EINVAL, "m and n must be non-negative (m=%lld, n=%lld)",
+                                         (long long)m, (long long)n);
+    if (k < 1) return set_error(NANOVLLM_GEMM_EINVAL, "k must be positive (k=%lld)", (long long)k);
+    if (lda < k) return set_error(NANOVLLM_GEMM_EINVAL, "lda (%lld) must be >= k (%lld)", (long long)lda, (long long)k);
+    const int64_t ldb_min = b_layout == NANOVLLM_GEMM_B_NK ? k : n;
+    if (ldb < ldb_min || ldb < 1)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldb (%lld) must be >= %s (%lld)", (long long)ldb,
+                         b_layout == NANOVLLM_GEMM_B_NK ? "k" : "n", (long long)ldb_min);
+    if (ldc < n || ldc < 1)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldc (%lld) must be >= n (%lld)", (long long)ldc, (long long)n);
+    return NANOVLLM_GEMM_OK;
+}
+
+// Half-precision problems whose rows can be read as aligned 16-byte chunks.
+bool vector_ok(int64_t k, int64_t lda, int64_t ldb, int b_layout, int aligned16) {
+    return aligned16 && k % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && b_layout == NANOVLLM_GEMM_B_NK;
+}
+
+// M at or below this is streamed by splitk_decode: the problem is bound by
+// reading W once (arithmetic intensity ~M flop/byte, far under the
+// ~312 flop/byte bf16 ridge of MI355X).
+constexpr int64_t kDecodeMaxM = 32;
+
+bool supports(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldb, int b_layout, int din,
+              int aligned16) {
+    switch (kernel_id) {
+        case NANOVLLM_GEMM_KERNEL_FP32_NAIVE:
+        case NANOVLLM_GEMM_KERNEL_FP32_TILED: return din == NANOVLLM_GEMM_F32;
+        case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return is_half(din);
+        case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16);
+        case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE:
+            return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && m <= kDecodeMaxM;
+        default: return false;
+    }
+}
+
+// The shape-selection table (replaces supports_wmma + choose_path,
+// cuda_kernels/gemm/src/gemm_bench.cu:252-273).  Every valid problem maps
+// to a kernel of this library; there is no vendor fallback.
+int select(int64_t m, int64_t k, int64_t lda, int64_t ldb, int b_layout, int din, int aligned16) {
+    if (din == NANOVLLM_GEMM_F32) return NANOVLLM_GEMM_KERNEL_FP32_TILED;
+    if (vector_ok(k, lda, ldb, b_layout, aligned16)) {
+        if (m <= kDecodeMaxM) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+        return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
+    }
+    return NANOVLLM_GEMM_KERNEL_MFMA_DIRECT;
+}
+
+int run(int kernel_id, const Problem& p, hipStream_t s) {
+    switch (kernel_id) {
+        case NANOVLLM_GEMM_KERNEL_FP32_NAIVE: return launch_fp32_naive(p, s);
+        case NANOVLLM_GEMM_KERNEL_FP32_TILED: return launch_fp32_tiled(p, s);
+        case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return launch_mfma_direct(p, s);
+        case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return launch_mfma_staged(p, s);
+        case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return launch_splitk_decode(p, s);
+        default: return set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+}
+
+int aligned16_of(const void* a, const void* b) {
+    return (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (reinterpret_cast<uintptr_t>(b) % 16 == 0);
+}
+
+int gemm_entry(int forced_kernel, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+               int64_t lda, int64_t ldb, int64_t ldc, int b_layout, int din, int dout, void* stream) {
+    g_last_error.clear();
+    int rc = validate(m, n, k, lda, ldb, ldc, b_layout, din, dout);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m == 0 || n == 0) return NANOVLLM_GEMM_OK;
+    if (a == nullptr || b == nullptr || c == nullptr)
+        return set_error(NANOVLLM_GEMM_EINVAL, "a, b and c must be non-null device pointers");
+    const int al = aligned16_of(a, b);
+    int kernel = forced_kernel;
+    if (kernel < 0) {
+        kernel = select(m, k, lda, ldb, b_layout, din, al);
+    } else if (kernel >= NANOVLLM_GEMM_KERNEL_COUNT) {
+        return set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel);
+    } else if (!supports(kernel, m, k, lda, ldb, b_layout, din, al)) {
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "kernel %s cannot run this problem (m=%lld n=%lld k=%lld)",
+                         nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);
+    }
+    const Problem p{a, b, c, m, n, k, lda, ldb, ldc, b_layout, din, dout};
+    return run(kernel, p, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_launch(const char* kernel) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(NANOVLLM_GEMM_ELAUNCH, "%s launch failed: %s", kernel, hipGetErrorString(e));
+    return NANOVLLM_GEMM_OK;
+}
+
+}  // namespace nvg
+
+extern "C" {
+
+int nanovllm_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                  int64_t ldc, int b_layout, int dtype_in, int dtype_out, void* stream) {
+    return nvg::gemm_entry(-1, a, b, c, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, stream);
+}
+
+int nanovllm_gemm_with_kernel(int kernel_id, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                              int64_t lda, int64_t ldb, int64_t ldc, int b_layout, int dtype_in, int dtype_out,
+                              void* stream) {
+    if (kernel_id < 0) {
+        nvg::g_last_error.clear();
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+    return nvg::gemm_entry(kernel_id, a, b, c, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, stream);
+}
+
+int nanovllm_gemm_select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int b_layout,
+                         int dtype_in, int dtype_out, int aligned16) {
+    nvg::g_last_error.clear();
+    const int rc = nvg::validate(m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    return nvg::select(m, k, lda, ldb, b_layout, dtype_in, aligned16);
+}
+
+int nanovllm_gemm_kernel_supports(int kernel_id, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                                  int64_t ldc, int b_layout, int dtype_in, int dtype_out, int aligned16) {
+    nvg::g_last_error.clear();
+    if (nvg::validate(m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out) != NANOVLLM_GEMM_OK) return 0;
+    return nvg::supports(kernel_id, m, k, lda, ldb, b_layout, dtype_in, aligned16) ? 1 : 0;
+}
+
+const char* nanovllm_gemm_kernel_name(int kernel_id) {
+    switch (kernel_id) {
+        case NANOVLLM_GEMM_KERNEL_FP32_NAIVE: return "fp32_naive";
+        case NANOVLLM_GEMM_KERNEL_FP32_TILED: return "fp32_tiled";
+        case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return "mfma_direct";
+        case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return "mfma_staged";
+        case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return "splitk_decode";
+        default: return "unknown";
+    }
+}
+
+const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
+
+int nanovllm_gemm_version(void) { return (1 << 16) | 0; }
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// Shared definitions for the gfx950 GEMM kernels: problem descriptor,
+// element conversions, MFMA wrappers and the launcher declarations that
+// capi.cpp dispatches to.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nanovllm_gemm.h"
+
+namespace nvg {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// One GEMM problem as it crosses the C ABI (see include/nanovllm_gemm.h).
+struct Problem {
+    const void* a;
+    const void* b;
+    void* c;
+    int64_t m, n, k;
+    int64_t lda, ldb, ldc;
+    int b_layout;
+    int dtype_in;
+    int dtype_out;
+};
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Element conversions.  bf16 and fp16 travel as raw 16-bit patterns.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __builtin_bit_cast(float, uint32_t(h) << 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return float(__builtin_bit_cast(_Float16, h));
+}
+
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint16_t h) {
+    if constexpr (DT == NANOVLLM_GEMM_BF16) return bf16_to_f32(h);
+    else return f16_to_f32(h);
+}
+
+// fp32 -> bf16, round to nearest, ties to even; NaN stays a quiet NaN.
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+// fp32 -> fp16 through the hardware conversion (round to nearest even in
+// the default mode; overflow to infinity).
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Store one fp32 accumulator as the output element type.
+template <int DT_OUT>
+__device__ __forceinline__ void store_elem(void* c, int64_t idx, float v) {
+    if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
+        static_cast<float*>(c)[idx] = v;
+    } else if constexpr (DT_OUT == NANOVLLM_GEMM_BF16) {
+        static_cast<uint16_t*>(c)[idx] = f32_to_bf16_rne(v);
+    } else {
+        static_cast<uint16_t*>(c)[idx] = f32_to_f16_rne(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers (gfx950).  Operands are 8 packed 16-bit values per lane,
+// passed as raw bits.
+//
+// v_mfma_f32_32x32x16_{bf16,f16}: lane l holds row (l % 32) of the first
+// operand and column (l % 32) of the second, at k = 8 * (l / 32) + [0, 8);
+// accumulator register v of lane l is D[8*(v/4) + 4*(l/32) + v%4][l % 32].
+//
+// v_mfma_f32_16x16x32_{bf16,f16}: lane l holds row (l % 16) / column
+// (l % 16) at k = 8 * (l / 16) + [0, 8); accumulator v of lane l is
+// D[4*(l/16) + v][l % 16].
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ f32x16_t mfma_32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
+    if constexpr (DT == NANOVLLM_GEMM_BF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+    if constexpr (DT == NANOVLLM_GEMM_BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+}
+
+// 16-byte global load.
+__device__ __forceinline__ u32x4_t load16(const void* p) {
+    return *static_cast<const u32x4_t*>(p);
+}
+
+// ---------------------------------------------------------------------------
+// XCD-aware workgroup order.  Workgroups are handed to the 8 XCDs round
+// robin (workgroup w runs on XCD w % 8), and each XCD has its own L2.  The
+// remap gives XCD x a contiguous run of logical tile ids, and the grouped
+// row-major order below turns such a run into a compact block of tiles
+// that share A rows and W rows inside that XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_remap(int wg, int total) {
+    const int per = total / kNumXcd;
+    const int full = per * kNumXcd;
+    if (wg >= full) return wg;
+    return (wg % kNumXcd) * per + (wg / kNumXcd);
+}
+
+// Logical tile id -> (tile_m, tile_n), walking `group_m` tile rows at a
+// time so that consecutive ids stay inside a group_m-tall band.
+__device__ __forceinline__ void grouped_tile(int t, int tiles_m, int tiles_n, int group_m,
+                                             int& tm, int& tn) {
+    const int per_group = group_m * tiles_n;
+    const int g = t / per_group;
+    const int first_m = g * group_m;
+    const int rows = min(tiles_m - first_m, group_m);
+    const int r = t - g * per_group;
+    tm = first_m + r % rows;
+    tn = r / rows;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (one per kernel family).  Each returns NANOVLLM_GEMM_OK or a
+// negative code; the caller has already validated the problem and checked
+// that the kernel supports it.
+// ---------------------------------------------------------------------------
+int launch_fp32_naive(const Problem& p, hipStream_t s);
+int launch_fp32_tiled(const Problem& p, hipStream_t s);
+int launch_mfma_direct(const Problem& p, hipStream_t s);
+int launch_mfma_staged(const Problem& p, hipStream_t s);
+int launch_splitk_decode(const Problem& p, hipStream_t s);
+
+// Records a message for nanovllm_gemm_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+
+// Converts a hipError_t after a launch into a return code.
+int check_launch(const char* kernel);
+
+}  // namespace nvg

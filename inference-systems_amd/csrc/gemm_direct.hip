@@ -1,0 +1,120 @@
+// mfma_direct: BF16/FP16 GEMM with one wave per 32x32 output tile and the
+// matrix-core operands read straight from global memory (no LDS).  It is
+// the MI355X rung that corresponds to the reference's direct WMMA kernels
+// (cuda_kernels/gemm/src/gemm_bench.cu:80-115 with B[K,N];
+// gemm_wmma.cu:56-104 with B = W[N,K]) and also covers what they skip:
+// partial tiles (gemm_bench.cu:92), K that is not a multiple of 16, odd
+// strides and unaligned pointers.  It is the selection table's fallback for
+// any half-precision problem the faster kernels cannot take.
+#include "gemm_common.hpp"
+
+namespace nvg {
+namespace {
+
+// 8 consecutive 16-bit elements p[0..7] of which only the first `valid`
+// are read; the rest are zero.  Packed as a 16-byte MFMA operand.
+__device__ __forceinline__ u32x4_t load8_masked(const uint16_t* p, int64_t valid) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (2 * i < valid) ? p[2 * i] : 0u;
+        const uint32_t hi = (2 * i + 1 < valid) ? p[2 * i + 1] : 0u;
+        w[i] = lo | (hi << 16);
+    }
+    return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+// 8 elements p[0], p[stride], ..., p[7*stride], the first `valid` read.
+__device__ __forceinline__ u32x4_t load8_strided(const uint16_t* p, int64_t stride, int64_t valid) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (2 * i < valid) ? p[(2 * i) * stride] : 0u;
+        const uint32_t hi = (2 * i + 1 < valid) ? p[(2 * i + 1) * stride] : 0u;
+        w[i] = lo | (hi << 16);
+    }
+    return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+template <int DT, int DT_OUT, int BL>
+__global__ __launch_bounds__(256) void mfma_direct_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, void* __restrict__ c,
+    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
+    int tiles_m, int tiles_n, int vec_a, int vec_b) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int half = lane >> 5;
+    const int r32 = lane & 31;
+
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
+    const int64_t m0 = int64_t(tm) * 64 + (wave >> 1) * 32;
+    const int64_t n0 = int64_t(tn) * 64 + (wave & 1) * 32;
+
+    // Lane l feeds A row (m0 + l%32) and B column (n0 + l%32), K-chunk l/32.
+    const int64_t arow = m0 + r32;
+    const int64_t bcol = n0 + r32;
+    const bool a_in = arow < m;
+    const bool b_in = bcol < n;
+    const uint16_t* ap = a + (a_in ? arow : 0) * lda;
+
+    f32x16_t acc = {};
+    for (int64_t k0 = 0; k0 < k; k0 += 16) {
+        const int64_t kb = k0 + 8 * half;
+        const int64_t kvalid = k - kb;  // may be <= 0 for the tail chunk
+        u32x4_t af, bf;
+        if (!a_in || kvalid <= 0) {
+            af = u32x4_t{0u, 0u, 0u, 0u};
+        } else if (vec_a && kvalid >= 8) {
+            af = load16(ap + kb);
+        } else {
+            af = load8_masked(ap + kb, kvalid);
+        }
+        if (!b_in || kvalid <= 0) {
+            bf = u32x4_t{0u, 0u, 0u, 0u};
+        } else if constexpr (BL == NANOVLLM_GEMM_B_NK) {
+            const uint16_t* bp = b + bcol * ldb + kb;
+            bf = (vec_b && kvalid >= 8) ? load16(bp) : load8_masked(bp, kvalid);
+        } else {
+            bf = load8_strided(b + kb * ldb + bcol, ldb, kvalid);
+        }
+        acc = mfma_32x32x16<DT>(af, bf, acc);
+    }
+
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int64_t row = m0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        if (row < m && b_in) store_elem<DT_OUT>(c, row * ldc + bcol, acc[v]);
+    }
+}
+
+template <int DT, int DT_OUT>
+int launch_typed(const Problem& p, hipStream_t s) {
+    const int64_t tiles_m = (p.m + 63) / 64, tiles_n = (p.n + 63) / 64;
+    if (tiles_m * tiles_n > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "mfma_direct: grid too large");
+    const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n)), block(256);
+    const auto* a = static_cast<const uint16_t*>(p.a);
+    const auto* b = static_cast<const uint16_t*>(p.b);
+    const int vec_a = (reinterpret_cast<uintptr_t>(p.a) % 16 == 0) && (p.lda % 8 == 0);
+    const int vec_b = (reinterpret_cast<uintptr_t>(p.b) % 16 == 0) && (p.ldb % 8 == 0);
+    if (p.b_layout == NANOVLLM_GEMM_B_NK)
+        hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_NK>), grid, block, 0, s, a, b, p.c,
+                           p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), vec_a, vec_b);
+    else
+        hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_KN>), grid, block, 0, s, a, b, p.c,
+                           p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), vec_a, vec_b);
+    return check_launch("mfma_direct");
+}
+
+}  // namespace
+
+int launch_mfma_direct(const Problem& p, hipStream_t s) {
+    if (p.dtype_in == NANOVLLM_GEMM_BF16) {
+        if (p.dtype_out == NANOVLLM_GEMM_BF16) return launch_typed<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_BF16>(p, s);
+        return launch_typed<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_F32>(p, s);
+    }
+    if (p.dtype_out == NANOVLLM_GEMM_F16) return launch_typed<NANOVLLM_GEMM_F16, NANOVLLM_GEMM_F16>(p, s);
+    return launch_typed<NANOVLLM_GEMM_F16, NANOVLLM_GEMM_F32>(p, s);
+}
+
+}  // namespace nvg

@@ -1,0 +1,197 @@
+"""``nanovllm::gemm`` — the shape-aware MI355X GEMM as a PyTorch custom op.
+
+Contract (the F.linear contract of nanovllm/layers/linear.py:51,73,153 and
+nanovllm/layers/embed_head.py:61, without the bias):
+
+    gemm(a[..., K], w[N, K], out_dtype=None) -> out[..., N]
+    out = a @ w.T, accumulated in fp32, stored as out_dtype (default a.dtype)
+
+Supported (in -> out): fp32 -> fp32, fp16 -> {fp16, fp32},
+bf16 -> {bf16, fp32}.  ``gemm_kn(a[..., K], b[K, N])`` is the same op for a
+row-major B[K, N] (the layout of cuda_kernels/gemm/src/gemm_bench.cu:103-106
+and gemm_tiled.cu:16).
+
+The op follows the reference's custom-op conventions:
+  * schema in the ``nanovllm`` namespace (nanovllm/csrc/ops.cpp:48-71);
+  * argument checks that raise ``RuntimeError`` with a fixed message, like
+    the TORCH_CHECKs of nanovllm/csrc/add_kernel.cu:49-63 ("... must be
+    contiguous", "... same dtype", ...);
+  * a fake (meta) implementation for torch.compile (nanovllm/kernels/add.py:11-16);
+  * launch on PyTorch's current stream of the input's device
+    (add_kernel.cu:65-67), so the op is graph-capturable;
+  * a ``torch | hip | auto`` backend switch with a contract-reason check
+    (nanovllm/kernels/gdn.py:138-259), in ``linear`` below.
+
+The HIP path has no substitute: if the native library is missing the op
+raises, and ``auto`` only routes to ``F.linear`` for inputs outside the
+op's contract (CPU tensors, unsupported dtypes), never because the library
+could not be loaded.
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib
+
+_CODE = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+_OUT_OK = {
+    torch.float32: (torch.float32,),
+    torch.float16: (torch.float16, torch.float32),
+    torch.bfloat16: (torch.bfloat16, torch.float32),
+}
+
+BACKENDS = ("torch", "hip", "auto")
+BACKEND_ENV = "NANOVLLM_GEMM_BACKEND"
+
+
+def contract_reason(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None,
+                    b_layout: int = _lib.B_NK) -> Optional[str]:
+    """Why the HIP op cannot take these inputs, or None if it can."""
+    if not (a.is_cuda and b.is_cuda):
+        return "a and w must be CUDA (HIP) tensors"
+    if a.device != b.device:
+        return "a and w must be on the same device"
+    if a.dtype not in _CODE:
+        return "a must be float32, float16 or bfloat16"
+    if b.dtype != a.dtype:
+        return "a and w must have the same dtype"
+    out = a.dtype if out_dtype is None else out_dtype
+    if out not in _OUT_OK[a.dtype]:
+        return f"out_dtype {out} is not supported for {a.dtype} inputs"
+    if b.dim() != 2:
+        return "w must be 2-D"
+    if a.dim() < 1:
+        return "a must have at least one dimension"
+    k = b.shape[1] if b_layout == _lib.B_NK else b.shape[0]
+    if a.shape[-1] != k:
+        what = "w.size(1)" if b_layout == _lib.B_NK else "b.size(0)"
+        return f"a.size(-1) ({a.shape[-1]}) must equal {what} ({k})"
+    if k == 0:
+        return "K must be positive"
+    if not a.is_contiguous():
+        return "a must be contiguous"
+    if not b.is_contiguous():
+        return "w must be contiguous"
+    return None
+
+
+def _launch(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype], b_layout: int,
+            kernel: Optional[int] = None) -> torch.Tensor:
+    reason = contract_reason(a, b, out_dtype, b_layout)
+    if reason is not None:
+        raise RuntimeError(f"nanovllm::gemm: {reason}")
+    out_dtype = a.dtype if out_dtype is None else out_dtype
+    k = a.shape[-1]
+    n = b.shape[0] if b_layout == _lib.B_NK else b.shape[1]
+    m = a.numel() // k
+    out = torch.empty((*a.shape[:-1], n), dtype=out_dtype, device=a.device)
+    if m == 0 or n == 0:
+        return out
+    with torch.cuda.device(a.device):
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+        ldb = k if b_layout == _lib.B_NK else n
+        _lib.gemm_raw(a.data_ptr(), b.data_ptr(), out.data_ptr(), m, n, k, k, ldb, n, b_layout,
+                      _CODE[a.dtype], _CODE[out_dtype], stream, kernel)
+    return out
+
+
+@torch.library.custom_op("nanovllm::gemm", mutates_args=())
+def _gemm_op(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    return _launch(a, w, out_dtype, _lib.B_NK)
+
+
+@_gemm_op.register_fake
+def _gemm_fake(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    torch._check(w.dim() == 2)
+    torch._check(a.shape[-1] == w.shape[1])
+    torch._check(a.dtype == w.dtype)
+    torch._check(a.device == w.device)
+    return a.new_empty((*a.shape[:-1], w.shape[0]), dtype=a.dtype if out_dtype is None else out_dtype)
+
+
+@torch.library.custom_op("nanovllm::gemm_kn", mutates_args=())
+def _gemm_kn_op(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    return _launch(a, b, out_dtype, _lib.B_KN)
+
+
+@_gemm_kn_op.register_fake
+def _gemm_kn_fake(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    torch._check(b.dim() == 2)
+    torch._check(a.shape[-1] == b.shape[0])
+    torch._check(a.dtype == b.dtype)
+    torch._check(a.device == b.device)
+    return a.new_empty((*a.shape[:-1], b.shape[1]), dtype=a.dtype if out_dtype is None else out_dtype)
+
+
+def gemm(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """a @ w.T on the MI355X kernels (w in nn.Linear [N, K] layout)."""
+    return torch.ops.nanovllm.gemm(a, w, out_dtype)
+
+
+def gemm_kn(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """a @ b on the MI355X kernels (b row-major [K, N])."""
+    return torch.ops.nanovllm.gemm_kn(a, b, out_dtype)
+
+
+def gemm_with_kernel(a: torch.Tensor, b: torch.Tensor, kernel: int, out_dtype: Optional[torch.dtype] = None,
+                     b_layout: int = _lib.B_NK) -> torch.Tensor:
+    """Run one named kernel of the ladder (raises if it cannot take the shape)."""
+    return _launch(a, b, out_dtype, b_layout, kernel)
+
+
+def selected_kernel(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None,
+                    b_layout: int = _lib.B_NK) -> str:
+    """Name of the kernel the selection table picks for these operands."""
+    k = a.shape[-1]
+    n = w.shape[0] if b_layout == _lib.B_NK else w.shape[1]
+    m = a.numel() // max(k, 1)
+    out_dtype = a.dtype if out_dtype is None else out_dtype
+    aligned = a.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0
+    ldb = k if b_layout == _lib.B_NK else n
+    kid = _lib.select(m, n, k, k, ldb, n, b_layout, _CODE[a.dtype], _CODE[out_dtype], aligned)
+    if kid < 0:
+        raise RuntimeError(f"nanovllm::gemm: {_lib.last_error()}")
+    return _lib.kernel_name(kid)
+
+
+def validate_gemm_backend(backend: str) -> str:
+    """Normalise a backend name (pattern of validate_gdn_decode_backend, gdn.py:13)."""
+    value = str(backend).strip().lower()
+    if value not in BACKENDS:
+        raise ValueError(f"GEMM backend must be one of {BACKENDS}, got {backend!r}")
+    return value
+
+
+def default_backend() -> str:
+    return validate_gemm_backend(os.environ.get(BACKEND_ENV, "torch"))
+
+
+def _torch_linear(x, weight, bias, out_dtype):
+    y = F.linear(x, weight, bias)
+    return y if out_dtype is None or y.dtype == out_dtype else y.to(out_dtype)
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
+           out_dtype: Optional[torch.dtype] = None, backend: Optional[str] = None) -> torch.Tensor:
+    """Drop-in for ``F.linear(x, weight, bias)`` with a backend switch.
+
+    ``torch``: F.linear.  ``hip``: the nanovllm::gemm op; inputs outside its
+    contract raise.  ``auto``: the op when the inputs satisfy its contract,
+    F.linear otherwise (e.g. CPU tensors).  The bias is added after the GEMM.
+    """
+    backend = validate_gemm_backend(backend) if backend is not None else default_backend()
+    if backend == "torch":
+        return _torch_linear(x, weight, bias, out_dtype)
+    reason = contract_reason(x, weight, out_dtype)
+    if reason is not None:
+        if backend == "auto":
+            return _torch_linear(x, weight, bias, out_dtype)
+        raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
+    y = gemm(x, weight, out_dtype)
+    if bias is not None:
+        y = y + bias.to(y.dtype)
+    return y

@@ -1,0 +1,313 @@
+"""CPU oracle for the shape-aware GEMM path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
+torch op, the selection table) imports or calls this module; only tests/,
+``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may use it,
+and only as the checker.
+
+It restates, in numpy, what the reference computes on the CPU for this
+path (paths relative to the reference repo):
+
+  * known-answer input generators
+      gemm_bench.cu:296-305   a[i]=((17i+3)%31-15)/32, b[i]=((11i+5)%29-14)/32, B[K,N]
+      gemm_wmma.cu:300-311    a[r][k]=((17r+13k)%31-15)/32, w[c][k]=((11c+7k)%29-14)/32, W[N,K]
+      gemm_tiled.cu:243-248   a[i]=(i%19-9)*0.1f, b[i]=(i%13-6)*0.1f (also gemm.cu:21-22)
+  * the double-accumulated reference GEMM (gemm.cu:23-29, gemm_tiled.cu:251-260,
+    gemm_wmma.cu:315-327), here in float64 with one final rounding to the
+    output type;
+  * round-to-nearest-even to bf16 / fp16 (TypeTraits::convert,
+    gemm_bench.cu:59-78, which calls __float2bfloat16 / __float2half);
+  * the differential checks: compare (gemm_bench.cu:225-250),
+    compare_result (gemm_wmma.cu:209-247), check_result (common.cuh:18-31);
+  * the dispatch policy supports_wmma / choose_path (gemm_bench.cu:252-273),
+    the shape table kDefaultShapes (gemm_bench.cu:45-57) and the repeat
+    rule (gemm_bench.cu:371-379).
+
+Pinning (what fixes each function independently of this file): the KAT
+results are checked against exact integer arithmetic and against the
+reference's recorded zero error on every KAT row
+(results/rtx3060_gemm_matrix.csv:4-23); the float64 GEMM against
+torch.matmul in float64; the bf16/fp16 rounding against torch's and numpy's
+conversions and against hand-picked ties; the ULP metric against
+np.nextafter.  See tests/test_oracle.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# Known-answer generators
+# ---------------------------------------------------------------------------
+
+def kat_bench_a_int(m: int, k: int) -> np.ndarray:
+    """Numerators (units of 1/32) of A[M,K] from gemm_bench.cu:296-300."""
+    i = np.arange(m * k, dtype=np.int64)
+    return ((i * 17 + 3) % 31 - 15).reshape(m, k)
+
+
+def kat_bench_b_int(k: int, n: int) -> np.ndarray:
+    """Numerators of B[K,N] (row-major, flat index i) from gemm_bench.cu:301-305."""
+    i = np.arange(k * n, dtype=np.int64)
+    return ((i * 11 + 5) % 29 - 14).reshape(k, n)
+
+
+def kat_wmma_a_int(m: int, k: int) -> np.ndarray:
+    """Numerators of A[M,K] from gemm_wmma.cu:300-305."""
+    r = np.arange(m, dtype=np.int64)[:, None]
+    kk = np.arange(k, dtype=np.int64)[None, :]
+    return (r * 17 + kk * 13) % 31 - 15
+
+
+def kat_wmma_w_int(n: int, k: int) -> np.ndarray:
+    """Numerators of W[N,K] (B col-major) from gemm_wmma.cu:306-311."""
+    c = np.arange(n, dtype=np.int64)[:, None]
+    kk = np.arange(k, dtype=np.int64)[None, :]
+    return (c * 11 + kk * 7) % 29 - 14
+
+
+def kat_value(numerators: np.ndarray) -> np.ndarray:
+    """numerator * 0.03125 as float32 (exact: |value| <= 15/32)."""
+    return numerators.astype(np.float32) * np.float32(0.03125)
+
+
+def kat_tiled_a(m: int, k: int) -> np.ndarray:
+    """A[M,K] fp32 from gemm_tiled.cu:243-245 / gemm.cu:21: (i%19-9)*0.1f."""
+    i = np.arange(m * k, dtype=np.int64)
+    return ((i % 19 - 9).astype(np.float32) * np.float32(0.1)).reshape(m, k)
+
+
+def kat_tiled_b(k: int, n: int) -> np.ndarray:
+    """B[K,N] fp32 from gemm_tiled.cu:246-248 / gemm.cu:22: (i%13-6)*0.1f."""
+    i = np.arange(k * n, dtype=np.int64)
+    return ((i % 13 - 6).astype(np.float32) * np.float32(0.1)).reshape(k, n)
+
+
+# ---------------------------------------------------------------------------
+# bf16 / fp16 encodings (bf16 is carried as uint16 bit patterns)
+# ---------------------------------------------------------------------------
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even; NaN -> quiet NaN."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    quiet = ((u >> 16) | 0x40) & 0xFFFF
+    return np.where(nan, quiet, rounded).astype(np.uint16)
+
+
+def f64_to_f32_round_odd(x: np.ndarray) -> np.ndarray:
+    """float64 -> float32 rounded to odd (truncate, then set the last bit if
+    inexact).  A second rounding of this value to any format with at least
+    2 fewer significand bits equals one correct rounding of x."""
+    x = np.asarray(x, dtype=np.float64)
+    f = x.astype(np.float32)
+    back = f.astype(np.float64)
+    inexact = back != x
+    bits = f.view(np.uint32).copy()
+    over = inexact & (np.abs(back) > np.abs(x))
+    bits[over] -= 1
+    bits[inexact] |= 1
+    return bits.view(np.float32)
+
+
+def round_f64(x: np.ndarray, out: str) -> np.ndarray:
+    """One correct round-to-nearest-even of float64 values to `out`.
+
+    Returns float32 / float16 arrays, or uint16 bf16 bit patterns."""
+    x = np.asarray(x, dtype=np.float64)
+    if out == "f32":
+        return x.astype(np.float32)
+    if out == "f16":
+        return f64_to_f32_round_odd(x).astype(np.float16)
+    if out == "bf16":
+        return f32_to_bf16_bits(f64_to_f32_round_odd(x))
+    raise ValueError(out)
+
+
+def to_f64(values: np.ndarray, dtype: str) -> np.ndarray:
+    """Decode an array of `dtype` ("f32", "f16", or "bf16" bits) to float64."""
+    if dtype == "bf16":
+        return bf16_bits_to_f32(values).astype(np.float64)
+    return np.asarray(values).astype(np.float64)
+
+
+def encode(x_f32: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 -> storage of `dtype` with round-to-nearest-even."""
+    if dtype == "f32":
+        return np.asarray(x_f32, dtype=np.float32)
+    if dtype == "f16":
+        return np.asarray(x_f32, dtype=np.float32).astype(np.float16)
+    if dtype == "bf16":
+        return f32_to_bf16_bits(x_f32)
+    raise ValueError(dtype)
+
+
+# ---------------------------------------------------------------------------
+# Reference GEMM
+# ---------------------------------------------------------------------------
+
+def gemm_f64(a64: np.ndarray, b64: np.ndarray, b_layout: str = "nk") -> np.ndarray:
+    """C = A * B in float64 (gemm.cu:23-29): B is W[N,K] for "nk", B[K,N] for "kn"."""
+    a64 = np.asarray(a64, dtype=np.float64)
+    b64 = np.asarray(b64, dtype=np.float64)
+    if b_layout == "nk":
+        return a64 @ b64.T
+    if b_layout == "kn":
+        return a64 @ b64
+    raise ValueError(b_layout)
+
+
+def abs_products_f64(a64: np.ndarray, b64: np.ndarray, b_layout: str = "nk") -> np.ndarray:
+    """S[m,n] = sum_k |A[m,k] B(k,n)|, the scale of fp32 accumulation error."""
+    return gemm_f64(np.abs(a64), np.abs(b64), b_layout)
+
+
+def exact_kat_int(a_int: np.ndarray, b_int: np.ndarray, b_layout: str = "nk") -> np.ndarray:
+    """Exact integer numerators (units of 1/1024) of a KAT product."""
+    a_int = np.asarray(a_int, dtype=np.int64)
+    b_int = np.asarray(b_int, dtype=np.int64)
+    return a_int @ (b_int.T if b_layout == "nk" else b_int)
+
+
+# ---------------------------------------------------------------------------
+# Error metrics
+# ---------------------------------------------------------------------------
+_FMT = {"f32": (32, 23, 127), "f16": (16, 10, 15), "bf16": (16, 7, 127)}
+
+
+def ulp_at(r64: np.ndarray, dtype: str) -> np.ndarray:
+    """Spacing of `dtype` at |r| (the subnormal spacing below the smallest normal)."""
+    _, mant, bias = _FMT[dtype]
+    r = np.abs(np.asarray(r64, dtype=np.float64))
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(r > 0, r, 1.0)))
+    e = np.maximum(np.where(r > 0, e, 1 - bias), 1 - bias)
+    return np.ldexp(1.0, (e - mant).astype(np.int64))
+
+
+def _ordered(bits: np.ndarray, nbits: int) -> np.ndarray:
+    b = np.asarray(bits).astype(np.int64)
+    sign = (b >> (nbits - 1)) & 1
+    mag = b & ((1 << (nbits - 1)) - 1)
+    return np.where(sign == 1, -mag, mag)
+
+
+def ulp_distance(x: np.ndarray, y: np.ndarray, dtype: str) -> np.ndarray:
+    """Number of representable `dtype` values between x and y (same encoding
+    as `encode`/`round_f64` output).  +0 and -0 are the same point."""
+    if dtype == "f32":
+        xb = np.asarray(x, dtype=np.float32).view(np.uint32)
+        yb = np.asarray(y, dtype=np.float32).view(np.uint32)
+        return np.abs(_ordered(xb, 32) - _ordered(yb, 32))
+    if dtype == "f16":
+        xb = np.asarray(x, dtype=np.float16).view(np.uint16)
+        yb = np.asarray(y, dtype=np.float16).view(np.uint16)
+    else:
+        xb = np.asarray(x, dtype=np.uint16)
+        yb = np.asarray(y, dtype=np.uint16)
+    return np.abs(_ordered(xb, 16) - _ordered(yb, 16))
+
+
+def fp32_accumulation_bound(s64: np.ndarray, k: int) -> np.ndarray:
+    """First-order bound K * 2^-24 * sum|a b| on the error of summing K
+    exact fp32 products in any order (Higham, gamma_K)."""
+    return k * 2.0 ** -24 * np.asarray(s64, dtype=np.float64)
+
+
+def gemm_tolerance(r64: np.ndarray, s64: np.ndarray, k: int, dtype: str, ulps: float = 2.0) -> np.ndarray:
+    """Per-element bound used by the parity tests for narrow and fp32 outputs:
+    `ulps` units in the last place of the output type at the exact value,
+    plus the fp32 accumulation bound.  Any kernel that accumulates in fp32
+    and rounds once to the output type meets it; a dropped or repeated
+    K-chunk, a transposed operand or a wrong row exceeds it."""
+    return ulps * ulp_at(r64, dtype) + fp32_accumulation_bound(s64, k)
+
+
+def rel_frobenius(x: np.ndarray, ref: np.ndarray) -> float:
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.linalg.norm(x - ref) / np.linalg.norm(ref))
+
+
+def compare_bench(actual: np.ndarray, reference: np.ndarray) -> dict:
+    """gemm_bench.cu:225-250: max/mean abs error; FAIL if non-finite or
+    |e| > 5e-2 + 1e-2 |ref|."""
+    a = np.asarray(actual, dtype=np.float64)
+    r = np.asarray(reference, dtype=np.float64)
+    err = np.abs(a - r)
+    bad = ~np.isfinite(a) | (err > 5.0e-2 + 1.0e-2 * np.abs(r))
+    return {"max_absolute": float(np.nanmax(err)) if err.size else 0.0,
+            "mean_absolute": float(np.nanmean(err)) if err.size else 0.0,
+            "correct": not bool(bad.any())}
+
+
+def compare_result(actual: np.ndarray, reference: np.ndarray, atol: float, rtol: float) -> dict:
+    """gemm_wmma.cu:217-247: non-finite count, max/mean abs, rmse over the
+    finite elements; FAIL on any non-finite or |e| > atol + rtol |ref|."""
+    a = np.asarray(actual, dtype=np.float64)
+    r = np.asarray(reference, dtype=np.float64)
+    finite = np.isfinite(a)
+    err = np.abs(a[finite] - r[finite])
+    n = a.size
+    return {
+        "max_absolute": float(err.max()) if err.size else 0.0,
+        "mean_absolute": float(err.sum() / n) if n else 0.0,
+        "rmse": float(np.sqrt((err ** 2).sum() / n)) if n else 0.0,
+        "non_finite": int((~finite).sum()),
+        "correct": bool(finite.all()) and not bool((err > atol + rtol * np.abs(r[finite])).any()),
+    }
+
+
+def check_result(result: np.ndarray, reference: np.ndarray) -> dict:
+    """common.cuh:18-31: FAIL if non-finite or |e| > 1e-4 + 1e-4 |ref|."""
+    x = np.asarray(result, dtype=np.float32)
+    r = np.asarray(reference, dtype=np.float32)
+    err = np.abs(x - r)
+    ok = np.isfinite(x).all() and not (err > np.float32(1e-4) + np.float32(1e-4) * np.abs(r)).any()
+    return {"max_absolute": float(err.max()) if err.size else 0.0, "correct": bool(ok)}
+
+
+# ---------------------------------------------------------------------------
+# Reference dispatch policy and bench constants
+# ---------------------------------------------------------------------------
+WMMA_M = WMMA_N = WMMA_K = 16
+
+# gemm_bench.cu:45-57 (label, M, N, K)
+DEFAULT_SHAPES = [
+    ("qwen35_decode_qkv", 1, 6144, 1024),
+    ("qwen35_prefill16_qkv", 16, 6144, 1024),
+    ("qwen35_prefill64_qkv", 64, 6144, 1024),
+    ("qwen35_prefill256_qkv", 256, 6144, 1024),
+    ("qwen35_prefill16_out", 16, 1024, 2048),
+    ("qwen35_prefill64_out", 64, 1024, 2048),
+    ("qwen35_prefill16_gate_up", 16, 7168, 1024),
+    ("qwen35_prefill64_gate_up", 64, 7168, 1024),
+    ("qwen35_prefill64_down", 64, 1024, 3584),
+    ("square256", 256, 256, 256),
+    ("square512", 512, 512, 512),
+]
+
+
+def supports_wmma(m: int, n: int, k: int) -> bool:
+    """gemm_bench.cu:252-256."""
+    return m % WMMA_M == 0 and n % WMMA_N == 0 and k % WMMA_K == 0
+
+
+def choose_path_reference(m: int, n: int, k: int, dtype: str) -> str:
+    """gemm_bench.cu:260-273: the reference's RTX 3060 dispatch policy."""
+    if not supports_wmma(m, n, k):
+        return "cublas"
+    if dtype == "bf16" and m == 16 and k == 1024 and n >= 4096:
+        return "wmma_direct"
+    return "cublas"
+
+
+def repeats_for(flops: float, repeat_override: int = -1) -> int:
+    """gemm_bench.cu:371-377: clamp(2e10 / flops, 10, 200)."""
+    if repeat_override > 0:
+        return repeat_override
+    return int(min(max(int(2.0e10 / max(flops, 1.0)), 10), 200))

@@ -1,0 +1,151 @@
+"""CPU tests of the C ABI: the library loads, exports every symbol the header
+declares, validates arguments before touching the GPU, and its shape-selection
+table maps every valid problem to a kernel of its own (the replacement for
+supports_wmma / choose_path, cuda_kernels/gemm/src/gemm_bench.cu:252-273).
+No test here launches a kernel."""
+from __future__ import annotations
+
+import itertools
+import re
+from pathlib import Path
+
+import pytest
+
+from conftest import PKG, ROOT
+
+L = PKG._lib
+F32, F16, BF16 = L.F32, L.F16, L.BF16
+NK, KN = L.B_NK, L.B_KN
+
+
+def _declared_functions():
+    names = []
+    for header in sorted((ROOT / "include").glob("*.h")):
+        text = header.read_text()
+        names += re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(nanovllm_\w+)\s*\(", text, flags=re.M)
+    return names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared_functions()
+    assert len(names) >= 7
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(L.SIGNATURES), "ctypes signatures must cover exactly the header"
+
+
+def test_version_and_names(lib):
+    assert lib.nanovllm_gemm_version() >> 16 == 1
+    expected = ["fp32_naive", "fp32_tiled", "mfma_direct", "mfma_staged", "splitk_decode"]
+    assert [L.kernel_name(i) for i in range(L.KERNEL_COUNT)] == expected
+    assert L.kernel_name(99) == "unknown" and L.kernel_name(-1) == "unknown"
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    (dict(m=4, n=4, k=0), L.EINVAL, "k must be positive"),
+    (dict(m=-1, n=4, k=4), L.EINVAL, "non-negative"),
+    (dict(m=4, n=4, k=8, lda=7), L.EINVAL, "lda"),
+    (dict(m=4, n=4, k=8, ldb=7), L.EINVAL, "ldb"),
+    (dict(m=4, n=9, k=8, ldb=8, layout=KN), L.EINVAL, "ldb"),
+    (dict(m=4, n=9, k=8, ldc=8), L.EINVAL, "ldc"),
+    (dict(m=4, n=4, k=8, layout=2), L.EINVAL, "b_layout"),
+    (dict(m=4, n=4, k=8, din=F32, dout=BF16), L.EUNSUPPORTED, "dtype pair"),
+    (dict(m=4, n=4, k=8, din=BF16, dout=F16), L.EUNSUPPORTED, "dtype pair"),
+    (dict(m=4, n=4, k=8, din=7, dout=F32), L.EINVAL, "dtype code"),
+])
+def test_select_rejects_invalid_problems(args, code, msg):
+    m, n, k = args["m"], args["n"], args["k"]
+    layout = args.get("layout", NK)
+    lda = args.get("lda", k)
+    ldb = args.get("ldb", k if layout == NK else n)
+    ldc = args.get("ldc", n)
+    rc = L.select(m, n, k, lda, ldb, ldc, layout, args.get("din", BF16), args.get("dout", BF16))
+    assert rc == code
+    assert msg in L.last_error()
+
+
+def test_gemm_validates_before_launch(lib):
+    # Invalid sizes and null pointers are rejected on the host: no GPU needed.
+    rc = lib.nanovllm_gemm(None, None, None, 4, 4, 0, 4, 4, 4, NK, BF16, BF16, None)
+    assert rc == L.EINVAL and "k must be positive" in L.last_error()
+    rc = lib.nanovllm_gemm(None, None, None, 4, 4, 8, 8, 8, 4, NK, BF16, BF16, None)
+    assert rc == L.EINVAL and "non-null" in L.last_error()
+    # Empty output: a valid no-op that never dereferences the pointers.
+    assert lib.nanovllm_gemm(None, None, None, 0, 4, 8, 8, 8, 4, NK, BF16, BF16, None) == L.OK
+    assert lib.nanovllm_gemm(None, None, None, 4, 0, 8, 8, 8, 1, NK, BF16, BF16, None) == L.OK
+    assert L.last_error() == ""
+    rc = lib.nanovllm_gemm_with_kernel(-3, None, None, None, 4, 4, 8, 8, 8, 4, NK, BF16, BF16, None)
+    assert rc == L.EINVAL and "kernel id" in L.last_error()
+    rc = lib.nanovllm_gemm_with_kernel(17, None, None, None, 4, 4, 8, 8, 8, 4, NK, BF16, BF16, None)
+    assert rc == L.EINVAL
+
+
+def test_gemm_with_kernel_refuses_unsupported_rung(lib):
+    # fp32_tiled cannot take bf16; splitk_decode cannot take M = 64; the check
+    # happens before any launch (pointers are dummies never dereferenced).
+    dummy = 1 << 20
+    rc = lib.nanovllm_gemm_with_kernel(L.KERNEL_FP32_TILED, dummy, dummy, dummy, 4, 4, 8, 8, 8, 4, NK, BF16, BF16,
+                                       None)
+    assert rc == L.EUNSUPPORTED and "fp32_tiled" in L.last_error()
+    rc = lib.nanovllm_gemm_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, 64, 64, 64, 64, 64, 64, NK,
+                                       BF16, BF16, None)
+    assert rc == L.EUNSUPPORTED
+
+
+def _expected(m, k, lda, ldb, layout, din, aligned):
+    if din == F32:
+        return L.KERNEL_FP32_TILED
+    vec = aligned and k % 8 == 0 and lda % 8 == 0 and ldb % 8 == 0 and layout == NK
+    if vec:
+        return L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
+    return L.KERNEL_MFMA_DIRECT
+
+
+PAIRS = [(F32, F32), (F16, F16), (F16, F32), (BF16, BF16), (BF16, F32)]
+
+
+@pytest.mark.parametrize("din,dout", PAIRS)
+def test_selection_table_total_and_self_consistent(din, dout):
+    """Every valid problem maps to one of this library's kernels, that kernel
+    supports it, and the table follows its stated rule."""
+    ms = [0, 1, 4, 16, 31, 32, 33, 64, 127, 2048]
+    ns = [1, 15, 193, 4096, 151936]
+    ks = [1, 7, 8, 65, 1024, 3584]
+    for m, n, k, layout, aligned, pad in itertools.product(ms, ns, ks, (NK, KN), (0, 1), (0, 3)):
+        lda = k + pad
+        ldb = (k if layout == NK else n) + pad
+        kid = L.select(m, n, k, lda, ldb, n, layout, din, dout, aligned)
+        assert 0 <= kid < L.KERNEL_COUNT
+        assert kid == _expected(m, k, lda, ldb, layout, din, aligned), (m, n, k, layout, aligned, pad)
+        assert L.kernel_supports(kid, m, n, k, lda, ldb, n, layout, din, dout, aligned)
+
+
+def test_selection_on_workloads_and_qwen_shapes():
+    W = PKG.workloads
+    code = {"torch.float32": F32, "torch.float16": F16, "torch.bfloat16": BF16}
+    want = {
+        "fp32_square_1024": {1024: "fp32_tiled"},
+        "bf16_prefill_2048x4096x1024": {2048: "mfma_staged"},
+        "bf16_decode_n6144_k1024": {m: "splitk_decode" for m in (1, 4, 8, 16, 32)},
+        "fp16_down_4096x1024x3584": {4096: "mfma_staged"},
+        "bf16_lm_head_n151936_k1024": {1: "splitk_decode", 32: "splitk_decode", 512: "mfma_staged"},
+    }
+    for name, wl in W.WORKLOADS.items():
+        for m in wl.ms:
+            ldb = wl.k if wl.b_layout == NK else wl.n
+            kid = L.select(m, wl.n, wl.k, wl.k, ldb, wl.n, wl.b_layout, code[str(wl.dtype_in)],
+                           code[str(wl.dtype_out)], 1)
+            assert L.kernel_name(kid) == want[name][m], (name, m)
+    for label, m, n, k in W.QWEN35_SHAPES:
+        kid = L.select(m, n, k, k, k, n, NK, BF16, BF16, 1)
+        assert L.kernel_name(kid) == ("splitk_decode" if m <= 32 else "mfma_staged"), label
+        # the reference's B[K,N] layout of the same shapes runs on the direct rung
+        kid = L.select(m, n, k, k, n, n, KN, BF16, F32, 1)
+        assert L.kernel_name(kid) == "mfma_direct", label
+
+
+def test_no_vendor_kernel_id():
+    # The reference falls back to cuBLAS outside a narrow regime
+    # (gemm_bench.cu:260-273); here every id is one of the ladder's kernels.
+    names = {L.kernel_name(i) for i in range(L.KERNEL_COUNT)}
+    assert not any("blas" in nm for nm in names)

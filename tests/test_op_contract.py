@@ -1,0 +1,71 @@
+"""CPU tests of the torch op boundary: registration, fake (meta) shapes, the
+argument contract and the torch | hip | auto backend switch (patterns of the
+reference's tests/kernels/test_custom_add.py:36-46 and
+tests/kernels/test_gdn_decode_dispatch.py:48-64)."""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import importlib
+
+from conftest import PKG  # noqa: F401  (registers the package)
+
+G = importlib.import_module("inference_systems_amd.kernels.gemm")
+
+
+def test_ops_registered():
+    assert hasattr(torch.ops.nanovllm, "gemm")
+    assert hasattr(torch.ops.nanovllm, "gemm_kn")
+    schema = str(torch.ops.nanovllm.gemm.default._schema)
+    assert "Tensor a" in schema and "Tensor w" in schema and "ScalarType? out_dtype=None" in schema
+
+
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+def test_fake_impl_shapes_on_meta(out_dtype):
+    a = torch.empty((3, 5, 64), dtype=torch.bfloat16, device="meta")
+    w = torch.empty((96, 64), dtype=torch.bfloat16, device="meta")
+    out = torch.ops.nanovllm.gemm(a, w, out_dtype)
+    assert out.shape == (3, 5, 96)
+    assert out.dtype == (torch.bfloat16 if out_dtype is None else out_dtype)
+    b = torch.empty((64, 40), dtype=torch.float32, device="meta")
+    out = torch.ops.nanovllm.gemm_kn(torch.empty((7, 64), device="meta"), b)
+    assert out.shape == (7, 40) and out.dtype == torch.float32
+
+
+def test_op_rejects_cpu_tensors():
+    a = torch.randn(4, 8, dtype=torch.bfloat16)
+    w = torch.randn(6, 8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="must be CUDA"):
+        torch.ops.nanovllm.gemm(a, w)
+
+
+def test_contract_reason_cpu():
+    a = torch.randn(4, 8)
+    assert G.contract_reason(a, torch.randn(6, 8)) == "a and w must be CUDA (HIP) tensors"
+
+
+def test_backend_validation(monkeypatch):
+    assert G.validate_gemm_backend(" HIP ") == "hip"
+    with pytest.raises(ValueError, match="GEMM backend must be one of"):
+        G.validate_gemm_backend("cublas")
+    monkeypatch.setenv(G.BACKEND_ENV, "auto")
+    assert G.default_backend() == "auto"
+    monkeypatch.delenv(G.BACKEND_ENV)
+    assert G.default_backend() == "torch"
+
+
+def test_linear_backends_on_cpu_tensors():
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 16, generator=gen)
+    w = torch.randn(8, 16, generator=gen)
+    b = torch.randn(8, generator=gen)
+    ref = F.linear(x, w, b)
+    assert torch.equal(G.linear(x, w, b, backend="torch"), ref)
+    # auto: CPU tensors are outside the HIP op's contract -> F.linear
+    assert torch.equal(G.linear(x, w, b, backend="auto"), ref)
+    with pytest.raises(RuntimeError, match="HIP GEMM backend is unavailable: a and w must be CUDA"):
+        G.linear(x, w, b, backend="hip")
+    out = G.linear(x.bfloat16(), w.bfloat16(), None, out_dtype=torch.float32, backend="torch")
+    assert out.dtype == torch.float32

@@ -1,0 +1,299 @@
+"""Pins the CPU oracle (oracle/gemm_oracle.py) before it is trusted.
+
+Each check fixes an oracle function by something other than the oracle's
+own formula: exact integer arithmetic, values the reference recorded
+(cuda_kernels/gemm/results/rtx3060_gemm_matrix.csv), torch / numpy library
+routines, hand-worked ties, brute force over representable values, and
+planted mistakes that must be caught.
+"""
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm_oracle as orc
+
+# ---------------------------------------------------------------------------
+# Known-answer inputs
+# ---------------------------------------------------------------------------
+
+
+def test_kat_bench_first_values_by_hand():
+    # gemm_bench.cu:296-305: a[0] = (3 % 31 - 15)/32 = -12/32; a[1] = (20-15)/32;
+    # b[0] = (5 % 29 - 14)/32 = -9/32; b[1] = (16 - 14)/32.
+    a = orc.kat_bench_a_int(2, 3)
+    b = orc.kat_bench_b_int(3, 2)
+    assert a.ravel().tolist()[:2] == [-12, 5]
+    assert b.ravel().tolist()[:2] == [-9, 2]
+    assert orc.kat_value(a)[0, 0] == np.float32(-12 / 32)
+
+
+def test_kat_wmma_first_values_by_hand():
+    # gemm_wmma.cu:300-311: a[r][k] = ((17r + 13k) % 31 - 15)/32, w[c][k] = ((11c + 7k) % 29 - 14)/32
+    a = orc.kat_wmma_a_int(2, 2)
+    w = orc.kat_wmma_w_int(2, 2)
+    assert a.tolist() == [[-15, -2], [2, 15]]
+    assert w.tolist() == [[-14, -7], [-3, 4]]
+
+
+@pytest.mark.parametrize("gen", ["bench_a", "bench_b", "wmma_a", "wmma_w"])
+def test_kat_values_exact_in_half_types(gen):
+    ints = {"bench_a": orc.kat_bench_a_int(7, 64), "bench_b": orc.kat_bench_b_int(64, 7),
+            "wmma_a": orc.kat_wmma_a_int(7, 64), "wmma_w": orc.kat_wmma_w_int(7, 64)}[gen]
+    v = orc.kat_value(ints)
+    assert np.all(np.abs(ints) <= 15)
+    assert np.array_equal(orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(v)), v)
+    assert np.array_equal(v.astype(np.float16).astype(np.float32), v)
+
+
+# Shapes whose reference rows recorded direct/staged max-abs 0 against cuBLAS
+# (rtx3060_gemm_matrix.csv:4-23, all WMMA-capable rows of gemm_bench.cu:45-57).
+KAT_SHAPES = [s for s in orc.DEFAULT_SHAPES if orc.supports_wmma(*s[1:])]
+
+
+@pytest.mark.parametrize("label,m,n,k", [s for s in KAT_SHAPES if s[1] * s[2] * s[3] <= 64 * 7168 * 1024])
+def test_kat_bench_fp32_sum_is_exact(label, m, n, k):
+    """The fp32-accumulated product of the KAT inputs is exact in any order,
+    so the expected output is the exact value (what cuBLAS returned, with
+    zero error, in every reference row)."""
+    a_int = orc.kat_bench_a_int(m, k)
+    b_int = orc.kat_bench_b_int(k, n)
+    exact = orc.exact_kat_int(a_int, b_int, "kn")
+    assert np.abs(exact).max() < 2 ** 24  # every partial sum fits fp32 exactly
+    f32 = orc.kat_value(a_int) @ orc.kat_value(b_int)  # float32 BLAS, its own order
+    assert np.array_equal(f32.astype(np.float64) * 1024.0, exact.astype(np.float64))
+    f64 = orc.gemm_f64(orc.kat_value(a_int), orc.kat_value(b_int), "kn")
+    assert np.array_equal(f64 * 1024.0, exact.astype(np.float64))
+
+
+def test_kat_wmma_256_cube_exact():
+    """gemm_wmma.cu:279-327: 256^3 FP16 case, W[N,K]."""
+    a_int = orc.kat_wmma_a_int(256, 256)
+    w_int = orc.kat_wmma_w_int(256, 256)
+    exact = orc.exact_kat_int(a_int, w_int, "nk")
+    f64 = orc.gemm_f64(orc.kat_value(a_int), orc.kat_value(w_int), "nk")
+    assert np.array_equal(f64 * 1024.0, exact.astype(np.float64))
+    # a few entries by the definition
+    for r, c in [(0, 0), (3, 200), (255, 255)]:
+        assert exact[r, c] == sum(int(a_int[r, i]) * int(w_int[c, i]) for i in range(256))
+
+
+def test_kat_tiled_values_match_float32_arithmetic():
+    # gemm_tiled.cu:243-248: (i % 19 - 9) * 0.1f evaluated in float32.
+    a = orc.kat_tiled_a(127, 65)
+    for i in (0, 5, 9, 18, 19, 1000):
+        assert a.ravel()[i] == np.float32(np.float32(i % 19 - 9) * np.float32(0.1))
+    # The float32 product is not the decimal literal: -9 * 0.1f = -0.90000004.
+    assert a.ravel()[0] == np.float32(-0.90000004) and a.ravel()[0] != np.float32(-0.9)
+
+
+# ---------------------------------------------------------------------------
+# Rounding
+# ---------------------------------------------------------------------------
+
+
+def _bits(x):
+    return int(orc.f32_to_bf16_bits(np.array([x], dtype=np.float32))[0])
+
+
+def test_bf16_rne_hand_worked_cases():
+    assert _bits(1.0) == 0x3F80
+    assert _bits(1.0 + 2.0 ** -8) == 0x3F80          # tie -> even (down)
+    assert _bits(1.0 + 3 * 2.0 ** -8) == 0x3F82      # tie -> even (up)
+    assert _bits(1.0 + 2.0 ** -8 + 2.0 ** -20) == 0x3F81
+    assert _bits(-0.0) == 0x8000
+    assert _bits(float("inf")) == 0x7F80
+    assert _bits(np.finfo(np.float32).max) == 0x7F80  # rounds past the largest bf16
+    nan = _bits(float("nan"))
+    assert (nan & 0x7F80) == 0x7F80 and (nan & 0x7F) != 0
+
+
+def test_bf16_rne_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32),
+        (rng.standard_normal(2000) * 1e-38).astype(np.float32),  # subnormal range
+        np.array([0.0, -0.0, np.inf, -np.inf, 65504.0, 3.0e38], dtype=np.float32),
+    ])
+    mine = orc.f32_to_bf16_bits(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(mine, ref)
+
+
+def _nearest_even(value: Fraction, candidates):
+    """Brute-force correct rounding: nearest candidate, ties to even mantissa."""
+    best = sorted(candidates, key=lambda c: (abs(Fraction(c[0]) - value), c[1] & 1))
+    return best[0][1]
+
+
+def _bf16_neighbours(x: float):
+    f = np.float32(x)
+    b = int(orc.f32_to_bf16_bits(np.array([f]))[0])
+    out = []
+    for bits in (b - 2, b - 1, b, b + 1, b + 2):
+        val = float(orc.bf16_bits_to_f32(np.array([bits], dtype=np.uint16))[0])
+        out.append((val, bits))
+    return out
+
+
+@pytest.mark.parametrize("x", [
+    1.0 + 2.0 ** -8 + 2.0 ** -30,     # double rounding through fp32 would give 1.0
+    1.0 + 2.0 ** -8 - 2.0 ** -30,
+    -(3.0 + 2.0 ** -7 + 2.0 ** -35),
+    0.1, 1.0 / 3.0, 1234.5678, 2.0 ** -130 + 2.0 ** -140,
+])
+def test_round_f64_bf16_single_rounding(x):
+    got = int(orc.round_f64(np.array([x]), "bf16")[0])
+    assert got == _nearest_even(Fraction(x), _bf16_neighbours(x))
+
+
+@pytest.mark.parametrize("x", [1.0 + 2.0 ** -11 + 2.0 ** -40, 1.0 + 2.0 ** -11 - 2.0 ** -40,
+                               0.1, 2.0 ** -24 * 1.5 + 2.0 ** -50, 60000.123])
+def test_round_f64_f16_single_rounding(x):
+    got = orc.round_f64(np.array([x]), "f16")[0]
+    h = np.float16(x)
+    cands = [(float(v), int(np.array([v], dtype=np.float16).view(np.uint16)[0]))
+             for v in (np.nextafter(np.nextafter(h, -np.inf), -np.inf), np.nextafter(h, -np.inf), h,
+                       np.nextafter(h, np.inf), np.nextafter(np.nextafter(h, np.inf), np.inf))]
+    want = _nearest_even(Fraction(x), cands)
+    assert int(np.array([got], dtype=np.float16).view(np.uint16)[0]) == want
+
+
+def test_naive_double_rounding_is_caught():
+    """A planted mistake (RNE to fp32, then RNE to bf16) differs on the
+    double-rounding case, so the single-rounding test above has teeth."""
+    x = 1.0 + 2.0 ** -8 + 2.0 ** -30
+    naive = int(orc.f32_to_bf16_bits(np.array([x], dtype=np.float64).astype(np.float32))[0])
+    assert naive != int(orc.round_f64(np.array([x]), "bf16")[0])
+
+
+# ---------------------------------------------------------------------------
+# ULP metrics
+# ---------------------------------------------------------------------------
+
+
+def test_ulp_distance_float_types():
+    x = np.array([1.0, -2.5, 0.0, 1e-3], dtype=np.float32)
+    nx = np.nextafter(x, np.float32(np.inf))
+    assert orc.ulp_distance(x, nx, "f32").tolist() == [1, 1, 1, 1]
+    assert orc.ulp_distance(np.float32(0.0), np.float32(-0.0), "f32") == 0
+    tiny = np.float32(np.nextafter(np.float32(0), np.float32(1)))
+    assert orc.ulp_distance(-tiny, tiny, "f32") == 2
+    h = np.array([1.0, -3.0], dtype=np.float16)
+    assert orc.ulp_distance(h, np.nextafter(h, np.float16(np.inf)), "f16").tolist() == [1, 1]
+    b = orc.f32_to_bf16_bits(np.array([1.0, -1.0], dtype=np.float32))
+    assert orc.ulp_distance(b, b + 1, "bf16").tolist() == [1, 1]
+
+
+def test_ulp_at_matches_spacing():
+    r = np.array([1.0, 0.75, 3.0, 1e-3, 6.0e4])
+    assert np.array_equal(orc.ulp_at(r, "f32"), np.spacing(r.astype(np.float32)).astype(np.float64))
+    assert np.array_equal(orc.ulp_at(r, "f16"), np.spacing(r.astype(np.float16)).astype(np.float64))
+    assert orc.ulp_at(np.array([1.0]), "bf16")[0] == 2.0 ** -7
+    assert orc.ulp_at(np.array([0.75]), "bf16")[0] == 2.0 ** -8
+    assert orc.ulp_at(np.array([0.0]), "bf16")[0] == 2.0 ** -133
+
+
+# ---------------------------------------------------------------------------
+# Reference GEMM and tolerance
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_gemm_f64_matches_torch(layout):
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((37, 53))
+    b = rng.standard_normal((29, 53)) if layout == "nk" else rng.standard_normal((53, 29))
+    ref = torch.from_numpy(a) @ (torch.from_numpy(b).T if layout == "nk" else torch.from_numpy(b))
+    assert np.allclose(orc.gemm_f64(a, b, layout), ref.numpy(), rtol=1e-13, atol=1e-13)
+
+
+def test_gemm_f64_closed_forms():
+    a = np.arange(12, dtype=np.float64).reshape(3, 4)
+    assert np.array_equal(orc.gemm_f64(a, np.eye(4), "nk"), a)          # identity W
+    ones = np.ones((5, 4))
+    assert np.array_equal(orc.gemm_f64(a, ones, "nk"), np.repeat(a.sum(1, keepdims=True), 5, axis=1))
+    u = np.array([1.0, 2.0, 3.0])
+    v = np.array([4.0, 5.0])
+    assert np.array_equal(orc.gemm_f64(u[:, None], v[:, None], "nk"), np.outer(u, v))  # K = 1
+    kn = np.arange(20, dtype=np.float64).reshape(4, 5)
+    assert np.array_equal(orc.gemm_f64(a, kn, "kn"), orc.gemm_f64(a, kn.T, "nk"))
+
+
+def _fp32_accumulated(a32, w32):
+    """A correct kernel: exact products summed in fp32 (sequential order)."""
+    acc = np.zeros((a32.shape[0], w32.shape[0]), dtype=np.float32)
+    for kk in range(a32.shape[1]):
+        acc += a32[:, kk:kk + 1] * w32[:, kk][None, :]
+    return acc
+
+
+def test_tolerance_accepts_fp32_accumulation_and_catches_planted_mistakes():
+    gen = torch.Generator().manual_seed(3)
+    m, n, k = 16, 48, 1024
+    a = (torch.randn((m, k), generator=gen)).to(torch.bfloat16).float().numpy()
+    w = (torch.randn((n, k), generator=gen) * 0.02).to(torch.bfloat16).float().numpy()
+    a64, w64 = a.astype(np.float64), w.astype(np.float64)
+    r = orc.gemm_f64(a64, w64)
+    tol = orc.gemm_tolerance(r, orc.abs_products_f64(a64, w64), k, "bf16")
+
+    def ok(out_f32):
+        got = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(out_f32)).astype(np.float64)
+        return bool((np.abs(got - r) <= tol).all())
+
+    good = _fp32_accumulated(a, w)
+    assert ok(good)
+    assert ok(np.flip(_fp32_accumulated(a[:, ::-1].copy(), w[:, ::-1].copy()), 0)[::-1])  # other order
+    assert not ok(_fp32_accumulated(a[:, :-8], w[:, :-8]))                  # dropped K chunk
+    assert not ok(_fp32_accumulated(a, np.roll(w, 1, axis=0)))              # wrong W row
+    assert not ok(_fp32_accumulated(a, w[:, ::-1].copy()))                  # reversed K on one operand
+    bad = good.copy()
+    bad[3, 7] = -bad[3, 7] if abs(bad[3, 7]) > 0.05 else bad[3, 7] + 0.1
+    assert not ok(bad)                                                       # one wrong element
+
+
+def test_rel_frobenius_and_checks():
+    ref = np.array([[1.0, 2.0], [3.0, 4.0]])
+    assert orc.rel_frobenius(ref, ref) == 0.0
+    assert math.isclose(orc.rel_frobenius(ref * 1.001, ref), 1e-3, rel_tol=1e-9)
+    assert orc.check_result(ref.astype(np.float32), ref)["correct"]
+    assert not orc.check_result(ref.astype(np.float32) + 1e-3, ref)["correct"]
+    assert not orc.check_result(np.array([np.nan, 1.0]), np.array([1.0, 1.0]))["correct"]
+    cb = orc.compare_bench(np.array([1.0, 2.06]), np.array([1.0, 2.0]))
+    assert cb["correct"] and math.isclose(cb["max_absolute"], 0.06, rel_tol=1e-9)
+    assert not orc.compare_bench(np.array([1.0, 2.1]), np.array([1.0, 2.0]))["correct"]
+    cr = orc.compare_result(np.array([1.0, np.inf, 3.0]), np.array([1.0, 2.0, 3.0]), 1e-2, 1e-2)
+    assert cr["non_finite"] == 1 and not cr["correct"]
+
+
+# ---------------------------------------------------------------------------
+# Reference dispatch policy and repeat rule, against the recorded CSV columns
+# ---------------------------------------------------------------------------
+
+# (dtype, label) -> (repeats, dispatch), rtx3060_gemm_matrix.csv:2-23
+CSV_ROWS = {
+    ("fp16", "qwen35_decode_qkv"): (200, "cublas"), ("bf16", "qwen35_decode_qkv"): (200, "cublas"),
+    ("fp16", "qwen35_prefill16_qkv"): (99, "cublas"), ("bf16", "qwen35_prefill16_qkv"): (99, "wmma_direct"),
+    ("fp16", "qwen35_prefill64_qkv"): (24, "cublas"), ("bf16", "qwen35_prefill64_qkv"): (24, "cublas"),
+    ("fp16", "qwen35_prefill256_qkv"): (10, "cublas"), ("bf16", "qwen35_prefill256_qkv"): (10, "cublas"),
+    ("fp16", "qwen35_prefill16_out"): (200, "cublas"), ("bf16", "qwen35_prefill16_out"): (200, "cublas"),
+    ("fp16", "qwen35_prefill64_out"): (74, "cublas"), ("bf16", "qwen35_prefill64_out"): (74, "cublas"),
+    ("fp16", "qwen35_prefill16_gate_up"): (85, "cublas"),
+    ("bf16", "qwen35_prefill16_gate_up"): (85, "wmma_direct"),
+    ("fp16", "qwen35_prefill64_gate_up"): (21, "cublas"), ("bf16", "qwen35_prefill64_gate_up"): (21, "cublas"),
+    ("fp16", "qwen35_prefill64_down"): (42, "cublas"), ("bf16", "qwen35_prefill64_down"): (42, "cublas"),
+    ("fp16", "square256"): (200, "cublas"), ("bf16", "square256"): (200, "cublas"),
+    ("fp16", "square512"): (74, "cublas"), ("bf16", "square512"): (74, "cublas"),
+}
+
+
+@pytest.mark.parametrize("dtype,label", sorted(CSV_ROWS))
+def test_reference_policy_matches_recorded_rows(dtype, label):
+    m, n, k = {s[0]: s[1:] for s in orc.DEFAULT_SHAPES}[label]
+    repeats, dispatch = CSV_ROWS[(dtype, label)]
+    assert orc.repeats_for(2.0 * m * n * k) == repeats
+    assert orc.choose_path_reference(m, n, k, dtype) == dispatch
