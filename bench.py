@@ -48,7 +48,24 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-vendor", action="store_true", help="skip the torch GPU GEMM comparison")
     p.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                   help="only run 10 device copies of MIB MiB (reference kernel for HBM counter scaling)")
     return p.parse_args()
+
+
+def calibrate_copy(mib: int) -> int:
+    """A plain device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE
+    counters give the scale between the counters and bytes moved."""
+    import torch
+
+    n = mib * 2 ** 20 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_each_way": n * 4, "copies": 10}), flush=True)
+    return 0
 
 
 class GraphTimer:
@@ -108,6 +125,8 @@ def main() -> int:
         print("bench.py measures one GPU only: this GEMM path runs on one MI355X per process and has no "
               "multi-GPU mode (run with --gpus 1).", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2

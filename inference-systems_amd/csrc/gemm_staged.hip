@@ -6,21 +6,24 @@
 // designed for CDNA4 instead of translated:
 //   * BM x BN macro tile per 256-thread workgroup (4 waves in a 2x2 grid),
 //     K-tiles of 64 elements;
+//   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging) into a ring of STAGES tile buffers; tiles t+1 .. t+STAGES-1
+//     are in flight while tile t is multiplied, and each wave waits on its
+//     own vmcnt for exactly the tile it needs before the one barrier per
+//     K-tile;
+//   * LDS rows of 64 elements are 8 chunks of 16 bytes; chunk c of row r
+//     sits at position c ^ ((r >> 1) & 7).  gfx950's LDS serves 16 lanes of
+//     a ds_read_b128 per clock from 64 banks (256 bytes), and with this key
+//     the 16 rows one MFMA fragment read touches per clock land in 16
+//     distinct 16-byte bank groups (rows r and r+8 no longer collide);
 //   * v_mfma_f32_32x32x16_{bf16,f16} with W as the first operand and A as
 //     the second, so each lane ends with 4 consecutive output columns per
 //     accumulator quad and stores them with one 8- or 16-byte write;
-//   * 16-byte coalesced global loads (8 threads cover one 128-byte row
-//     segment), register-staged into a double-buffered LDS tile;
-//   * LDS rows of 64 elements are 8 chunks of 16 bytes; chunk c of row r
-//     sits at position c ^ (r & 7), so both the ds_write_b128 of a row
-//     segment and the ds_read_b128 of an MFMA fragment (8 consecutive rows,
-//     one chunk) touch 8 distinct 16-byte bank groups;
-//   * one barrier per K-tile, the next tile's global loads in flight while
-//     the current one is multiplied;
 //   * XCD-aware tile order so the tiles that share A and W rows run on the
 //     same XCD's L2.
-// Rows past M or N are clamped for loading and masked at the store; the K
-// tail is zero-filled per 8-element chunk (K must be a multiple of 8).
+// Rows past M or N are clamped for loading and masked at the store; K-tail
+// chunks (K must be a multiple of 8) are copied from a zero chunk in device
+// memory, so the LDS tile is zero past K.
 #include "gemm_common.hpp"
 
 namespace nvg {
@@ -29,26 +32,49 @@ namespace {
 constexpr int kBK = 64;        // K elements per tile = 8 chunks of 16 bytes
 constexpr int kChunks = kBK / 8;
 
-template <int DT, int DT_OUT, int BM, int BN>
-__global__ __launch_bounds__(256) void mfma_staged_kernel(
+// Source of the K-tail chunks: 16 zero bytes in global memory.
+__device__ u32x4_t g_zero_chunk = {0u, 0u, 0u, 0u};
+
+__device__ __forceinline__ int lds_swizzle(int row) { return (row >> 1) & 7; }
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their no-wait maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES>
+__global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
     int tiles_m, int tiles_n, int c_vec) {
-    constexpr int WM = BM / 2;           // wave tile rows (M)
-    constexpr int WN = BN / 2;           // wave tile cols (N)
+    constexpr int NW = WGM * WGN;        // waves, in a WGM x WGN grid
+    constexpr int NT = NW * 64;          // threads
+    constexpr int WM = BM / WGM;         // wave tile rows (M)
+    constexpr int WN = BN / WGN;         // wave tile cols (N)
     constexpr int MJ = WM / 32;          // 32-row blocks of A per wave
     constexpr int NI = WN / 32;          // 32-row blocks of W per wave
-    constexpr int A_PER = BM * kChunks / 256;
-    constexpr int B_PER = BN * kChunks / 256;
-    static_assert(A_PER * 256 == BM * kChunks && B_PER * 256 == BN * kChunks, "tile / thread mismatch");
+    constexpr int ROWS = BM + BN;        // LDS rows per stage (A rows, then W rows)
+    constexpr int IPW = ROWS / (8 * NW); // DMA instructions per wave per tile (8 rows each)
+    constexpr int AHEAD = STAGES - 1;    // tiles in flight ahead of the one multiplied
+    static_assert(IPW * 8 * NW == ROWS && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+    static_assert(AHEAD >= 1 && AHEAD <= 3 && AHEAD * IPW < 64, "vmcnt range");
 
-    __shared__ u32x4_t lds[2][(BM + BN) * kChunks];
+    // LDS: the ring of K-tile stages, reused after the K loop for the C tile.
+    constexpr int OB = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;     // output bytes
+    constexpr int PITCH = BN * OB + 16;                          // C-tile row pitch in LDS
+    constexpr int STAGE_CHUNKS = ROWS * kChunks;
+    constexpr int RING_BYTES = STAGES * STAGE_CHUNKS * 16;
+    constexpr int LDS_BYTES = RING_BYTES > BM * PITCH ? RING_BYTES : BM * PITCH;
+    __shared__ __attribute__((aligned(16))) char lds_raw[LDS_BYTES];
+    u32x4_t* const ring = reinterpret_cast<u32x4_t*>(lds_raw);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN;
+    const int wn = wave % WGN;
     const int half = lane >> 5;
     const int r32 = lane & 31;
 
@@ -57,42 +83,35 @@ __global__ __launch_bounds__(256) void mfma_staged_kernel(
     const int64_t m0 = int64_t(tm) * BM;
     const int64_t n0 = int64_t(tn) * BN;
 
-    // Global -> LDS assignment: chunk e = tid + 256 r is row e / 8, chunk e % 8.
-    const int my_chunk = tid & 7;
-    const uint16_t* a_src[A_PER];
-    const uint16_t* w_src[B_PER];
-    int a_dst[A_PER], w_dst[B_PER];
+    // DMA instruction j of this wave fills LDS rows 8 i .. 8 i + 7 of a stage,
+    // i = wave * IPW + j; lane L writes row 8 i + L / 8, position L % 8, which
+    // holds logical chunk (L % 8) ^ swizzle(row).
+    const uint16_t* src[IPW];
+    int koff[IPW];
 #pragma unroll
-    for (int r = 0; r < A_PER; ++r) {
-        const int row = (tid >> 3) + 32 * r;
-        const int64_t gm = min(m0 + row, m - 1);
-        a_src[r] = a + gm * lda + my_chunk * 8;
-        a_dst[r] = row * kChunks + (my_chunk ^ (row & 7));
-    }
-#pragma unroll
-    for (int r = 0; r < B_PER; ++r) {
-        const int row = (tid >> 3) + 32 * r;
-        const int64_t gn = min(n0 + row, n - 1);
-        w_src[r] = w + gn * ldb + my_chunk * 8;
-        w_dst[r] = BM * kChunks + row * kChunks + (my_chunk ^ (row & 7));
+    for (int j = 0; j < IPW; ++j) {
+        const int row = 8 * (wave * IPW + j) + (lane >> 3);
+        const int chunk = (lane & 7) ^ lds_swizzle(row);
+        koff[j] = chunk * 8;
+        if (row < BM) {
+            src[j] = a + min(m0 + row, m - 1) * lda + koff[j];
+        } else {
+            src[j] = w + min(n0 + (row - BM), n - 1) * ldb + koff[j];
+        }
     }
 
-    u32x4_t ra[A_PER], rb[B_PER];
-    auto load_tile = [&](int64_t k0) {
+    const int64_t ktiles = (k + kBK - 1) / kBK;
+    auto issue = [&](int64_t t) {
+        const int64_t k0 = t * kBK;
         const bool full = k0 + kBK <= k;
-        const bool in_k = k0 + my_chunk * 8 < k;
+        u32x4_t* stage = ring + (t % STAGES) * STAGE_CHUNKS;
 #pragma unroll
-        for (int r = 0; r < A_PER; ++r)
-            ra[r] = (full || in_k) ? load16(a_src[r] + k0) : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int r = 0; r < B_PER; ++r)
-            rb[r] = (full || in_k) ? load16(w_src[r] + k0) : u32x4_t{0u, 0u, 0u, 0u};
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < A_PER; ++r) lds[buf][a_dst[r]] = ra[r];
-#pragma unroll
-        for (int r = 0; r < B_PER; ++r) lds[buf][w_dst[r]] = rb[r];
+        for (int j = 0; j < IPW; ++j) {
+            const void* p = (full || k0 + koff[j] < k) ? static_cast<const void*>(src[j] + k0)
+                                                       : static_cast<const void*>(&g_zero_chunk);
+            __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*)(stage + 64 * (wave * IPW + j)),
+                                             16, 0, 0);
+        }
     };
 
     f32x16_t acc[NI][MJ];
@@ -101,100 +120,151 @@ __global__ __launch_bounds__(256) void mfma_staged_kernel(
 #pragma unroll
         for (int j = 0; j < MJ; ++j) acc[i][j] = f32x16_t{};
 
-    // Fragment rows: lane l reads row (base + l % 32); since every base is a
-    // multiple of 32, the swizzle key (row & 7) is (l & 7).
-    const int swz = lane & 7;
+    // Fragment rows: lane l reads row (base + l % 32) with base a multiple of
+    // 32, so the swizzle key is ((l % 32) >> 1) & 7 = (l >> 1) & 7.
+    const int swz = (lane >> 1) & 7;
     const int a_row0 = wm * WM + r32;
     const int w_row0 = BM + wn * WN + r32;
 
-    const int64_t ktiles = (k + kBK - 1) / kBK;
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
+    // Two fragment register sets: the MFMAs of K-step kk run from one while
+    // the ds_reads of kk + 1 fill the other.
+    u32x4_t af0[MJ], wf0[NI], af1[MJ], wf1[NI];
+    auto read_frags = [&](const u32x4_t* tile, int kk, u32x4_t (&af)[MJ], u32x4_t (&wf)[NI]) {
+        const int chunk = (2 * kk + half) ^ swz;
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) af[j] = tile[(a_row0 + 32 * j) * kChunks + chunk];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) wf[i] = tile[(w_row0 + 32 * i) * kChunks + chunk];
+    };
+    auto mfmas = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI]) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < MJ; ++j) acc[i][j] = mfma_32x32x16<DT>(wf[i], af[j], acc[i][j]);
+    };
+    // Wait until tile u has landed in every wave's part of its stage (each
+    // wave waits on its own vmcnt, the barrier covers the others), then
+    // refill the stage the previous tile used with tile u + AHEAD.
+    auto tile_ready = [&](int64_t u) {
+        const int64_t later = min<int64_t>(ktiles - 1 - u, AHEAD - 1);
+        if (later >= 2) wait_vmcnt<2 * IPW>();
+        else if (later == 1) wait_vmcnt<IPW>();
+        else wait_vmcnt<0>();
+        // Every ds_read of the previous tile has returned before the barrier,
+        // so the stage refilled below is free in every wave.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (u + AHEAD < ktiles) issue(u + AHEAD);
+    };
+
+#pragma unroll
+    for (int t = 0; t < AHEAD; ++t)
+        if (t < ktiles) issue(t);
+    tile_ready(0);
+    read_frags(ring, 0, af0, wf0);
+
     for (int64_t t = 0; t < ktiles; ++t) {
-        const int cur = int(t & 1);
-        const bool more = t + 1 < ktiles;
-        if (more) load_tile((t + 1) * kBK);
-        const u32x4_t* tile = lds[cur];
-#pragma unroll
-        for (int kk = 0; kk < kChunks / 2; ++kk) {
-            const int chunk = (2 * kk + half) ^ swz;
-            u32x4_t af[MJ], wf[NI];
-#pragma unroll
-            for (int j = 0; j < MJ; ++j) af[j] = tile[(a_row0 + 32 * j) * kChunks + chunk];
-#pragma unroll
-            for (int i = 0; i < NI; ++i) wf[i] = tile[(w_row0 + 32 * i) * kChunks + chunk];
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-#pragma unroll
-                for (int j = 0; j < MJ; ++j) acc[i][j] = mfma_32x32x16<DT>(wf[i], af[j], acc[i][j]);
+        const u32x4_t* tile = ring + (t % STAGES) * STAGE_CHUNKS;
+        read_frags(tile, 1, af1, wf1);
+        mfmas(af0, wf0);
+        read_frags(tile, 2, af0, wf0);
+        mfmas(af1, wf1);
+        read_frags(tile, 3, af1, wf1);
+        mfmas(af0, wf0);
+        if (t + 1 < ktiles) {
+            tile_ready(t + 1);
+            read_frags(ring + ((t + 1) % STAGES) * STAGE_CHUNKS, 0, af0, wf0);
         }
-        if (more) store_tile(cur ^ 1);
-        __syncthreads();
+        mfmas(af1, wf1);
     }
 
-    // Epilogue.  acc[i][j][v] is D[n][m] with n = 8 (v/4) + 4 half + v%4 and
-    // m = l % 32 inside the (i, j) block, so each quad v/4 is 4 consecutive
-    // columns of one output row.
+    // Epilogue through LDS.  acc[i][j][v] is D[n][m] with n = 8 (v/4) +
+    // 4 half + v%4 and m = l % 32 inside the (i, j) block, so each quad v/4
+    // is 4 consecutive columns of one output row.  The quads are converted
+    // and written into a BM x BN tile in LDS (row pitch padded by 16 bytes so
+    // the 32 rows one store instruction touches spread over the banks), then
+    // all 256 threads copy the tile out row by row, 16 bytes per lane, so
+    // every global store instruction writes whole 512-byte row segments.
+    constexpr int CPR = BN * OB / 16;                            // 16-byte chunks per row
+    static_assert(NT % CPR == 0, "rows per copy pass");
+    char* ctile = lds_raw;
+    __syncthreads();   // every wave is done reading the last K-tile
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
-        const int64_t row = m0 + wm * WM + 32 * j + r32;
-        if (row >= m) continue;
+        const int row = wm * WM + 32 * j + r32;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t col = n0 + wn * WN + 32 * i + 8 * q + 4 * half;
+                const int col = wn * WN + 32 * i + 8 * q + 4 * half;
                 const f32x16_t& v = acc[i][j];
                 const float x0 = v[4 * q], x1 = v[4 * q + 1], x2 = v[4 * q + 2], x3 = v[4 * q + 3];
-                const int64_t idx = row * ldc + col;
-                if (c_vec && col + 3 < n) {
-                    if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
-                        *reinterpret_cast<f32x4_t*>(static_cast<float*>(c) + idx) = f32x4_t{x0, x1, x2, x3};
-                    } else {
-                        uint32_t lo, hi;
-                        if constexpr (DT_OUT == NANOVLLM_GEMM_BF16) {
-                            lo = f32_to_bf16_rne(x0) | (uint32_t(f32_to_bf16_rne(x1)) << 16);
-                            hi = f32_to_bf16_rne(x2) | (uint32_t(f32_to_bf16_rne(x3)) << 16);
-                        } else {
-                            lo = f32_to_f16_rne(x0) | (uint32_t(f32_to_f16_rne(x1)) << 16);
-                            hi = f32_to_f16_rne(x2) | (uint32_t(f32_to_f16_rne(x3)) << 16);
-                        }
-                        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(c) + idx) = u32x2_t{lo, hi};
-                    }
+                char* dst = ctile + row * PITCH + col * OB;
+                if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
+                    *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{x0, x1, x2, x3};
+                } else if constexpr (DT_OUT == NANOVLLM_GEMM_BF16) {
+                    *reinterpret_cast<u32x2_t*>(dst) =
+                        u32x2_t{f32_to_bf16_rne(x0) | (uint32_t(f32_to_bf16_rne(x1)) << 16),
+                                f32_to_bf16_rne(x2) | (uint32_t(f32_to_bf16_rne(x3)) << 16)};
                 } else {
-                    if (col < n) store_elem<DT_OUT>(c, idx, x0);
-                    if (col + 1 < n) store_elem<DT_OUT>(c, idx + 1, x1);
-                    if (col + 2 < n) store_elem<DT_OUT>(c, idx + 2, x2);
-                    if (col + 3 < n) store_elem<DT_OUT>(c, idx + 3, x3);
+                    *reinterpret_cast<u32x2_t*>(dst) =
+                        u32x2_t{f32_to_f16_rne(x0) | (uint32_t(f32_to_f16_rne(x1)) << 16),
+                                f32_to_f16_rne(x2) | (uint32_t(f32_to_f16_rne(x3)) << 16)};
                 }
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int EPC = 16 / OB;                 // output elements per chunk
+    constexpr int ROWS_PER_PASS = NT / CPR;
+    const int chunk = tid % CPR;
+#pragma unroll 4
+    for (int r = tid / CPR; r < BM; r += ROWS_PER_PASS) {
+        const int64_t grow = m0 + r;
+        const int64_t gcol = n0 + chunk * EPC;
+        if (grow >= m || gcol >= n) continue;
+        const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ctile + r * PITCH + chunk * 16);
+        char* gdst = static_cast<char*>(c) + (grow * ldc + gcol) * OB;
+        if (c_vec && gcol + EPC <= n) {
+            *reinterpret_cast<u32x4_t*>(gdst) = val;
+        } else {
+            const int valid = int(min<int64_t>(EPC, n - gcol));
+            if constexpr (OB == 4) {
+                for (int e = 0; e < valid; ++e) reinterpret_cast<uint32_t*>(gdst)[e] = val[e];
+            } else {
+                for (int e = 0; e < valid; ++e)
+                    reinterpret_cast<uint16_t*>(gdst)[e] = uint16_t(val[e >> 1] >> (16 * (e & 1)));
             }
         }
     }
 }
 
-// Tile shape for a problem: the largest tile that still gives at least
-// one workgroup per CU (256 CUs), else the smallest.
+// Tile configuration for a problem.  Measured on MI355X (2048 x 4096 x
+// 1024 bf16): a 128 x 128 tile with 4 waves and a 2-deep LDS ring (64 KiB)
+// lets two workgroups share a CU, and the two run out of phase, so one's
+// MFMAs overlap the other's loads; 128 x 256 with 8 waves covers shapes
+// with too few 128 x 128 tiles to fill the CUs twice over.
 struct TileChoice {
-    int bm, bn;
+    int bm, bn, waves;
 };
 
 TileChoice choose_tile(int64_t m, int64_t n) {
     auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-    if (tiles(128, 256) >= 256) return {128, 256};
-    if (tiles(256, 128) >= 256 && m >= 256) return {256, 128};
-    return {128, 128};
+    if (tiles(128, 128) >= 512) return {128, 128, 4};
+    if (tiles(128, 256) >= 256) return {128, 256, 8};
+    return {128, 128, 4};
 }
 
-template <int DT, int DT_OUT, int BM, int BN>
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES>
 int launch_tile(const Problem& p, hipStream_t s) {
     const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
     if (tiles_m * tiles_n > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "mfma_staged: grid too large");
-    const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n)), block(256);
+    const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n)), block(WGM * WGN * 64);
     const int out_bytes = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;
-    // Vector stores write 4 elements: 16 B (fp32) or 8 B (bf16/fp16).
-    const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % (4 * out_bytes) == 0) && (p.ldc % 4 == 0);
-    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN>), grid, block, 0, s,
+    // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
+    const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && ((p.ldc * out_bytes) % 16 == 0);
+    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c,
                        p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec);
     return check_launch("mfma_staged");
@@ -203,9 +273,8 @@ int launch_tile(const Problem& p, hipStream_t s) {
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
     const TileChoice t = choose_tile(p.m, p.n);
-    if (t.bm == 128 && t.bn == 256) return launch_tile<DT, DT_OUT, 128, 256>(p, s);
-    if (t.bm == 256 && t.bn == 128) return launch_tile<DT, DT_OUT, 256, 128>(p, s);
-    return launch_tile<DT, DT_OUT, 128, 128>(p, s);
+    if (t.bn == 256) return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 2>(p, s);
+    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2>(p, s);
 }
 
 }  // namespace

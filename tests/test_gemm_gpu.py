@@ -64,7 +64,14 @@ def _check_tolerance(got: torch.Tensor, a: torch.Tensor, b: torch.Tensor, layout
     assert not bad.any(), f"{int(bad.sum())} elements outside tolerance; worst excess {float((err - tol).max()):.3g}"
     ulps = orc.ulp_distance(_to_np_out(got, dout), orc.round_f64(r, NAME[dout]), NAME[dout])
     frac = float((ulps <= 2).mean())
-    assert frac >= min_within_2ulp, f"only {frac:.4f} of elements within 2 ulp"
+    if dout == torch.float32:
+        # fp32 logits: reordering K = 1024 products already moves an fp32 sum
+        # by tens of fp32 ulps, so "2 ulp" is not a meaningful elementwise
+        # bar; the bound above is, plus a normwise one.
+        rel = orc.rel_frobenius(g64, r)
+        assert rel <= 1e-5, f"relative Frobenius error {rel:.3g}"
+    else:
+        assert frac >= min_within_2ulp, f"only {frac:.4f} of elements within 2 ulp"
     return {"max_ulp": int(ulps.max()), "within_2ulp": frac}
 
 
