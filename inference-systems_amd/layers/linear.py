@@ -1,0 +1,201 @@
+"""nano-vLLM linear layers with the MI355X GEMM as their matmul.
+
+Same classes, constructor arguments, weight layout ([out, in] = W[N, K]) and
+tensor-parallel sharding as nanovllm/layers/linear.py:12-156 and the LM head
+of nanovllm/layers/embed_head.py:45-66; the one change is the call that
+computes ``x @ W^T``: ``F.linear`` (linear.py:51, 73, 153; embed_head.py:61)
+becomes ``kernels.gemm.linear``, which routes to the ``nanovllm::gemm`` op.
+
+Routing is opt-in per process with ``NANOVLLM_GEMM_BACKEND`` = ``torch``
+(default, F.linear), ``hip`` or ``auto`` -- the module-level gating pattern
+of nanovllm/layers/layernorm.py:17-20 -- or per module with the
+``gemm_backend`` attribute.  The tensor-parallel collectives are unchanged
+(one GPU here: tp_size is 1 unless a process group says otherwise).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.distributed as dist
+from torch import nn
+
+from ..kernels import linear as gemm_linear
+
+
+def divide(numerator: int, denominator: int) -> int:
+    assert numerator % denominator == 0
+    return numerator // denominator
+
+
+def _tp_rank_size() -> tuple[int, int]:
+    """(rank, world size) of the default process group; (0, 1) without one.
+
+    The reference calls dist.get_rank() unconditionally (linear.py:23-24);
+    a single-GPU process without a group is treated as tp_size 1."""
+    if dist.is_available() and dist.is_initialized():
+        return dist.get_rank(), dist.get_world_size()
+    return 0, 1
+
+
+class LinearBase(nn.Module):
+
+    def __init__(self, input_size: int, output_size: int, bias: bool = False, tp_dim: Optional[int] = None):
+        super().__init__()
+        self.tp_dim = tp_dim
+        self.tp_rank, self.tp_size = _tp_rank_size()
+        self.weight = nn.Parameter(torch.empty(output_size, input_size))
+        self.weight.weight_loader = self.weight_loader
+        if bias:
+            self.bias = nn.Parameter(torch.empty(output_size))
+            self.bias.weight_loader = self.weight_loader
+        else:
+            self.register_parameter("bias", None)
+        self.gemm_backend: Optional[str] = None   # None: NANOVLLM_GEMM_BACKEND
+
+    def matmul(self, x: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+        return gemm_linear(x, self.weight, bias, backend=self.gemm_backend)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        raise NotImplementedError
+
+
+class ReplicatedLinear(LinearBase):
+
+    def __init__(self, input_size: int, output_size: int, bias: bool = False):
+        super().__init__(input_size, output_size, bias)
+
+    def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor):
+        param.data.copy_(loaded_weight)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.matmul(x, self.bias)
+
+
+class ColumnParallelLinear(LinearBase):
+
+    def __init__(self, input_size: int, output_size: int, bias: bool = False):
+        _, tp_size = _tp_rank_size()
+        super().__init__(input_size, divide(output_size, tp_size), bias, 0)
+
+    def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor):
+        param_data = param.data
+        shard_size = param_data.size(self.tp_dim)
+        start_idx = self.tp_rank * shard_size
+        param_data.copy_(loaded_weight.narrow(self.tp_dim, start_idx, shard_size))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.matmul(x, self.bias)
+
+
+class MergedColumnParallelLinear(ColumnParallelLinear):
+
+    def __init__(self, input_size: int, output_sizes: list[int], bias: bool = False):
+        self.output_sizes = output_sizes
+        super().__init__(input_size, sum(output_sizes), bias)
+
+    def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor, loaded_shard_id: int):
+        param_data = param.data
+        shard_offset = sum(self.output_sizes[:loaded_shard_id]) // self.tp_size
+        shard_size = self.output_sizes[loaded_shard_id] // self.tp_size
+        param_data = param_data.narrow(self.tp_dim, shard_offset, shard_size)
+        param_data.copy_(loaded_weight.chunk(self.tp_size, self.tp_dim)[self.tp_rank])
+
+
+class QKVParallelLinear(ColumnParallelLinear):
+
+    def __init__(self, hidden_size: int, head_size: int, total_num_heads: int,
+                 total_num_kv_heads: Optional[int] = None, bias: bool = False):
+        _, tp_size = _tp_rank_size()
+        total_num_kv_heads = total_num_kv_heads or total_num_heads
+        self.head_size = head_size
+        self.num_heads = divide(total_num_heads, tp_size)
+        self.num_kv_heads = divide(total_num_kv_heads, tp_size)
+        output_size = (total_num_heads + 2 * total_num_kv_heads) * self.head_size
+        super().__init__(hidden_size, output_size, bias)
+
+    def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor, loaded_shard_id: str):
+        param_data = param.data
+        assert loaded_shard_id in ["q", "k", "v"]
+        if loaded_shard_id == "q":
+            shard_size = self.num_heads * self.head_size
+            shard_offset = 0
+        elif loaded_shard_id == "k":
+            shard_size = self.num_kv_heads * self.head_size
+            shard_offset = self.num_heads * self.head_size
+        else:
+            shard_size = self.num_kv_heads * self.head_size
+            shard_offset = self.num_heads * self.head_size + self.num_kv_heads * self.head_size
+        param_data = param_data.narrow(self.tp_dim, shard_offset, shard_size)
+        param_data.copy_(loaded_weight.chunk(self.tp_size, self.tp_dim)[self.tp_rank])
+
+
+class RowParallelLinear(LinearBase):
+
+    def __init__(self, input_size: int, output_size: int, bias: bool = False):
+        _, tp_size = _tp_rank_size()
+        super().__init__(divide(input_size, tp_size), output_size, bias, 1)
+
+    def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor):
+        param_data = param.data
+        if param_data.ndim == 1:
+            param_data.copy_(loaded_weight)
+            return
+        shard_size = param_data.size(self.tp_dim)
+        start_idx = self.tp_rank * shard_size
+        param_data.copy_(loaded_weight.narrow(self.tp_dim, start_idx, shard_size))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = self.matmul(x, self.bias if self.tp_rank == 0 else None)
+        if self.tp_size > 1:
+            dist.all_reduce(y)
+        return y
+
+
+class ParallelLMHead(nn.Module):
+    """Tied / vocab-parallel LM head (embed_head.py:45-66) producing fp32 logits.
+
+    The reference selects the last token of each sequence from the forward
+    context in prefill (embed_head.py:57-60); here the caller passes
+    ``last_indices`` (or None in decode).  On the HIP path the GEMM writes
+    fp32 logits directly (out_dtype=float32), which is the dtype the sampler
+    casts to (nanovllm/layers/sampler.py:26)."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, bias: bool = False):
+        super().__init__()
+        assert not bias
+        self.tp_rank, self.tp_size = _tp_rank_size()
+        self.num_embeddings = num_embeddings
+        self.num_embeddings_per_partition = divide(num_embeddings, self.tp_size)
+        self.vocab_start_idx = self.num_embeddings_per_partition * self.tp_rank
+        self.vocab_end_idx = self.vocab_start_idx + self.num_embeddings_per_partition
+        self.weight = nn.Parameter(torch.empty(self.num_embeddings_per_partition, embedding_dim))
+        self.weight.weight_loader = self.weight_loader
+        self.gemm_backend: Optional[str] = None
+
+    def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor):
+        param_data = param.data
+        shard_size = param_data.size(0)
+        start_idx = self.tp_rank * shard_size
+        param_data.copy_(loaded_weight.narrow(0, start_idx, shard_size))
+
+    def forward(self, x: torch.Tensor, last_indices: Optional[torch.Tensor] = None):
+        if last_indices is not None:
+            x = x[last_indices].contiguous()
+        logits = gemm_linear(x, self.weight, None, out_dtype=torch.float32, backend=self.gemm_backend)
+        if self.tp_size > 1:
+            all_logits = [torch.empty_like(logits) for _ in range(self.tp_size)] if self.tp_rank == 0 else None
+            dist.gather(logits, all_logits, 0)
+            logits = torch.cat(all_logits, -1) if self.tp_rank == 0 else None
+        return logits
+
+
+class GemmLinear(nn.Linear):
+    """``nn.Linear`` whose matmul goes through the backend switch; drop-in for
+    the plain nn.Linear projections of nanovllm/layers/gated_delta_net.py:60-63,
+    90 and nanovllm/models/qwen3_5_mtp.py:41."""
+
+    gemm_backend: Optional[str] = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return gemm_linear(x, self.weight, self.bias, backend=self.gemm_backend)

@@ -1,0 +1,124 @@
+"""CPU tests of the nano-vLLM layer mirrors (inference-systems_amd/layers).
+
+Weight loading and tensor-parallel sharding must match the reference layers
+(nanovllm/layers/linear.py:12-156, embed_head.py:45-66); on CPU tensors the
+``auto`` backend routes to F.linear, so outputs compare exactly with an
+unsharded F.linear.  The 2-rank case follows the reference's gloo pattern
+(tests/test_qwen35_tp.py:26-31, 125-158)."""
+from __future__ import annotations
+
+import os
+import tempfile
+
+import pytest
+import torch
+import torch.distributed as dist
+import torch.multiprocessing as mp
+import torch.nn.functional as F
+
+from conftest import PKG
+
+Lyr = PKG.layers
+
+
+def _full_weights(seed=0, k=64, n=96):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(n, k, generator=g), torch.randn(n, generator=g)
+
+
+def test_single_process_layers_match_f_linear():
+    w, b = _full_weights()
+    x = torch.randn(5, 64)
+    for cls in (Lyr.ReplicatedLinear, Lyr.ColumnParallelLinear):
+        layer = cls(64, 96, bias=True)
+        layer.weight.weight_loader(layer.weight, w)
+        layer.bias.weight_loader(layer.bias, b)
+        layer.gemm_backend = "auto"
+        assert torch.equal(layer(x), F.linear(x, w, b))
+    row = Lyr.RowParallelLinear(96, 64, bias=True)
+    wr, br = torch.randn(64, 96), torch.randn(64)
+    row.weight.weight_loader(row.weight, wr)
+    row.bias.weight_loader(row.bias, br)
+    row.gemm_backend = "torch"
+    y = torch.randn(3, 96)
+    assert torch.equal(row(y), F.linear(y, wr, br))
+
+
+def test_merged_and_qkv_loaders():
+    merged = Lyr.MergedColumnParallelLinear(32, [48, 48])
+    g0, g1 = torch.randn(48, 32), torch.randn(48, 32)
+    merged.weight.weight_loader(merged.weight, g0, 0)
+    merged.weight.weight_loader(merged.weight, g1, 1)
+    assert torch.equal(merged.weight.data, torch.cat([g0, g1]))
+    qkv = Lyr.QKVParallelLinear(32, head_size=8, total_num_heads=4, total_num_kv_heads=2)
+    q, k, v = torch.randn(32, 32), torch.randn(16, 32), torch.randn(16, 32)
+    for shard, t in (("q", q), ("k", k), ("v", v)):
+        qkv.weight.weight_loader(qkv.weight, t, shard)
+    assert torch.equal(qkv.weight.data, torch.cat([q, k, v]))
+    qkv.gemm_backend = "auto"
+    x = torch.randn(2, 32)
+    assert torch.equal(qkv(x), F.linear(x, torch.cat([q, k, v])))
+
+
+def test_lm_head_last_indices_and_fp32_logits():
+    head = Lyr.ParallelLMHead(100, 16)
+    w = torch.randn(100, 16).bfloat16()
+    head.weight.data = torch.empty(100, 16, dtype=torch.bfloat16)
+    head.weight.weight_loader(head.weight, w)
+    head.gemm_backend = "auto"
+    x = torch.randn(7, 16).bfloat16()
+    last = torch.tensor([2, 6])
+    logits = head(x, last)
+    assert logits.shape == (2, 100) and logits.dtype == torch.float32
+    assert torch.equal(logits, F.linear(x[last], w).float())
+
+
+def test_gemm_linear_module():
+    m = Lyr.GemmLinear(16, 8)
+    m.gemm_backend = "auto"
+    x = torch.randn(3, 16)
+    assert torch.equal(m(x), F.linear(x, m.weight, m.bias))
+
+
+def _tp_worker(rank, world, init_file, result_file):
+    dist.init_process_group("gloo", init_method=f"file://{init_file}", rank=rank, world_size=world)
+    try:
+        torch.manual_seed(0)
+        k, n, m = 32, 64, 6
+        w1, b1 = torch.randn(n, k), torch.randn(n)
+        w2, b2 = torch.randn(k, n), torch.randn(k)
+        x = torch.randn(m, k)
+        col = Lyr.ColumnParallelLinear(k, n, bias=True)
+        col.weight.weight_loader(col.weight, w1)
+        col.bias.weight_loader(col.bias, b1)
+        row = Lyr.RowParallelLinear(n, k, bias=True)
+        row.weight.weight_loader(row.weight, w2)
+        row.bias.weight_loader(row.bias, b2)
+        for mod in (col, row):
+            mod.gemm_backend = "auto"
+        y = row(col(x))
+        ref = F.linear(F.linear(x, w1, b1), w2, b2)
+        # sharded partial sums + all_reduce reorder the fp32 sum: tolerance 1e-4
+        ok = torch.allclose(y, ref, rtol=1e-4, atol=1e-4)
+        head = Lyr.ParallelLMHead(40, k)
+        wh = torch.randn(40, k)
+        head.weight.weight_loader(head.weight, wh)
+        head.gemm_backend = "auto"
+        logits = head(x)
+        if rank == 0:
+            ok = ok and torch.allclose(logits, F.linear(x, wh), rtol=1e-6, atol=1e-6)
+        else:
+            ok = ok and logits is None
+        with open(f"{result_file}.{rank}", "w") as fh:
+            fh.write("ok" if ok else "mismatch")
+    finally:
+        dist.destroy_process_group()
+
+
+def test_tensor_parallel_two_ranks_gloo():
+    with tempfile.TemporaryDirectory() as tmp:
+        init_file = os.path.join(tmp, "init")
+        result = os.path.join(tmp, "result")
+        mp.start_processes(_tp_worker, args=(2, init_file, result), nprocs=2, start_method="fork")
+        for r in range(2):
+            assert open(f"{result}.{r}").read() == "ok", f"rank {r}"
