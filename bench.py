@@ -48,6 +48,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-vendor", action="store_true", help="skip the torch GPU GEMM comparison")
     p.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
+    p.add_argument("--workload", default=None,
+                   help="measure this workload instead of the prefill headline (for profiling one kernel)")
+    p.add_argument("--m", type=int, default=None, help="M of --workload (default: its largest)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run 10 device copies of MIB MiB (reference kernel for HBM counter scaling)")
     return p.parse_args()
@@ -152,26 +155,50 @@ def main() -> int:
         return f
 
     # ---------------------------------------------------------------- headline
-    name = W.HEADLINE
+    name = args.workload or W.HEADLINE
+    if name not in W.WORKLOADS:
+        print(f"unknown workload {name!r}; choose from {sorted(W.WORKLOADS)}", file=sys.stderr)
+        return 2
     wl = W.WORKLOADS[name]
-    m, n, k = wl.ms[0], wl.n, wl.k
+    m = args.m if args.m is not None else wl.ms[-1]
+    n, k = wl.n, wl.k
     a, w = W.make_inputs(name, m, device=dev)
     out = torch.empty(m, n, dtype=wl.dtype_out, device=dev)
-    kid = L.select(m, n, k, k, k, n, wl.b_layout, code[wl.dtype_in], code[wl.dtype_out], True)
+    ldb_h = k if wl.b_layout == L.B_NK else n
+    kid = L.select(m, n, k, k, ldb_h, n, wl.b_layout, code[wl.dtype_in], code[wl.dtype_out], True)
     kernel = L.kernel_name(kid)
     flops = W.problem_flops(m, n, k)
-    launch = launcher(a, w, out, m, n, k, wl.b_layout, wl.dtype_in, wl.dtype_out)
-    log(f"headline {name}: kernel {kernel}, warmup {args.warmup}, steps {args.steps}")
+    # Bandwidth-bound problems rotate W over more than twice the Infinity
+    # Cache so every launch streams W from HBM.
+    copies = 1
+    if wl.bound == "hbm":
+        w_bytes = w.numel() * w.element_size()
+        copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / w_bytes) + 1)
+    ws_h = [w] + [w.clone() for _ in range(copies - 1)]
+    launches = [launcher(a, ws_h[i % copies], out, m, n, k, wl.b_layout, wl.dtype_in, wl.dtype_out)
+                for i in range(copies)]
+    log(f"headline {name} M={m}: kernel {kernel}, W buffers {copies}, warmup {args.warmup}, steps {args.steps}")
     if args.warmup > 0:
-        GraphTimer(torch, [launch] * args.warmup).time_ms()
-    timer = GraphTimer(torch, [launch] * args.steps)
+        GraphTimer(torch, [launches[i % copies] for i in range(args.warmup)]).time_ms()
+    timer = GraphTimer(torch, [launches[i % copies] for i in range(args.steps)])
     torch.cuda.synchronize()
     elapsed_ms = timer.time_ms()
     torch.cuda.synchronize()
     ms_per_step = elapsed_ms / args.steps
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_MFMA_TFLOPS[dname[wl.dtype_in]]
-    log(f"  {ms_per_step * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  {100 * tflops / peak:.1f}% of {peak} TFLOP/s")
+    byts = W.problem_bytes(m, n, k, wl.dtype_in, wl.dtype_out)
+    gbs = byts / (ms_per_step * 1e-3) / 1e9
+    log(f"  {ms_per_step * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  {100 * tflops / peak:.1f}% of {peak} TFLOP/s  "
+        f"{gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM")
+    if wl.bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(tflops / peak, 4)}
+    roof.update({"traffic": read_traffic() if name == W.HEADLINE else None,
+                 "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": byts})
 
     result = {
         "metric": "TFLOP/s & % MFMA peak (prefill GEMM); HBM GB/s & % peak (decode M<=32)",
@@ -184,14 +211,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, rounded to bf16)",
-        "config": {"workload": name, "m": m, "n": n, "k": k, "b_layout": "W[N,K]", "out_dtype": "bf16",
-                   "kernel": kernel, "timing": "K launches back to back in one HIP graph, HIP events"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 4), "traffic": read_traffic(),
-                     "algorithmic_flops_per_launch": flops,
-                     "algorithmic_bytes_per_launch": W.problem_bytes(m, n, k, wl.dtype_in, wl.dtype_out)},
+        "dtype": dname[wl.dtype_in],
+        "data": "synthetic (seeded random activations and weights, rounded to the input dtype)",
+        "config": {"workload": name, "m": m, "n": n, "k": k,
+                   "b_layout": "W[N,K]" if wl.b_layout == L.B_NK else "B[K,N]",
+                   "out_dtype": dname[wl.dtype_out], "kernel": kernel,
+                   "w_buffers": copies, "timing": "K launches back to back in one HIP graph, HIP events"},
+        "roofline": roof,
     }
 
     # ------------------------------------------------------------ decode rows
@@ -258,25 +284,28 @@ def main() -> int:
                 F.linear(aa, ww)
             return f
         try:
+            if wl.b_layout != L.B_NK:
+                raise RuntimeError("vendor comparison is timed for the W[N,K] layout only")
             t_ms = median_graph_ms(torch, [vendor(a, w)] * 200)
             vt = flops / (t_ms * 1e-3) / 1e12
-            extras["vendor_torch_linear_prefill"] = {"us": round(t_ms * 1e3, 3), "TFLOP/s": round(vt, 2),
+            extras["vendor_torch_linear"] = {"us": round(t_ms * 1e3, 3), "TFLOP/s": round(vt, 2),
                                                      "note": "torch.matmul on the GPU (hipBLASLt/rocBLAS), "
                                                              "comparison only, never dispatched to"}
-            log(f"vendor torch.matmul prefill: {t_ms * 1e3:.2f} us  {vt:.1f} TFLOP/s")
+            log(f"vendor torch F.linear ({name}): {t_ms * 1e3:.2f} us  {vt:.1f} TFLOP/s")
         except Exception as exc:  # comparison only; never fails the bench
-            extras["vendor_torch_linear_prefill"] = {"error": str(exc)[:200]}
+            extras["vendor_torch_linear"] = {"error": str(exc)[:200]}
 
     # ------------------------------------------------------------ CPU baseline
     if not args.no_cpu:
         from oracle import cpu_baseline
 
         a_cpu, w_cpu = W.make_inputs(name, m)
-        cb = cpu_baseline.time_cpu_gemm(a_cpu, w_cpu, True, wl.dtype_out, budget_s=args.cpu_budget)
+        cb = cpu_baseline.time_cpu_gemm(a_cpu, w_cpu, wl.b_layout == L.B_NK, wl.dtype_out,
+                                        budget_s=args.cpu_budget)
         cpu_tf = flops / cb["seconds"] / 1e12
         result["cpu_baseline"] = {
             "value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
-            "sample": f"full {m}x{n}x{k} bf16 F.linear on the host CPU ({cb['cpu_model']}, "
+            "sample": f"full {m}x{n}x{k} {dname[wl.dtype_in]} GEMM on the host CPU ({cb['cpu_model']}, "
                       f"{cb['threads']} threads of {cb['cpu_count']}), median of {cb['samples']} calls",
         }
         log(f"cpu baseline: {cb['seconds'] * 1e3:.1f} ms/call  {cpu_tf:.3f} TFLOP/s on {cb['threads']} threads")

@@ -32,6 +32,7 @@ def _init(layer, gen, scale=0.02):
     return layer
 
 
+@torch.inference_mode()
 def test_layers_hip_match_op():
     gen = torch.Generator().manual_seed(21)
     x = torch.randn(40, 1024, generator=gen).bfloat16().to(DEV)
@@ -57,7 +58,8 @@ def test_lm_head_fp32_logits(m):
     head.gemm_backend = "hip"
     x = torch.randn(m + 3, hidden, generator=gen).bfloat16()
     last = torch.arange(m) + 3
-    logits = head(x.to(DEV), last.to(DEV))
+    with torch.inference_mode():        # the reference runs its model in inference mode
+        logits = head(x.to(DEV), last.to(DEV))
     torch.cuda.synchronize()
     assert logits.dtype == torch.float32 and logits.shape == (m, vocab)
     rows = np.unique(np.linspace(0, m - 1, min(m, 16)).astype(int))
@@ -84,6 +86,7 @@ class _QwenMLP(torch.nn.Module):
 
 
 @pytest.mark.parametrize("m", [4, 32])
+@torch.inference_mode()
 def test_mlp_block_graph_capture(m):
     gen = torch.Generator().manual_seed(23)
     mlp = _QwenMLP()
