@@ -62,9 +62,12 @@ enum {
  *                  global memory, any shape          (gemm_bench.cu:80-115, gemm_wmma.cu:56-104)
  *   MFMA_STAGED    LDS multi-buffered macro-tile MFMA kernel for
  *                  prefill-shaped problems           (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
- *   SPLITK_DECODE  split-K wavefront-reduction kernel for M <= 32 that
+ *   SPLITK_DECODE  split-K wavefront-reduction kernel for 2 <= M <= 32 that
  *                  streams W once                    (replaces the cuBLAS fallback of
  *                                                     gemm_bench.cu:260-273 for decode shapes)
+ *   GEMV_DECODE    M == 1: one wave per W row, coalesced 16-byte streaming,
+ *                  VALU dot products                 (the qwen35_decode_qkv shape of
+ *                                                     gemm_bench.cu:46, cuBLAS there)
  */
 enum {
     NANOVLLM_GEMM_KERNEL_FP32_NAIVE = 0,
@@ -72,7 +75,8 @@ enum {
     NANOVLLM_GEMM_KERNEL_MFMA_DIRECT = 2,
     NANOVLLM_GEMM_KERNEL_MFMA_STAGED = 3,
     NANOVLLM_GEMM_KERNEL_SPLITK_DECODE = 4,
-    NANOVLLM_GEMM_KERNEL_COUNT = 5
+    NANOVLLM_GEMM_KERNEL_GEMV_DECODE = 5,
+    NANOVLLM_GEMM_KERNEL_COUNT = 6
 };
 
 /* Return codes. */

@@ -25,7 +25,8 @@ KERNEL_FP32_TILED = 1
 KERNEL_MFMA_DIRECT = 2
 KERNEL_MFMA_STAGED = 3
 KERNEL_SPLITK_DECODE = 4
-KERNEL_COUNT = 5
+KERNEL_GEMV_DECODE = 5
+KERNEL_COUNT = 6
 
 OK, EINVAL, EUNSUPPORTED, ELAUNCH = 0, -1, -2, -3
 

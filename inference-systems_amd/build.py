@@ -40,6 +40,7 @@ SOURCES = [
     "gemm_direct.hip",
     "gemm_staged.hip",
     "gemm_decode.hip",
+    "gemm_gemv.hip",
 ]
 
 

@@ -70,16 +70,25 @@ bool supports(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldb, int
         case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16);
         case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE:
             return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && m <= kDecodeMaxM;
+        case NANOVLLM_GEMM_KERNEL_GEMV_DECODE:
+            return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && m == 1;
         default: return false;
     }
 }
 
+// M = 1 with a W of at most this many bytes goes to gemv_decode: its many
+// small workgroups win when the stream is short (12.6 MB: 4.5 vs 5.0 us on
+// MI355X), while for long streams (the 311 MB LM head) splitk_decode's
+// longer per-lane runs are faster (53 vs 64 us).
+constexpr int64_t kGemvMaxWBytes = int64_t(64) << 20;
+
 // The shape-selection table (replaces supports_wmma + choose_path,
 // cuda_kernels/gemm/src/gemm_bench.cu:252-273).  Every valid problem maps
 // to a kernel of this library; there is no vendor fallback.
-int select(int64_t m, int64_t k, int64_t lda, int64_t ldb, int b_layout, int din, int aligned16) {
+int select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_layout, int din, int aligned16) {
     if (din == NANOVLLM_GEMM_F32) return NANOVLLM_GEMM_KERNEL_FP32_TILED;
     if (vector_ok(k, lda, ldb, b_layout, aligned16)) {
+        if (m == 1 && n * k * 2 <= kGemvMaxWBytes) return NANOVLLM_GEMM_KERNEL_GEMV_DECODE;
         if (m <= kDecodeMaxM) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
         return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
     }
@@ -93,6 +102,7 @@ int run(int kernel_id, const Problem& p, hipStream_t s) {
         case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return launch_mfma_direct(p, s);
         case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return launch_mfma_staged(p, s);
         case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return launch_splitk_decode(p, s);
+        case NANOVLLM_GEMM_KERNEL_GEMV_DECODE: return launch_gemv_decode(p, s);
         default: return set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
     }
 }
@@ -112,7 +122,7 @@ int gemm_entry(int forced_kernel, const void* a, const void* b, void* c, int64_t
     const int al = aligned16_of(a, b);
     int kernel = forced_kernel;
     if (kernel < 0) {
-        kernel = select(m, k, lda, ldb, b_layout, din, al);
+        kernel = select(m, n, k, lda, ldb, b_layout, din, al);
     } else if (kernel >= NANOVLLM_GEMM_KERNEL_COUNT) {
         return set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel);
     } else if (!supports(kernel, m, k, lda, ldb, b_layout, din, al)) {
@@ -165,7 +175,7 @@ int nanovllm_gemm_select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t l
     nvg::g_last_error.clear();
     const int rc = nvg::validate(m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out);
     if (rc != NANOVLLM_GEMM_OK) return rc;
-    return nvg::select(m, k, lda, ldb, b_layout, dtype_in, aligned16);
+    return nvg::select(m, n, k, lda, ldb, b_layout, dtype_in, aligned16);
 }
 
 int nanovllm_gemm_kernel_supports(int kernel_id, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
@@ -182,6 +192,7 @@ const char* nanovllm_gemm_kernel_name(int kernel_id) {
         case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return "mfma_direct";
         case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return "mfma_staged";
         case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return "splitk_decode";
+        case NANOVLLM_GEMM_KERNEL_GEMV_DECODE: return "gemv_decode";
         default: return "unknown";
     }
 }

@@ -152,6 +152,7 @@ int launch_fp32_tiled(const Problem& p, hipStream_t s);
 int launch_mfma_direct(const Problem& p, hipStream_t s);
 int launch_mfma_staged(const Problem& p, hipStream_t s);
 int launch_splitk_decode(const Problem& p, hipStream_t s);
+int launch_gemv_decode(const Problem& p, hipStream_t s);
 
 // Records a message for nanovllm_gemm_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...);

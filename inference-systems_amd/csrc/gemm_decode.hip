@@ -2,11 +2,12 @@
 // with W[N,K] in the nn.Linear layout.  At these shapes the work is
 // streaming W once from HBM (N*K*2 bytes) while A (M*K*2 bytes, at most
 // 64 KiB) stays in L2.  Design:
-//   * one 256-thread workgroup per 16 rows of W; its 4 waves split K,
-//     taking 32-element K-steps round robin (wave w takes steps w, w+4, ..),
-//     so together the 4 waves read 256 contiguous bytes of each W row;
-//   * each lane issues all of its W loads (8 x 16 B for K = 1024) before
-//     the first MFMA, so the whole of W is in flight almost at once;
+//   * one workgroup per 16 rows of W (4 waves; M <= 8) or per 32 rows (8
+//     waves; 8 < M <= 32, so each A fragment serves two W row groups); the
+//     waves split K, taking 32-element K-steps round robin, so together they
+//     read contiguous runs of each W row;
+//   * each lane issues its W loads for several K-steps (8 x 16 B for K = 1024
+//     with 4 waves) before the first MFMA, so W is in flight almost at once;
 //   * v_mfma_f32_16x16x32 with W as the first operand (16 rows of W) and up
 //     to two 16-row groups of A as the second; rows of A past M are zero;
 //   * the four per-wave partial tiles are summed in LDS in a fixed order
@@ -18,25 +19,25 @@
 namespace nvg {
 namespace {
 
-constexpr int kDecWaves = 4;
-constexpr int kDecRows = 16;   // W rows per workgroup
 constexpr int kDecStep = 32;   // K elements per MFMA
-constexpr int kDecUnroll = 8;  // K-steps whose loads are issued together
 
-template <int DT, int DT_OUT, int MG>
-__global__ __launch_bounds__(256) void splitk_decode_kernel(
+// RG groups of 16 W rows per workgroup, WAVES waves splitting K round robin,
+// MG groups of 16 A rows, UNROLL K-steps whose loads are issued together.
+template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL>
+__global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc) {
-    __shared__ float red[kDecWaves][MG][kDecRows][16];
+    __shared__ float red[WAVES][RG][MG][16][16];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int i16 = lane & 15;   // W row (first operand) / A row (second operand)
     const int grp = lane >> 4;   // which 8-element chunk of the 32-wide K-step
 
-    const int64_t n0 = int64_t(blockIdx.x) * kDecRows;
-    const int64_t wrow = min(n0 + i16, n - 1);
-    const uint16_t* wp = w + wrow * ldb + grp * 8;
+    const int64_t n0 = int64_t(blockIdx.x) * 16 * RG;
+    const uint16_t* wp[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) wp[r] = w + min(n0 + 16 * r + i16, n - 1) * ldb + grp * 8;
     const uint16_t* ap[MG];
     bool a_in[MG];
 #pragma unroll
@@ -47,61 +48,76 @@ __global__ __launch_bounds__(256) void splitk_decode_kernel(
     }
 
     const int64_t steps = (k + kDecStep - 1) / kDecStep;
-    f32x4_t acc[MG];
+    f32x4_t acc[RG][MG];
 #pragma unroll
-    for (int g = 0; g < MG; ++g) acc[g] = f32x4_t{};
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[r][g] = f32x4_t{};
 
-    for (int64_t s0 = wave; s0 < steps; s0 += kDecWaves * kDecUnroll) {
-        u32x4_t wf[kDecUnroll];
-        u32x4_t af[MG][kDecUnroll];
+    for (int64_t s0 = wave; s0 < steps; s0 += WAVES * UNROLL) {
+        u32x4_t wf[RG][UNROLL];
+        u32x4_t af[MG][UNROLL];
 #pragma unroll
-        for (int u = 0; u < kDecUnroll; ++u) {
-            const int64_t kc = (s0 + kDecWaves * u) * kDecStep + grp * 8;
-            const bool in_k = kc < k;  // K % 8 == 0: a chunk is all in or all out
-            wf[u] = in_k ? load16(wp + (kc - grp * 8)) : u32x4_t{0u, 0u, 0u, 0u};
+        for (int u = 0; u < UNROLL; ++u) {
+            const int64_t ks = (s0 + WAVES * u) * kDecStep;
+            const bool in_k = ks + grp * 8 < k;  // K % 8 == 0: a chunk is all in or all out
+#pragma unroll
+            for (int r = 0; r < RG; ++r) wf[r][u] = in_k ? load16(wp[r] + ks) : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int g = 0; g < MG; ++g)
-                af[g][u] = (in_k && a_in[g]) ? load16(ap[g] + (kc - grp * 8)) : u32x4_t{0u, 0u, 0u, 0u};
+                af[g][u] = (in_k && a_in[g]) ? load16(ap[g] + ks) : u32x4_t{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int u = 0; u < kDecUnroll; ++u)
+        for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-            for (int g = 0; g < MG; ++g) acc[g] = mfma_16x16x32<DT>(wf[u], af[g][u], acc[g]);
+            for (int r = 0; r < RG; ++r)
+#pragma unroll
+                for (int g = 0; g < MG; ++g) acc[r][g] = mfma_16x16x32<DT>(wf[r][u], af[g][u], acc[r][g]);
     }
 
-    // acc[g][v] is D[n = 4*(l/16) + v][m = l%16] of group g.
+    // acc[r][g][v] is D[n = 4*(l/16) + v][m = l%16] of W-row group r, A-row group g.
 #pragma unroll
-    for (int g = 0; g < MG; ++g)
+    for (int r = 0; r < RG; ++r)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) red[wave][g][4 * grp + v][i16] = acc[g][v];
+        for (int g = 0; g < MG; ++g)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[wave][r][g][4 * grp + v][i16] = acc[r][g][v];
     __syncthreads();
 
-    const int t = threadIdx.x;
-    const int nn = t & 15;
-    const int mm = t >> 4;
+    // Sum the per-wave partials in wave order (deterministic) and store.
+    for (int e = threadIdx.x; e < RG * MG * 256; e += WAVES * 64) {
+        const int r = e / (MG * 256);
+        const int g = (e / 256) % MG;
+        const int nn = e & 15;
+        const int mm = (e >> 4) & 15;
+        float sum = red[0][r][g][nn][mm];
 #pragma unroll
-    for (int g = 0; g < MG; ++g) {
-        const float sum = ((red[0][g][nn][mm] + red[1][g][nn][mm]) + red[2][g][nn][mm]) + red[3][g][nn][mm];
+        for (int wv = 1; wv < WAVES; ++wv) sum += red[wv][r][g][nn][mm];
         const int64_t row = g * 16 + mm;
-        const int64_t col = n0 + nn;
+        const int64_t col = n0 + 16 * r + nn;
         if (row < m && col < n) store_elem<DT_OUT>(c, row * ldc + col, sum);
     }
 }
 
+template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL>
+int launch_cfg(const Problem& p, hipStream_t s) {
+    const int64_t blocks = (p.n + 16 * RG - 1) / (16 * RG);
+    if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(WAVES * 64);
+    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, MG, RG, WAVES, UNROLL>), grid, block, 0, s,
+                       static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
+                       p.lda, p.ldb, p.ldc);
+    return check_launch("splitk_decode");
+}
+
+// Configurations measured on MI355X for N = 6144, K = 1024: up to 8 rows of A,
+// 16 W rows per 4-wave workgroup; beyond that 32 W rows per 8-wave workgroup,
+// which reads each A fragment once for two W row groups.
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
-    const int64_t blocks = (p.n + kDecRows - 1) / kDecRows;
-    if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
-    const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
-    const auto* a = static_cast<const uint16_t*>(p.a);
-    const auto* w = static_cast<const uint16_t*>(p.b);
-    if (p.m <= 16)
-        hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, 1>), grid, block, 0, s, a, w, p.c, p.m, p.n, p.k,
-                           p.lda, p.ldb, p.ldc);
-    else
-        hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, 2>), grid, block, 0, s, a, w, p.c, p.m, p.n, p.k,
-                           p.lda, p.ldb, p.ldc);
-    return check_launch("splitk_decode");
+    if (p.m <= 8) return launch_cfg<DT, DT_OUT, 1, 1, 4, 8>(p, s);
+    if (p.m <= 16) return launch_cfg<DT, DT_OUT, 1, 2, 8, 2>(p, s);
+    return launch_cfg<DT, DT_OUT, 2, 2, 8, 2>(p, s);
 }
 
 }  // namespace

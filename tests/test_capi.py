@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_names(lib):
     assert lib.nanovllm_gemm_version() >> 16 == 1
-    expected = ["fp32_naive", "fp32_tiled", "mfma_direct", "mfma_staged", "splitk_decode"]
+    expected = ["fp32_naive", "fp32_tiled", "mfma_direct", "mfma_staged", "splitk_decode", "gemv_decode"]
     assert [L.kernel_name(i) for i in range(L.KERNEL_COUNT)] == expected
     assert L.kernel_name(99) == "unknown" and L.kernel_name(-1) == "unknown"
 
@@ -92,11 +92,13 @@ def test_gemm_with_kernel_refuses_unsupported_rung(lib):
     assert rc == L.EUNSUPPORTED
 
 
-def _expected(m, k, lda, ldb, layout, din, aligned):
+def _expected(m, n, k, lda, ldb, layout, din, aligned):
     if din == F32:
         return L.KERNEL_FP32_TILED
     vec = aligned and k % 8 == 0 and lda % 8 == 0 and ldb % 8 == 0 and layout == NK
     if vec:
+        if m == 1 and n * k * 2 <= 64 * 2 ** 20:
+            return L.KERNEL_GEMV_DECODE
         return L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
     return L.KERNEL_MFMA_DIRECT
 
@@ -116,7 +118,7 @@ def test_selection_table_total_and_self_consistent(din, dout):
         ldb = (k if layout == NK else n) + pad
         kid = L.select(m, n, k, lda, ldb, n, layout, din, dout, aligned)
         assert 0 <= kid < L.KERNEL_COUNT
-        assert kid == _expected(m, k, lda, ldb, layout, din, aligned), (m, n, k, layout, aligned, pad)
+        assert kid == _expected(m, n, k, lda, ldb, layout, din, aligned), (m, n, k, layout, aligned, pad)
         assert L.kernel_supports(kid, m, n, k, lda, ldb, n, layout, din, dout, aligned)
 
 
@@ -126,7 +128,8 @@ def test_selection_on_workloads_and_qwen_shapes():
     want = {
         "fp32_square_1024": {1024: "fp32_tiled"},
         "bf16_prefill_2048x4096x1024": {2048: "mfma_staged"},
-        "bf16_decode_n6144_k1024": {m: "splitk_decode" for m in (1, 4, 8, 16, 32)},
+        "bf16_decode_n6144_k1024": {1: "gemv_decode", 4: "splitk_decode", 8: "splitk_decode",
+                                    16: "splitk_decode", 32: "splitk_decode"},
         "fp16_down_4096x1024x3584": {4096: "mfma_staged"},
         "bf16_lm_head_n151936_k1024": {1: "splitk_decode", 32: "splitk_decode", 512: "mfma_staged"},
     }
@@ -138,7 +141,8 @@ def test_selection_on_workloads_and_qwen_shapes():
             assert L.kernel_name(kid) == want[name][m], (name, m)
     for label, m, n, k in W.QWEN35_SHAPES:
         kid = L.select(m, n, k, k, k, n, NK, BF16, BF16, 1)
-        assert L.kernel_name(kid) == ("splitk_decode" if m <= 32 else "mfma_staged"), label
+        want_k = "gemv_decode" if m == 1 else ("splitk_decode" if m <= 32 else "mfma_staged")
+        assert L.kernel_name(kid) == want_k, label
         # the reference's B[K,N] layout of the same shapes runs on the direct rung
         kid = L.select(m, n, k, k, n, n, KN, BF16, F32, 1)
         assert L.kernel_name(kid) == "mfma_direct", label

@@ -81,7 +81,7 @@ def _check_tolerance(got: torch.Tensor, a: torch.Tensor, b: torch.Tensor, layout
 SMALL_SHAPES = [(1, 1, 8), (5, 7, 9), (1, 37, 64), (16, 16, 16), (31, 65, 72), (33, 100, 136),
                 (127, 193, 65), (130, 300, 264), (64, 1024, 2048), (257, 129, 520)]
 KERNELS = [L.KERNEL_FP32_NAIVE, L.KERNEL_FP32_TILED, L.KERNEL_MFMA_DIRECT, L.KERNEL_MFMA_STAGED,
-           L.KERNEL_SPLITK_DECODE]
+           L.KERNEL_SPLITK_DECODE, L.KERNEL_GEMV_DECODE]
 PAIRS = [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
          (torch.float16, torch.float16), (torch.float16, torch.float32)]
 
@@ -208,13 +208,13 @@ def test_unaligned_pointer_takes_direct_and_is_correct():
 
 
 @pytest.mark.parametrize("kernel", [L.KERNEL_FP32_TILED, L.KERNEL_MFMA_DIRECT, L.KERNEL_MFMA_STAGED,
-                                    L.KERNEL_SPLITK_DECODE], ids=lambda k: L.kernel_name(k))
+                                    L.KERNEL_SPLITK_DECODE, L.KERNEL_GEMV_DECODE], ids=lambda k: L.kernel_name(k))
 def test_guard_bands_untouched(kernel):
     """Write through the C ABI into a padded C (ldc > n, a row of canaries
     above and below): nothing outside the M x N window may change."""
     din = torch.float32 if kernel == L.KERNEL_FP32_TILED else torch.bfloat16
     dout = torch.float32 if kernel == L.KERNEL_FP32_TILED else torch.bfloat16
-    m = 20 if kernel == L.KERNEL_SPLITK_DECODE else 150
+    m = {L.KERNEL_SPLITK_DECODE: 20, L.KERNEL_GEMV_DECODE: 1}.get(kernel, 150)
     n, k, pad = 301, 200, 7
     ldc = n + pad
     gen = torch.Generator().manual_seed(8)
