@@ -48,18 +48,19 @@ __device__ __forceinline__ float half_to_f32(uint16_t h) {
     else return f16_to_f32(h);
 }
 
-// fp32 -> bf16, round to nearest, ties to even; NaN stays a quiet NaN.
-__host__ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
-}
+// fp32 -> bf16 / fp16 with gfx950's conversion instructions
+// (v_cvt_pk_bf16_f32, v_cvt_f16_f32 / v_cvt_pk_f16_f32): round to nearest,
+// ties to even, NaN stays NaN, overflow to infinity.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
-// fp32 -> fp16 through the hardware conversion (round to nearest even in
-// the default mode; overflow to infinity).
-__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+template <int DT_OUT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    if constexpr (DT_OUT == NANOVLLM_GEMM_BF16) {
+        return __builtin_bit_cast(uint32_t, bf16x2_t{static_cast<__bf16>(lo), static_cast<__bf16>(hi)});
+    } else {
+        return __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(lo), static_cast<_Float16>(hi)});
+    }
 }
 
 // Store one fp32 accumulator as the output element type.
@@ -68,9 +69,9 @@ __device__ __forceinline__ void store_elem(void* c, int64_t idx, float v) {
     if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
         static_cast<float*>(c)[idx] = v;
     } else if constexpr (DT_OUT == NANOVLLM_GEMM_BF16) {
-        static_cast<uint16_t*>(c)[idx] = f32_to_bf16_rne(v);
+        static_cast<uint16_t*>(c)[idx] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
     } else {
-        static_cast<uint16_t*>(c)[idx] = f32_to_f16_rne(v);
+        static_cast<uint16_t*>(c)[idx] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
     }
 }
 

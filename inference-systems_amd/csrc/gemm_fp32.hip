@@ -4,7 +4,8 @@
 //                 reference ladder: cuda_kernels/gemm/src/gemm.cu:7-15,
 //                 gemm_tiled.cu:36-51).
 //   fp32_tiled  — 64x64 output tile per 256-thread workgroup, K-tiles of 32
-//                 staged in LDS (double buffered, one barrier per K-tile),
+//                 staged in LDS (double buffered, one barrier per K-tile,
+//                 fragments read with ds_read_b128 in a K-permuted order),
 //                 products on the fp32 matrix cores with
 //                 v_mfma_f32_32x32x2_f32 (full fp32 precision; gfx950 has no
 //                 reduced-precision fp32 MFMA).  Replaces the shared-memory and
@@ -38,17 +39,20 @@ __global__ __launch_bounds__(256) void fp32_naive_kernel(
 constexpr int kT32BM = 64;
 constexpr int kT32BN = 64;
 constexpr int kT32BK = 32;
-constexpr int kT32Pad = 1;  // odd row pitch: transposed LDS writes hit 32 distinct banks
+constexpr int kT32Pitch = kT32BK + 4;   // 36 floats: 16-lane ds_read_b128 groups hit 64 distinct banks
 
 template <int BL>
 __global__ __launch_bounds__(256) void fp32_tiled_kernel(
     const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
     int tiles_m, int tiles_n) {
-    // Both tiles are kept k-major so that lane l of an MFMA reads element
-    // (k, base + l % 32): consecutive lanes hit consecutive banks.
-    __shared__ float As[2][kT32BK][kT32BM + kT32Pad];
-    __shared__ float Bs[2][kT32BK][kT32BN + kT32Pad];
+    // Both tiles are kept row-major over K ([row][k], pitch 36 floats), double
+    // buffered.  For v_mfma_f32_32x32x2_f32 lane l supplies A(i = l%32, k) and
+    // B(k, j = l%32) with the same k; MFMA step s of a K-tile uses
+    // k = 16 (l/32) + s, so lane l needs 16 consecutive k of one row of each
+    // tile and reads them with four ds_read_b128.
+    __shared__ __attribute__((aligned(16))) float As[2][kT32BM][kT32Pitch];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kT32BN][kT32Pitch];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -65,7 +69,8 @@ __global__ __launch_bounds__(256) void fp32_tiled_kernel(
 
     // Each thread moves 8 elements of each operand per K-tile.  A (and W in
     // the NK layout) is read along K: 32 consecutive threads cover one
-    // 128-byte row segment.  B in the KN layout is read along N.
+    // 128-byte row segment.  B in the KN layout is read along N and written
+    // transposed.
     auto load_tile = [&](int64_t k0) {
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
@@ -90,11 +95,11 @@ __global__ __launch_bounds__(256) void fp32_tiled_kernel(
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const int e = tid + 256 * r;
-            As[buf][e & 31][e >> 5] = ra[r];
+            As[buf][e >> 5][e & 31] = ra[r];
             if constexpr (BL == NANOVLLM_GEMM_B_NK) {
-                Bs[buf][e & 31][e >> 5] = rb[r];
+                Bs[buf][e >> 5][e & 31] = rb[r];
             } else {
-                Bs[buf][e >> 6][e & 63] = rb[r];
+                Bs[buf][e & 63][e >> 6] = rb[r];
             }
         }
     };
@@ -112,15 +117,15 @@ __global__ __launch_bounds__(256) void fp32_tiled_kernel(
         const int cur = int(t & 1);
         const bool more = t + 1 < ktiles;
         if (more) load_tile((t + 1) * kT32BK);
-        // 32x32x2: lane l supplies A(i = l%32, k) and B(k, j = l%32) with
-        // k = 2 s + l/32; the pairing is identical for both operands, so
-        // every k of the tile is used exactly once.
+        f32x4_t av[4], bv[4];
 #pragma unroll
-        for (int s = 0; s < kT32BK / 2; ++s) {
-            const float av = As[cur][2 * s + half][ai];
-            const float bv = Bs[cur][2 * s + half][bj];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) {
+            av[q] = *reinterpret_cast<const f32x4_t*>(&As[cur][ai][16 * half + 4 * q]);
+            bv[q] = *reinterpret_cast<const f32x4_t*>(&Bs[cur][bj][16 * half + 4 * q]);
         }
+#pragma unroll
+        for (int st = 0; st < kT32BK / 2; ++st)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[st >> 2][st & 3], bv[st >> 2][st & 3], acc, 0, 0, 0);
         if (more) store_tile(cur ^ 1);
         __syncthreads();
     }

@@ -67,8 +67,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int STAGE_CHUNKS = ROWS * kChunks;
     constexpr int RING_BYTES = STAGES * STAGE_CHUNKS * 16;
     constexpr int LDS_BYTES = RING_BYTES > BM * PITCH ? RING_BYTES : BM * PITCH;
-    __shared__ __attribute__((aligned(16))) char lds_raw[LDS_BYTES];
-    u32x4_t* const ring = reinterpret_cast<u32x4_t*>(lds_raw);
+    __shared__ u32x4_t ring[LDS_BYTES / 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -188,7 +187,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // every global store instruction writes whole 512-byte row segments.
     constexpr int CPR = BN * OB / 16;                            // 16-byte chunks per row
     static_assert(NT % CPR == 0, "rows per copy pass");
-    char* ctile = lds_raw;
+    char* ctile = reinterpret_cast<char*>(ring);
     __syncthreads();   // every wave is done reading the last K-tile
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
@@ -203,14 +202,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
                 char* dst = ctile + row * PITCH + col * OB;
                 if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
                     *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{x0, x1, x2, x3};
-                } else if constexpr (DT_OUT == NANOVLLM_GEMM_BF16) {
-                    *reinterpret_cast<u32x2_t*>(dst) =
-                        u32x2_t{f32_to_bf16_rne(x0) | (uint32_t(f32_to_bf16_rne(x1)) << 16),
-                                f32_to_bf16_rne(x2) | (uint32_t(f32_to_bf16_rne(x3)) << 16)};
                 } else {
-                    *reinterpret_cast<u32x2_t*>(dst) =
-                        u32x2_t{f32_to_f16_rne(x0) | (uint32_t(f32_to_f16_rne(x1)) << 16),
-                                f32_to_f16_rne(x2) | (uint32_t(f32_to_f16_rne(x3)) << 16)};
+                    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2<DT_OUT>(x0, x1), pack2<DT_OUT>(x2, x3)};
                 }
             }
         }
@@ -219,7 +212,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int EPC = 16 / OB;                 // output elements per chunk
     constexpr int ROWS_PER_PASS = NT / CPR;
     const int chunk = tid % CPR;
-#pragma unroll 4
+    if (c_vec && m0 + BM <= m && n0 + BN <= n) {
+        // Interior tile (uniform branch): whole 16-byte chunks, no masks.
+        static_assert(BM % ROWS_PER_PASS == 0, "copy passes");
+#pragma unroll
+        for (int pass = 0; pass < BM / ROWS_PER_PASS; ++pass) {
+            const int r = tid / CPR + pass * ROWS_PER_PASS;
+            const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ctile + r * PITCH + chunk * 16);
+            *reinterpret_cast<u32x4_t*>(static_cast<char*>(c) + ((m0 + r) * ldc + n0 + chunk * EPC) * OB) = val;
+        }
+        return;
+    }
     for (int r = tid / CPR; r < BM; r += ROWS_PER_PASS) {
         const int64_t grow = m0 + r;
         const int64_t gcol = n0 + chunk * EPC;

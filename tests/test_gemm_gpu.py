@@ -319,3 +319,39 @@ def test_linear_backends_on_gpu():
     assert torch.equal(G.linear(x, w, bias, backend="auto"), y_hip)
     y_torch = G.linear(x, w, bias, backend="torch").float()
     assert torch.allclose(y_hip.float(), y_torch, atol=0.05, rtol=0.02)
+
+
+# ---------------------------------------------------------------------------
+# Output rounding: round to nearest, ties to even, on every kernel
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_output_rounding_ties_to_even(din):
+    """C[m, n] = a_m * w_n exactly (one non-zero K term), with a = +-(1 + i/s)
+    and w = 1 + j/s exact in the input type: many products fall exactly half
+    way between two output values, so truncation, ties-away or double
+    rounding would differ from the oracle's single RNE in some element."""
+    step = 128.0 if din == torch.bfloat16 else 1024.0
+    m, n, k = 64, 96, 8
+    a = torch.zeros(m, k, dtype=torch.float64)
+    w = torch.zeros(n, k, dtype=torch.float64)
+    idx_m = torch.arange(m, dtype=torch.float64)
+    idx_n = torch.arange(n, dtype=torch.float64)
+    a[:, 0] = (1.0 + torch.remainder(idx_m * 3, step) / step) * torch.where(torch.arange(m) % 2 == 0, 1.0, -1.0)
+    w[:, 0] = 1.0 + torch.remainder(idx_n * 5, step) / step
+    a_t, w_t = a.to(din), w.to(din)
+    assert torch.equal(a_t.double(), a) and torch.equal(w_t.double(), w)   # inputs exact
+    exact = (a @ w.T).numpy()
+    want = orc.round_f64(exact, NAME[din])
+    ad, wd = a_t.to(DEV), w_t.to(DEV)
+    ran = 0
+    for kernel in KERNELS:
+        for mm in (1, 32, m):
+            if not L.kernel_supports(kernel, mm, n, k, k, k, n, L.B_NK, CODE[din], CODE[din], True):
+                continue
+            _say(f"rounding {L.kernel_name(kernel)} {NAME[din]} M={mm}")
+            out = G.gemm_with_kernel(ad[:mm].contiguous(), wd, kernel, din)
+            torch.cuda.synchronize()
+            got = _to_np_out(out, din)
+            assert np.array_equal(got, want[:mm]), f"{L.kernel_name(kernel)}: {int((got != want[:mm]).sum())} differ"
+            ran += 1
+    assert ran >= 6   # direct x3, staged x3, splitk x2, gemv x1
