@@ -62,11 +62,14 @@ enum {
  *                  global memory, any shape          (gemm_bench.cu:80-115, gemm_wmma.cu:56-104)
  *   MFMA_STAGED    LDS multi-buffered macro-tile MFMA kernel for
  *                  prefill-shaped problems           (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
- *   SPLITK_DECODE  split-K wavefront-reduction kernel for 2 <= M <= 32 that
- *                  streams W once                    (replaces the cuBLAS fallback of
+ *   SPLITK_DECODE  split-K wavefront-reduction kernel for M <= 32 that
+ *                  streams W once; selected for 2 <= M <= 32, and for
+ *                  M == 1 when W is larger than 64 MiB (LM head)
+ *                                                    (replaces the cuBLAS fallback of
  *                                                     gemm_bench.cu:260-273 for decode shapes)
  *   GEMV_DECODE    M == 1: one wave per W row, coalesced 16-byte streaming,
- *                  VALU dot products                 (the qwen35_decode_qkv shape of
+ *                  VALU dot products; selected when W is at most 64 MiB
+ *                                                    (the qwen35_decode_qkv shape of
  *                                                     gemm_bench.cu:46, cuBLAS there)
  */
 enum {
