@@ -114,6 +114,11 @@ __device__ __forceinline__ u32x4_t load16(const void* p) {
     return *static_cast<const u32x4_t*>(p);
 }
 
+// Integer minimum.  The device `min` overload set has no exact match for
+// 64-bit integers here and resolves to a double-precision one, which costs
+// a dozen f64 instructions per call.
+__device__ __forceinline__ int64_t min_i64(int64_t x, int64_t y) { return x < y ? x : y; }
+
 // ---------------------------------------------------------------------------
 // XCD-aware workgroup order.  Workgroups are handed to the 8 XCDs round
 // robin (workgroup w runs on XCD w % 8), and each XCD has its own L2.  The

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const int64_t n0 = int64_t(blockIdx.x) * 16 * RG;
     const uint16_t* wp[RG];
 #pragma unroll
-    for (int r = 0; r < RG; ++r) wp[r] = w + min(n0 + 16 * r + i16, n - 1) * ldb + grp * 8;
+    for (int r = 0; r < RG; ++r) wp[r] = w + min_i64(n0 + 16 * r + i16, n - 1) * ldb + grp * 8;
     const uint16_t* ap[MG];
     bool a_in[MG];
 #pragma unroll

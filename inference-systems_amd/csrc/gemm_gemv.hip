@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(
     int64_t n, int64_t k, int64_t ldb) {
     const int lane = threadIdx.x & 63;
     const int64_t row = int64_t(blockIdx.x) * kGemvRows + (threadIdx.x >> 6);
-    const uint16_t* wr = w + min(row, n - 1) * ldb;
+    const uint16_t* wr = w + min_i64(row, n - 1) * ldb;
     const int64_t chunks = k / 8;   // K % 8 == 0 is required by the selection table
 
     float acc = 0.0f;

@@ -4,8 +4,8 @@
 // This is the "staged" rung of the reference ladder
 // (cuda_kernels/gemm/src/gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
 // designed for CDNA4 instead of translated:
-//   * BM x BN macro tile per 256-thread workgroup (4 waves in a 2x2 grid),
-//     K-tiles of 64 elements;
+//   * 128 x 128 macro tile per 256-thread workgroup (4 waves in a 2x2
+//     grid, 64 x 64 each), K-tiles of 64 elements;
 //   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging) into a ring of STAGES tile buffers; tiles t+1 .. t+STAGES-1
 //     are in flight while tile t is multiplied, and each wave waits on its
@@ -44,6 +44,32 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const u32x4_t* p) {
+    typedef const __attribute__((address_space(3))) u32x4_t* lds_ptr;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)p));
+}
+
+// One global_load_lds_dwordx4: lane L copies 16 bytes from its `src` to LDS
+// bytes lds + 16 L .. lds + 16 L + 15 (lds must be wave-uniform).
+//
+// Written as inline assembly rather than __builtin_amdgcn_global_load_lds:
+// the compiler models that builtin as pending on both the vector-memory and
+// the LDS counters, so while a prefetch is in flight every wait it inserts
+// for a fragment ds_read becomes lgkmcnt(0), which drains the reads of the
+// next K-step too and serialises LDS reads with the MFMAs.  On gfx950 the
+// instruction completes on vmcnt alone (measured: lgkmcnt(0) after it does
+// not wait for the data), and the K loop waits on vmcnt explicitly before
+// the barrier that publishes a stage.  Nothing else in these kernels uses
+// M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES>
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
@@ -77,6 +103,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const int half = lane >> 5;
     const int r32 = lane & 31;
 
+    // The epilogue's arguments are loaded now.  A scalar load still in flight
+    // inside the K loop shares the LDS counter with the fragment reads and
+    // completes out of order, which would turn every fragment wait into
+    // lgkmcnt(0).
+    asm volatile("" :: "s"(c), "s"(ldc), "s"(c_vec), "s"(m), "s"(n));
+
     int tm, tn;
     grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const int64_t m0 = int64_t(tm) * BM;
@@ -93,23 +125,32 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         const int chunk = (lane & 7) ^ lds_swizzle(row);
         koff[j] = chunk * 8;
         if (row < BM) {
-            src[j] = a + min(m0 + row, m - 1) * lda + koff[j];
+            src[j] = a + min_i64(m0 + row, m - 1) * lda + koff[j];
         } else {
-            src[j] = w + min(n0 + (row - BM), n - 1) * ldb + koff[j];
+            src[j] = w + min_i64(n0 + (row - BM), n - 1) * ldb + koff[j];
         }
     }
 
-    const int64_t ktiles = (k + kBK - 1) / kBK;
-    auto issue = [&](int64_t t) {
-        const int64_t k0 = t * kBK;
-        const bool full = k0 + kBK <= k;
-        u32x4_t* stage = ring + (t % STAGES) * STAGE_CHUNKS;
+    // K-tiles are counted in 32 bits (the launcher checks k < 2^31), and the
+    // ring stage of a tile advances without a division.
+    const int ktiles = static_cast<int>((k + kBK - 1) / kBK);
+    const uint32_t ring_lds = lds_address(ring);
+    // Address of the zero chunk, held in registers for the whole kernel (in
+    // position-independent code it is otherwise reloaded from the GOT by a
+    // scalar load at every use).
+    const void* zero = &g_zero_chunk;
+    asm volatile("" : "+s"(zero));
+    auto issue = [&](int t, int stage) {
+        const int64_t k0 = int64_t(t) * kBK;
+        const uint32_t dst = ring_lds + uint32_t(stage * STAGE_CHUNKS + 64 * wave * IPW) * 16u;
+        if (k0 + kBK <= k) {
 #pragma unroll
-        for (int j = 0; j < IPW; ++j) {
-            const void* p = (full || k0 + koff[j] < k) ? static_cast<const void*>(src[j] + k0)
-                                                       : static_cast<const void*>(&g_zero_chunk);
-            __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*)(stage + 64 * (wave * IPW + j)),
-                                             16, 0, 0);
+            for (int j = 0; j < IPW; ++j) dma16(src[j] + k0, dst + 1024u * j);
+        } else {
+            // The last K-tile of a K that is not a multiple of 64.
+#pragma unroll
+            for (int j = 0; j < IPW; ++j)
+                dma16(k0 + koff[j] < k ? static_cast<const void*>(src[j] + k0) : zero, dst + 1024u * j);
         }
     };
 
@@ -143,38 +184,49 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     };
     // Wait until tile u has landed in every wave's part of its stage (each
     // wave waits on its own vmcnt, the barrier covers the others), then
-    // refill the stage the previous tile used with tile u + AHEAD.
-    auto tile_ready = [&](int64_t u) {
-        const int64_t later = min<int64_t>(ktiles - 1 - u, AHEAD - 1);
-        if (later >= 2) wait_vmcnt<2 * IPW>();
-        else if (later == 1) wait_vmcnt<IPW>();
-        else wait_vmcnt<0>();
+    // refill `free_stage`, the stage the previous tile used, with tile
+    // u + AHEAD.
+    auto tile_ready = [&](int u, int free_stage) {
+        const int later = ktiles - 1 - u;   // tiles already issued after u, capped at AHEAD - 1
+        if constexpr (AHEAD >= 3) {
+            if (later >= 2) wait_vmcnt<2 * IPW>();
+            else if (later == 1) wait_vmcnt<IPW>();
+            else wait_vmcnt<0>();
+        } else if constexpr (AHEAD == 2) {
+            if (later >= 1) wait_vmcnt<IPW>();
+            else wait_vmcnt<0>();
+        } else {
+            wait_vmcnt<0>();
+        }
         // Every ds_read of the previous tile has returned before the barrier,
         // so the stage refilled below is free in every wave.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (u + AHEAD < ktiles) issue(u + AHEAD);
+        if (u + AHEAD < ktiles) issue(u + AHEAD, free_stage);
     };
 
 #pragma unroll
     for (int t = 0; t < AHEAD; ++t)
-        if (t < ktiles) issue(t);
-    tile_ready(0);
+        if (t < ktiles) issue(t, t);
+    tile_ready(0, STAGES - 1);
     read_frags(ring, 0, af0, wf0);
 
-    for (int64_t t = 0; t < ktiles; ++t) {
-        const u32x4_t* tile = ring + (t % STAGES) * STAGE_CHUNKS;
+    int cur = 0;   // ring stage of tile t
+    for (int t = 0; t < ktiles; ++t) {
+        const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
         read_frags(tile, 1, af1, wf1);
         mfmas(af0, wf0);
         read_frags(tile, 2, af0, wf0);
         mfmas(af1, wf1);
         read_frags(tile, 3, af1, wf1);
         mfmas(af0, wf0);
+        const int next = cur + 1 == STAGES ? 0 : cur + 1;
         if (t + 1 < ktiles) {
-            tile_ready(t + 1);
-            read_frags(ring + ((t + 1) % STAGES) * STAGE_CHUNKS, 0, af0, wf0);
+            tile_ready(t + 1, cur);
+            read_frags(ring + next * STAGE_CHUNKS, 0, af0, wf0);
         }
+        cur = next;
         mfmas(af1, wf1);
     }
 
@@ -232,7 +284,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         if (c_vec && gcol + EPC <= n) {
             *reinterpret_cast<u32x4_t*>(gdst) = val;
         } else {
-            const int valid = int(min<int64_t>(EPC, n - gcol));
+            const int valid = int(min_i64(EPC, n - gcol));
             if constexpr (OB == 4) {
                 for (int e = 0; e < valid; ++e) reinterpret_cast<uint32_t*>(gdst)[e] = val[e];
             } else {
@@ -243,26 +295,26 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     }
 }
 
-// Tile configuration for a problem.  Measured on MI355X (2048 x 4096 x
-// 1024 bf16): a 128 x 128 tile with 4 waves and a 2-deep LDS ring (64 KiB)
-// lets two workgroups share a CU, and the two run out of phase, so one's
-// MFMAs overlap the other's loads; 128 x 256 with 8 waves covers shapes
-// with too few 128 x 128 tiles to fill the CUs twice over.
-struct TileChoice {
-    int bm, bn, waves;
-};
+// Ring depth for a problem.  Measured on MI355X with 128 x 128 tiles and
+// 4 waves: when the grid has more tiles than CUs, a 2-deep ring (64 KiB)
+// lets two workgroups share a CU and run out of phase, so one's MFMAs
+// overlap the other's loads (bf16 2048 x 4096 x 1024, 512 tiles: 19-20 us,
+// against 24 us with a 3-deep ring at one workgroup per CU).  With at most
+// one tile per CU there is nothing to pair with, and a 3-deep ring (96 KiB)
+// keeps two K-tiles in flight instead (4096 x 1024 x 3584, 256 tiles:
+// 34 us, against 39 us with the 2-deep ring).
+constexpr int64_t kCus = 256;
 
-TileChoice choose_tile(int64_t m, int64_t n) {
-    auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-    if (tiles(128, 128) >= 512) return {128, 128, 4};
-    if (tiles(128, 256) >= 256) return {128, 256, 8};
-    return {128, 128, 4};
+int choose_stages(int64_t m, int64_t n) {
+    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+    return tiles <= kCus ? 3 : 2;
 }
 
 template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES>
 int launch_tile(const Problem& p, hipStream_t s) {
     const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
     if (tiles_m * tiles_n > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "mfma_staged: grid too large");
+    if (p.k > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "mfma_staged: k must be below 2^31");
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n)), block(WGM * WGN * 64);
     const int out_bytes = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;
     // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
@@ -275,8 +327,7 @@ int launch_tile(const Problem& p, hipStream_t s) {
 
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
-    const TileChoice t = choose_tile(p.m, p.n);
-    if (t.bn == 256) return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 2>(p, s);
+    if (choose_stages(p.m, p.n) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3>(p, s);
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2>(p, s);
 }
 

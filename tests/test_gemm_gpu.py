@@ -172,6 +172,25 @@ def test_workload_parity(name, m):
     _check_tolerance(got, a, b, wl.b_layout, wl.dtype_out, rows=rows)
 
 
+@pytest.mark.parametrize("m,n", [(600, 1000), (2100, 4100)], ids=["40tiles", "561tiles"])
+@pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
+                         ids=["bf16", "f16-f32"])
+def test_staged_ring_depths_ragged(m, n, din, dout):
+    """mfma_staged keeps a 3-deep LDS ring when the 128 x 128 grid has at
+    most 256 tiles and a 2-deep one above that; both on ragged M and N and a
+    K that is not a multiple of the 64-wide K-tile (the last tile is padded
+    with zeros)."""
+    k = 1000
+    _say(f"staged ring M={m} N={n} K={k} {NAME[din]}->{NAME[dout]}")
+    gen = torch.Generator().manual_seed(m + n)
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_MFMA_STAGED, dout, L.B_NK)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 48).astype(int), np.arange(m - 16, m)]))
+    _check_tolerance(out.cpu(), a, w, L.B_NK, dout, rows=rows)
+
+
 # ---------------------------------------------------------------------------
 # Edge cases and API behaviour
 # ---------------------------------------------------------------------------
