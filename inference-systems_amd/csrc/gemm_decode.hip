@@ -2,10 +2,11 @@
 // with W[N,K] in the nn.Linear layout.  At these shapes the work is
 // streaming W once from HBM (N*K*2 bytes) while A (M*K*2 bytes, at most
 // 64 KiB) stays in L2.  Design:
-//   * one workgroup per 16 rows of W (4 waves; M <= 8) or per 32 rows (8
-//     waves; 8 < M <= 32, so each A fragment serves two W row groups); the
-//     waves split K, taking 32-element K-steps round robin, so together they
-//     read contiguous runs of each W row;
+//   * one workgroup per 16 rows of W (4 waves; M <= 8), per 32 rows (8
+//     waves; 8 < M <= 32, so each A fragment serves two W row groups) or,
+//     for very wide W, per 64 rows (4 waves); the waves split K, taking
+//     32-element K-steps round robin, so together they read contiguous runs
+//     of each W row;
 //   * each lane issues its W loads for several K-steps (8 x 16 B for K = 1024
 //     with 4 waves) before the first MFMA, so W is in flight almost at once;
 //   * v_mfma_f32_16x16x32 with W as the first operand (16 rows of W) and up
@@ -110,13 +111,28 @@ int launch_cfg(const Problem& p, hipStream_t s) {
     return check_launch("splitk_decode");
 }
 
-// Configurations measured on MI355X for N = 6144, K = 1024: up to 8 rows of A,
-// 16 W rows per 4-wave workgroup; beyond that 32 W rows per 8-wave workgroup,
-// which reads each A fragment once for two W row groups.
+// Configurations measured on MI355X, K = 1024.
+//   N = 6144: up to 8 rows of A, 16 W rows per 4-wave workgroup; beyond that
+//   32 W rows per 8-wave workgroup, which reads each A fragment once for two
+//   W row groups (M = 16: 5.9 us, M = 32: 7.2 us).
+//   N >= 65536 (LM head, 151936 rows): every workgroup reads all of A from
+//   L2, so for M > 1 a workgroup takes 64 W rows with 4 waves, which cuts
+//   that traffic 4x against 16 rows (M = 8 / 16 / 32: 61 / 66 / 76 us,
+//   against 64 / 70 / 81 us); M = 1 keeps the 16-row workgroups (51 us).
+constexpr int64_t kWideN = 65536;
+
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
-    if (p.m <= 8) return launch_cfg<DT, DT_OUT, 1, 1, 4, 8>(p, s);
-    if (p.m <= 16) return launch_cfg<DT, DT_OUT, 1, 2, 8, 2>(p, s);
+    const bool wide = p.n >= kWideN && p.m > 1;
+    if (p.m <= 8) {
+        if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4>(p, s);
+        return launch_cfg<DT, DT_OUT, 1, 1, 4, 8>(p, s);
+    }
+    if (p.m <= 16) {
+        if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4>(p, s);
+        return launch_cfg<DT, DT_OUT, 1, 2, 8, 2>(p, s);
+    }
+    if (wide) return launch_cfg<DT, DT_OUT, 2, 4, 4, 4>(p, s);
     return launch_cfg<DT, DT_OUT, 2, 2, 8, 2>(p, s);
 }
 

@@ -191,6 +191,21 @@ def test_staged_ring_depths_ragged(m, n, din, dout):
     _check_tolerance(out.cpu(), a, w, L.B_NK, dout, rows=rows)
 
 
+@pytest.mark.parametrize("m", [1, 5, 13, 29])
+def test_splitk_wide_n_ragged(m):
+    """splitk_decode takes 64 W rows per workgroup when N >= 65536 and M > 1
+    (16 rows for M = 1); a ragged N leaves the last workgroup partly past N
+    (clamped loads, masked stores)."""
+    n, k = 70001, 256
+    _say(f"splitk wide N={n} M={m} K={k}")
+    gen = torch.Generator().manual_seed(m)
+    a = torch.randn((m, k), generator=gen).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(torch.bfloat16)
+    out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_SPLITK_DECODE, torch.float32, L.B_NK)
+    torch.cuda.synchronize()
+    _check_tolerance(out.cpu(), a, w, L.B_NK, torch.float32)
+
+
 # ---------------------------------------------------------------------------
 # Edge cases and API behaviour
 # ---------------------------------------------------------------------------
