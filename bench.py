@@ -11,8 +11,10 @@ and timed with HIP events on the stream they run on.
 Alongside (extra keys of the same JSON line): the decode GEMMs M in
 {1,4,8,16,32} x N=6144 x K=1024 with W rotated over more than twice the
 256 MB Infinity Cache, the FP32 1024^3 GEMM, the FP16 down projection, the
-BF16 LM head, torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
-for comparison only, and the CPU baseline (host F.linear, multi-threaded).
+BF16 LM head, the merged gated-delta-net input projection (one N = 8224 GEMM
+against four launches), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the
+same inputs for comparison only, and the CPU baseline (host F.linear,
+multi-threaded).
 
 Prints ONE JSON line on stdout; a readable table goes to stderr.
 """
@@ -284,6 +286,36 @@ def main() -> int:
                     f"{gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)  [{ko}]")
                 del bs, a_o, b_o, o_o
         extras["other_workloads"] = other
+
+        # ----------------------- merged gated-delta-net input projection
+        # One N = 8224 GEMM (6144 + 2048 + 16 + 16 rows of W) against the four
+        # launches of gated_delta_net.py:192-195, W streamed from HBM.
+        g_gen = torch.Generator().manual_seed(1006)
+        g_rows = (6144, 2048, 16, 16)
+        g_w = (torch.randn(sum(g_rows), 1024, generator=g_gen) * 0.02).bfloat16().to(dev)
+        g_copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (g_w.numel() * 2)) + 1)
+        g_ws = [g_w] + [g_w.clone() for _ in range(g_copies - 1)]
+        g_rows_out = []
+        for gm in (1, 32):
+            g_a = torch.randn(gm, 1024, generator=g_gen).bfloat16().to(dev)
+            g_out = torch.empty(gm, sum(g_rows), dtype=torch.bfloat16, device=dev)
+            merged = [launcher(g_a, g_ws[i % g_copies], g_out, gm, sum(g_rows), 1024, L.B_NK, torch.bfloat16,
+                               torch.bfloat16) for i in range(g_copies * 2)]
+            g_parts = [torch.empty(gm, rows, dtype=torch.bfloat16, device=dev) for rows in g_rows]
+            separate = []
+            for i in range(g_copies * 2):
+                off = 0
+                for rows, part in zip(g_rows, g_parts):
+                    separate.append(launcher(g_a, g_ws[i % g_copies][off:off + rows], part, gm, rows, 1024,
+                                             L.B_NK, torch.bfloat16, torch.bfloat16))
+                    off += rows
+            t_one = median_graph_ms(torch, merged)
+            t_four = median_graph_ms(torch, separate) * len(g_rows)   # per step of four launches
+            g_rows_out.append({"m": gm, "merged_us": round(t_one * 1e3, 3), "four_launches_us": round(t_four * 1e3, 3),
+                               "speedup": round(t_four / t_one, 3)})
+            log(f"gdn input projection M={gm}: merged {t_one * 1e3:.2f} us, four launches {t_four * 1e3:.2f} us")
+        extras["gdn_input_projection_bf16_k1024"] = g_rows_out
+        del g_ws, g_w
 
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:

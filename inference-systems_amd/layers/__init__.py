@@ -1,4 +1,6 @@
-"""nano-vLLM layer mirrors whose matmul is the MI355X GEMM (see linear.py)."""
+"""nano-vLLM layer mirrors whose matmul is the MI355X GEMM (see linear.py and
+gdn_projection.py)."""
+from .gdn_projection import GdnInputProjection
 from .linear import (
     ColumnParallelLinear,
     GemmLinear,
@@ -12,6 +14,7 @@ from .linear import (
 
 __all__ = [
     "ColumnParallelLinear",
+    "GdnInputProjection",
     "GemmLinear",
     "LinearBase",
     "MergedColumnParallelLinear",

@@ -80,6 +80,33 @@ def test_gemm_linear_module():
     assert torch.equal(m(x), F.linear(x, m.weight, m.bias))
 
 
+def _gdn_weights(hidden=8, key_heads=2, value_heads=4, kdim=3, vdim=2, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    conv = 2 * key_heads * kdim + value_heads * vdim
+    return {"qkv": torch.randn(conv, hidden, generator=g), "z": torch.randn(value_heads * vdim, hidden, generator=g),
+            "b": torch.randn(value_heads, hidden, generator=g), "a": torch.randn(value_heads, hidden, generator=g)}
+
+
+@pytest.mark.parametrize("dims", [(8, 2, 4, 3, 2), (64, 4, 8, 16, 8)])
+def test_gdn_projection_matches_four_linears(dims):
+    """One GEMM over the merged weight gives the four projections of
+    gated_delta_net.py:192-195, in the order qkv, z, b, a."""
+    hidden, kh, vh, kd, vd = dims
+    full = _gdn_weights(hidden, kh, vh, kd, vd)
+    proj = Lyr.GdnInputProjection(hidden, kh, vh, kd, vd)
+    for sid, w in full.items():
+        proj.weight.weight_loader(proj.weight, w, sid)
+    assert proj.weight.shape == (2 * kh * kd + 2 * vh * vd + 2 * vh, hidden)
+    proj.gemm_backend = "auto"
+    x = torch.randn(5, hidden)
+    outs = proj(x)
+    assert [o.shape[-1] for o in outs] == [2 * kh * kd + vh * vd, vh * vd, vh, vh]
+    for out, sid in zip(outs, ("qkv", "z", "b", "a")):
+        torch.testing.assert_close(out, F.linear(x, full[sid]))
+    with pytest.raises(ValueError, match="shard id"):
+        proj.weight.weight_loader(proj.weight, full["z"], "v")
+
+
 def _tp_worker(rank, world, init_file, result_file):
     dist.init_process_group("gloo", init_method=f"file://{init_file}", rank=rank, world_size=world)
     try:
@@ -109,6 +136,23 @@ def _tp_worker(rank, world, init_file, result_file):
             ok = ok and torch.allclose(logits, F.linear(x, wh), rtol=1e-6, atol=1e-6)
         else:
             ok = ok and logits is None
+        # Merged GDN projection: the per-rank rows the reference's loaders
+        # pick (tests/test_qwen35_tp.py:39-55 with 2 key heads of 3 and 4
+        # value heads of 2: q, k, v each cut from its own third).
+        proj = Lyr.GdnInputProjection(8, 2, 4, 3, 2)
+        full_qkv = torch.arange(20 * 8, dtype=torch.float32).reshape(20, 8)
+        full_z = torch.arange(8 * 8, dtype=torch.float32).reshape(8, 8)
+        full_b = torch.arange(4 * 8, dtype=torch.float32).reshape(4, 8) * 2
+        full_a = torch.arange(4 * 8, dtype=torch.float32).reshape(4, 8) * 3
+        for sid, wt in (("qkv", full_qkv), ("z", full_z), ("b", full_b), ("a", full_a)):
+            proj.weight.weight_loader(proj.weight, wt, sid)
+        want = torch.cat((full_qkv[rank * 3:(rank + 1) * 3], full_qkv[6 + rank * 3:6 + (rank + 1) * 3],
+                          full_qkv[12 + rank * 4:12 + (rank + 1) * 4], full_z[rank * 4:(rank + 1) * 4],
+                          full_b[rank * 2:(rank + 1) * 2], full_a[rank * 2:(rank + 1) * 2]), dim=0)
+        ok = ok and proj.conv_dim == 10 and torch.equal(proj.weight.data, want)
+        proj.gemm_backend = "auto"
+        xg = torch.randn(3, 8)
+        ok = ok and torch.allclose(torch.cat(proj(xg), dim=-1), F.linear(xg, want), rtol=1e-6, atol=1e-5)
         with open(f"{result_file}.{rank}", "w") as fh:
             fh.write("ok" if ok else "mismatch")
     finally:

@@ -116,3 +116,36 @@ def test_mlp_block_graph_capture(m):
         layer.gemm_backend = "torch"
     ref = mlp(x).float()
     assert torch.allclose(eager.float(), ref, rtol=0.05, atol=0.02)
+
+
+@torch.inference_mode()
+@pytest.mark.parametrize("m", [1, 4, 32, 300])
+def test_gdn_merged_projection_bit_exact(m):
+    """Qwen3.5-0.8B gated-delta-net input projections (hidden 1024; 16 key
+    and 16 value heads of 128; N = 6144 + 2048 + 16 + 16 = 8224) as one GEMM:
+    every kernel's per-element arithmetic is independent of N, so the merged
+    launch must equal the four separate launches bit for bit, and the oracle
+    bound like any other GEMM."""
+    gen = torch.Generator().manual_seed(40 + m)
+    proj = Lyr.GdnInputProjection(1024, 16, 16, 128, 128)
+    parts = {sid: torch.randn(rows, 1024, generator=gen) * 0.02
+             for sid, rows in (("qkv", 6144), ("z", 2048), ("b", 16), ("a", 16))}
+    for sid, w in parts.items():
+        proj.weight.weight_loader(proj.weight, w, sid)
+    proj = proj.to(DEV, torch.bfloat16)
+    proj.gemm_backend = "hip"
+    x = torch.randn(m, 1024, generator=gen).bfloat16()
+    print(f"gdn merged projection M={m}", flush=True)
+    merged = proj(x.to(DEV))
+    torch.cuda.synchronize()
+    for out, sid in zip(merged, ("qkv", "z", "b", "a")):
+        w = parts[sid].bfloat16()
+        single = G.gemm(x.to(DEV), w.to(DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(out, single), sid
+    got = torch.cat(merged, dim=-1).cpu()
+    wall = torch.cat([parts[s].bfloat16() for s in ("qkv", "z", "b", "a")], dim=0)
+    a64, w64 = x.double().numpy(), wall.double().numpy()
+    r = orc.gemm_f64(a64, w64, "nk")
+    tol = orc.gemm_tolerance(r, orc.abs_products_f64(a64, w64, "nk"), 1024, "bf16")
+    assert (np.abs(got.double().numpy() - r) <= tol).all()
