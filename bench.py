@@ -317,6 +317,49 @@ def main() -> int:
         extras["gdn_input_projection_bf16_k1024"] = g_rows_out
         del g_ws, g_w
 
+        # --------------- fused MLP gate/up projection + SiLU-and-mul
+        # One launch of the fused kernel against the reference's composition
+        # (gate_up GEMM writing [M, 7168], then F.silu(gate) * up on the GPU).
+        F_ = torch.nn.functional
+        inter = 3584
+        s_gen = torch.Generator().manual_seed(1007)
+        s_w = (torch.randn(2 * inter, 1024, generator=s_gen) * 0.02).bfloat16().to(dev)
+        s_rows = []
+        for sm in (1, 32, 2048):
+            s_copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (s_w.numel() * 2)) + 1) if sm <= 32 else 1
+            s_ws = [s_w] + [s_w.clone() for _ in range(s_copies - 1)]
+            s_a = torch.randn(sm, 1024, generator=s_gen).bfloat16().to(dev)
+            s_out = torch.empty(sm, inter, dtype=torch.bfloat16, device=dev)
+            s_gu = torch.empty(sm, 2 * inter, dtype=torch.bfloat16, device=dev)
+
+            def fused(wt, s_a=s_a, s_out=s_out, sm=sm):
+                args_ = (s_a.data_ptr(), wt.data_ptr(), s_out.data_ptr(), sm, inter, 1024, 1024, 1024, inter,
+                         L.BF16, L.BF16)
+
+                def f():
+                    L.silu_mul_raw(*args_, torch.cuda.current_stream().cuda_stream)
+                return f
+
+            def unfused(wt, s_a=s_a, s_gu=s_gu, sm=sm):
+                gemm = launcher(s_a, wt, s_gu, sm, 2 * inter, 1024, L.B_NK, torch.bfloat16, torch.bfloat16)
+
+                def f():
+                    gemm()
+                    gate, up = s_gu.chunk(2, -1)
+                    F_.silu(gate) * up
+                return f
+            reps = s_copies * 4 if sm <= 32 else 40
+            t_f = median_graph_ms(torch, [fused(s_ws[i % s_copies]) for i in range(reps)])
+            t_u = median_graph_ms(torch, [unfused(s_ws[i % s_copies]) for i in range(reps)])
+            kf = L.kernel_name(L.silu_mul_select(sm, inter, 1024, 1024, 1024, inter, L.BF16, L.BF16, True))
+            s_rows.append({"m": sm, "fused_us": round(t_f * 1e3, 3), "unfused_us": round(t_u * 1e3, 3),
+                           "speedup": round(t_u / t_f, 3), "kernel": kf})
+            log(f"mlp gate_up+SiLU-and-mul M={sm}: fused {t_f * 1e3:.2f} us ({kf}), "
+                f"GEMM + torch SiluAndMul {t_u * 1e3:.2f} us")
+            del s_ws
+        extras["mlp_gate_up_silu_mul_bf16_n3584_k1024"] = s_rows
+        del s_w
+
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:
         F = torch.nn.functional

@@ -137,6 +137,43 @@ int nanovllm_gemm_kernel_supports(int kernel_id,
                                   int b_layout, int dtype_in, int dtype_out,
                                   int aligned16);
 
+/*
+ * Fused gate/up projection and SiLU-and-mul of the Qwen3.5 MLP:
+ *
+ *     c[m, j] = silu(sum_k a[m,k] w[j,k]) * sum_k a[m,k] w[n + j, k],  j < n
+ *
+ * with w = [W_gate; W_up], 2n rows in the W[N,K] layout (the weight of the
+ * MergedColumnParallelLinear gate_up_proj, nanovllm/layers/linear.py:76-97)
+ * and silu(x) = x / (1 + e^-x).  Both sums accumulate in fp32; silu and the
+ * product are evaluated in fp32 and rounded once to dtype_out (f16->{f16,f32},
+ * bf16->{bf16,f32}).  Replaces gate_up_proj followed by SiluAndMul
+ * (nanovllm/models/qwen3_5.py:117, nanovllm/layers/activation.py:8-11),
+ * which writes and re-reads the [m, 2n] projection.  Needs the vector path
+ * (16-byte aligned a and w, k, lda and ldw multiples of 8); otherwise
+ * NANOVLLM_GEMM_EUNSUPPORTED.  Asynchronous, no allocation, capturable.
+ */
+int nanovllm_gemm_silu_mul(const void* a, const void* w, void* c,
+                           int64_t m, int64_t n, int64_t k,
+                           int64_t lda, int64_t ldw, int64_t ldc,
+                           int dtype_in, int dtype_out,
+                           void* stream);
+
+/* The fused problem forced onto one kernel (mfma_staged, splitk_decode for
+ * m <= 32, gemv_decode for m == 1), as nanovllm_gemm_with_kernel does for
+ * the plain GEMM (gemm_bench.cu:396-416 pattern). */
+int nanovllm_gemm_silu_mul_with_kernel(int kernel_id,
+                                       const void* a, const void* w, void* c,
+                                       int64_t m, int64_t n, int64_t k,
+                                       int64_t lda, int64_t ldw, int64_t ldc,
+                                       int dtype_in, int dtype_out,
+                                       void* stream);
+
+/* Kernel id nanovllm_gemm_silu_mul() would launch (or a negative code).
+ * Pure host function, like nanovllm_gemm_select (gemm_bench.cu:252-273). */
+int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k,
+                                  int64_t lda, int64_t ldw, int64_t ldc,
+                                  int dtype_in, int dtype_out, int aligned16);
+
 /* Stable name of a kernel id ("fp32_tiled", "mfma_staged", ...), or
  * "unknown".  Mirrors path_name (gemm_bench.cu:275-282). */
 const char* nanovllm_gemm_kernel_name(int kernel_id);

@@ -40,6 +40,10 @@ SIGNATURES = {
                                          _VP]),
     "nanovllm_gemm_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT]),
     "nanovllm_gemm_kernel_supports": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT]),
+    "nanovllm_gemm_silu_mul": (_INT, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _VP]),
+    "nanovllm_gemm_silu_mul_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT,
+                                                  _INT, _VP]),
+    "nanovllm_gemm_silu_mul_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT]),
     "nanovllm_gemm_kernel_name": (ctypes.c_char_p, [_INT]),
     "nanovllm_gemm_last_error": (ctypes.c_char_p, []),
     "nanovllm_gemm_version": (_INT, []),
@@ -114,6 +118,23 @@ def select(m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, aligned16=True
 def kernel_supports(kernel_id, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, aligned16=True) -> bool:
     return bool(load().nanovllm_gemm_kernel_supports(kernel_id, m, n, k, lda, ldb, ldc, b_layout, dtype_in,
                                                      dtype_out, int(bool(aligned16))))
+
+
+def silu_mul_select(m, n, k, lda, ldw, ldc, dtype_in, dtype_out, aligned16=True) -> int:
+    """Kernel id of the fused gate/up + SiLU-and-mul (negative code if invalid)."""
+    return load().nanovllm_gemm_silu_mul_select(m, n, k, lda, ldw, ldc, dtype_in, dtype_out, int(bool(aligned16)))
+
+
+def silu_mul_raw(a_ptr, w_ptr, c_ptr, m, n, k, lda, ldw, ldc, dtype_in, dtype_out, stream,
+                 kernel: int | None = None) -> None:
+    """Enqueue one fused gate/up + SiLU-and-mul on `stream`; raise on error."""
+    lib = load()
+    if kernel is None:
+        rc = lib.nanovllm_gemm_silu_mul(a_ptr, w_ptr, c_ptr, m, n, k, lda, ldw, ldc, dtype_in, dtype_out, stream)
+    else:
+        rc = lib.nanovllm_gemm_silu_mul_with_kernel(kernel, a_ptr, w_ptr, c_ptr, m, n, k, lda, ldw, ldc, dtype_in,
+                                                    dtype_out, stream)
+    check(rc, "nanovllm_gemm_silu_mul")
 
 
 def gemm_raw(a_ptr, b_ptr, c_ptr, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, stream,

@@ -133,6 +133,74 @@ int gemm_entry(int forced_kernel, const void* a, const void* b, void* c, int64_t
     return run(kernel, p, static_cast<hipStream_t>(stream));
 }
 
+// ---------------------------------------------------------------------------
+// Fused gate/up projection + SiLU-and-mul: c[M, n] from W = [W_gate; W_up]
+// of 2n rows in the W[N,K] layout.  Runs on the vector-path kernels only.
+// ---------------------------------------------------------------------------
+int validate_silu_mul(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int64_t ldc, int din, int dout) {
+    if (din < NANOVLLM_GEMM_F32 || din > NANOVLLM_GEMM_BF16 || dout < NANOVLLM_GEMM_F32 || dout > NANOVLLM_GEMM_BF16)
+        return set_error(NANOVLLM_GEMM_EINVAL, "unknown dtype code (in %d, out %d)", din, dout);
+    if (!is_half(din) || !dtype_pair_ok(din, dout))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "unsupported dtype pair for silu_mul (in %d, out %d): supported are f16->{f16,f32}, "
+                         "bf16->{bf16,f32}",
+                         din, dout);
+    if (m < 0 || n < 0) return set_error(NANOVLLM_GEMM_EINVAL, "m and n must be non-negative (m=%lld, n=%lld)",
+                                         (long long)m, (long long)n);
+    if (k < 1) return set_error(NANOVLLM_GEMM_EINVAL, "k must be positive (k=%lld)", (long long)k);
+    if (lda < k) return set_error(NANOVLLM_GEMM_EINVAL, "lda (%lld) must be >= k (%lld)", (long long)lda, (long long)k);
+    if (ldw < k) return set_error(NANOVLLM_GEMM_EINVAL, "ldw (%lld) must be >= k (%lld)", (long long)ldw, (long long)k);
+    if (ldc < n || ldc < 1)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldc (%lld) must be >= n (%lld)", (long long)ldc, (long long)n);
+    return NANOVLLM_GEMM_OK;
+}
+
+bool supports_silu_mul(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldw, int aligned16) {
+    if (!vector_ok(k, lda, ldw, NANOVLLM_GEMM_B_NK, aligned16)) return false;
+    switch (kernel_id) {
+        case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return true;
+        case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return m <= kDecodeMaxM;
+        case NANOVLLM_GEMM_KERNEL_GEMV_DECODE: return m == 1;
+        default: return false;
+    }
+}
+
+// Same regimes as select(): the fused epilogue does not change what bounds
+// each shape.
+int select_silu_mul(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int aligned16) {
+    if (!vector_ok(k, lda, ldw, NANOVLLM_GEMM_B_NK, aligned16))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "silu_mul needs 16-byte aligned a and w with k, lda and ldw multiples of 8 "
+                         "(k=%lld lda=%lld ldw=%lld)",
+                         (long long)k, (long long)lda, (long long)ldw);
+    if (m == 1 && 2 * n * k * 2 <= kGemvMaxWBytes) return NANOVLLM_GEMM_KERNEL_GEMV_DECODE;
+    if (m <= kDecodeMaxM) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+    return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
+}
+
+int silu_mul_entry(int forced_kernel, const void* a, const void* w, void* c, int64_t m, int64_t n, int64_t k,
+                   int64_t lda, int64_t ldw, int64_t ldc, int din, int dout, void* stream) {
+    g_last_error.clear();
+    int rc = validate_silu_mul(m, n, k, lda, ldw, ldc, din, dout);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m == 0 || n == 0) return NANOVLLM_GEMM_OK;
+    if (a == nullptr || w == nullptr || c == nullptr)
+        return set_error(NANOVLLM_GEMM_EINVAL, "a, w and c must be non-null device pointers");
+    const int al = aligned16_of(a, w);
+    int kernel = forced_kernel;
+    if (kernel < 0) {
+        kernel = select_silu_mul(m, n, k, lda, ldw, al);
+        if (kernel < 0) return kernel;
+    } else if (!supports_silu_mul(kernel, m, k, lda, ldw, al)) {
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "kernel %s cannot run silu_mul for this problem (m=%lld n=%lld k=%lld)",
+                         nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);
+    }
+    Problem p{a, w, c, m, n, k, lda, ldw, ldc, NANOVLLM_GEMM_B_NK, din, dout};
+    p.epi = EPI_SILU_MUL;
+    return run(kernel, p, static_cast<hipStream_t>(stream));
+}
+
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -197,8 +265,31 @@ const char* nanovllm_gemm_kernel_name(int kernel_id) {
     }
 }
 
+int nanovllm_gemm_silu_mul(const void* a, const void* w, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                           int64_t ldw, int64_t ldc, int dtype_in, int dtype_out, void* stream) {
+    return nvg::silu_mul_entry(-1, a, w, c, m, n, k, lda, ldw, ldc, dtype_in, dtype_out, stream);
+}
+
+int nanovllm_gemm_silu_mul_with_kernel(int kernel_id, const void* a, const void* w, void* c, int64_t m, int64_t n,
+                                       int64_t k, int64_t lda, int64_t ldw, int64_t ldc, int dtype_in, int dtype_out,
+                                       void* stream) {
+    if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
+        nvg::g_last_error.clear();
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+    return nvg::silu_mul_entry(kernel_id, a, w, c, m, n, k, lda, ldw, ldc, dtype_in, dtype_out, stream);
+}
+
+int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int64_t ldc,
+                                  int dtype_in, int dtype_out, int aligned16) {
+    nvg::g_last_error.clear();
+    const int rc = nvg::validate_silu_mul(m, n, k, lda, ldw, ldc, dtype_in, dtype_out);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    return nvg::select_silu_mul(m, n, k, lda, ldw, aligned16);
+}
+
 const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
 
-int nanovllm_gemm_version(void) { return (1 << 16) | 0; }
+int nanovllm_gemm_version(void) { return (1 << 16) | 1; }
 
 }  // extern "C"

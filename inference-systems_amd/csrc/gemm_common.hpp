@@ -17,6 +17,13 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
+// Output epilogues.  EPI_NONE stores the product.  EPI_SILU_MUL is the fused
+// SiluAndMul of a gate/up projection: W = [W_gate; W_up] has 2n rows, output
+// column j is silu(a . W_gate[j]) * (a . W_up[j]), computed in fp32 from the
+// fp32 accumulators and rounded once.
+constexpr int EPI_NONE = 0;
+constexpr int EPI_SILU_MUL = 1;
+
 // One GEMM problem as it crosses the C ABI (see include/nanovllm_gemm.h).
 struct Problem {
     const void* a;
@@ -27,6 +34,7 @@ struct Problem {
     int b_layout;
     int dtype_in;
     int dtype_out;
+    int epi = EPI_NONE;   // EPI_SILU_MUL: n output columns from 2n rows of b
 };
 
 constexpr int kWave = 64;
@@ -112,6 +120,12 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c
 // 16-byte global load.
 __device__ __forceinline__ u32x4_t load16(const void* p) {
     return *static_cast<const u32x4_t*>(p);
+}
+
+// x * sigmoid(x) = x / (1 + e^-x) in fp32 (library exp, IEEE divide; -0 for
+// very negative x, where e^-x overflows to infinity).
+__device__ __forceinline__ float silu_f32(float x) {
+    return x / (1.0f + expf(-x));
 }
 
 // Integer minimum.  The device `min` overload set has no exact match for

@@ -24,7 +24,7 @@ constexpr int kDecStep = 32;   // K elements per MFMA
 
 // RG groups of 16 W rows per workgroup, WAVES waves splitting K round robin,
 // MG groups of 16 A rows, UNROLL K-steps whose loads are issued together.
-template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL>
+template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc) {
@@ -35,10 +35,19 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const int i16 = lane & 15;   // W row (first operand) / A row (second operand)
     const int grp = lane >> 4;   // which 8-element chunk of the 32-wide K-step
 
-    const int64_t n0 = int64_t(blockIdx.x) * 16 * RG;
+    // EPI_SILU_MUL: W-row groups pair up, group 2s holding gate rows and
+    // group 2s + 1 the up rows of the same 16 output columns.
+    static_assert(EPI == EPI_NONE || RG % 2 == 0, "gate/up group pairs");
+    constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;   // 16-column output groups per workgroup
+    const int64_t n0 = int64_t(blockIdx.x) * 16 * OG;         // first output column
     const uint16_t* wp[RG];
 #pragma unroll
-    for (int r = 0; r < RG; ++r) wp[r] = w + min_i64(n0 + 16 * r + i16, n - 1) * ldb + grp * 8;
+    for (int r = 0; r < RG; ++r) {
+        if constexpr (EPI == EPI_SILU_MUL)
+            wp[r] = w + ((r & 1) ? n : 0) * ldb + min_i64(n0 + 16 * (r >> 1) + i16, n - 1) * ldb + grp * 8;
+        else
+            wp[r] = w + min_i64(n0 + 16 * r + i16, n - 1) * ldb + grp * 8;
+    }
     const uint16_t* ap[MG];
     bool a_in[MG];
 #pragma unroll
@@ -86,26 +95,37 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     __syncthreads();
 
     // Sum the per-wave partials in wave order (deterministic) and store.
-    for (int e = threadIdx.x; e < RG * MG * 256; e += WAVES * 64) {
-        const int r = e / (MG * 256);
+    for (int e = threadIdx.x; e < OG * MG * 256; e += WAVES * 64) {
+        const int o = e / (MG * 256);
         const int g = (e / 256) % MG;
         const int nn = e & 15;
         const int mm = (e >> 4) & 15;
-        float sum = red[0][r][g][nn][mm];
-#pragma unroll
-        for (int wv = 1; wv < WAVES; ++wv) sum += red[wv][r][g][nn][mm];
         const int64_t row = g * 16 + mm;
-        const int64_t col = n0 + 16 * r + nn;
-        if (row < m && col < n) store_elem<DT_OUT>(c, row * ldc + col, sum);
+        const int64_t col = n0 + 16 * o + nn;
+        if constexpr (EPI == EPI_SILU_MUL) {
+            float gate = red[0][2 * o][g][nn][mm], up = red[0][2 * o + 1][g][nn][mm];
+#pragma unroll
+            for (int wv = 1; wv < WAVES; ++wv) {
+                gate += red[wv][2 * o][g][nn][mm];
+                up += red[wv][2 * o + 1][g][nn][mm];
+            }
+            if (row < m && col < n) store_elem<DT_OUT>(c, row * ldc + col, silu_f32(gate) * up);
+        } else {
+            float sum = red[0][o][g][nn][mm];
+#pragma unroll
+            for (int wv = 1; wv < WAVES; ++wv) sum += red[wv][o][g][nn][mm];
+            if (row < m && col < n) store_elem<DT_OUT>(c, row * ldc + col, sum);
+        }
     }
 }
 
-template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL>
+template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL, int EPI = EPI_NONE>
 int launch_cfg(const Problem& p, hipStream_t s) {
-    const int64_t blocks = (p.n + 16 * RG - 1) / (16 * RG);
+    constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;
+    const int64_t blocks = (p.n + 16 * OG - 1) / (16 * OG);
     if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
     const dim3 grid(static_cast<uint32_t>(blocks)), block(WAVES * 64);
-    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, MG, RG, WAVES, UNROLL>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, MG, RG, WAVES, UNROLL, EPI>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
                        p.lda, p.ldb, p.ldc);
     return check_launch("splitk_decode");
@@ -121,8 +141,22 @@ int launch_cfg(const Problem& p, hipStream_t s) {
 //   against 64 / 70 / 81 us); M = 1 keeps the 16-row workgroups (51 us).
 constexpr int64_t kWideN = 65536;
 
+// Fused gate/up + SiLU-and-mul: W-row groups come in gate/up pairs, so the
+// workgroups take 2 (or, for very wide W, 4) groups of 16 rows.
+template <int DT, int DT_OUT>
+int launch_silu_mul(const Problem& p, hipStream_t s) {
+    const bool wide = 2 * p.n >= kWideN;
+    if (p.m <= 16) {
+        if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4, EPI_SILU_MUL>(p, s);
+        return launch_cfg<DT, DT_OUT, 1, 2, 4, 4, EPI_SILU_MUL>(p, s);
+    }
+    if (wide) return launch_cfg<DT, DT_OUT, 2, 4, 4, 4, EPI_SILU_MUL>(p, s);
+    return launch_cfg<DT, DT_OUT, 2, 2, 8, 2, EPI_SILU_MUL>(p, s);
+}
+
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
+    if (p.epi == EPI_SILU_MUL) return launch_silu_mul<DT, DT_OUT>(p, s);
     const bool wide = p.n >= kWideN && p.m > 1;
     if (p.m <= 8) {
         if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4>(p, s);

@@ -27,33 +27,46 @@ __device__ __forceinline__ float dot8(u32x4_t av, u32x4_t wv, float s) {
     return s;
 }
 
-template <int DT, int DT_OUT>
+template <int DT, int DT_OUT, int EPI>
 __global__ __launch_bounds__(256) void gemv_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t n, int64_t k, int64_t ldb) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = int64_t(blockIdx.x) * kGemvRows + (threadIdx.x >> 6);
+    const int64_t row = int64_t(blockIdx.x) * kGemvRows + (threadIdx.x >> 6);   // output column
     const uint16_t* wr = w + min_i64(row, n - 1) * ldb;
+    // EPI_SILU_MUL: the wave also streams the up row of its column (row n + j
+    // of W = [W_gate; W_up]).
+    const uint16_t* wu = EPI == EPI_SILU_MUL ? w + (n + min_i64(row, n - 1)) * ldb : wr;
     const int64_t chunks = k / 8;   // K % 8 == 0 is required by the selection table
 
-    float acc = 0.0f;
+    float acc = 0.0f, acc_up = 0.0f;
     for (int64_t c0 = lane; c0 < chunks; c0 += 64 * kGemvUnroll) {
-        u32x4_t wv[kGemvUnroll], av[kGemvUnroll];
+        u32x4_t wv[kGemvUnroll], uv[kGemvUnroll], av[kGemvUnroll];
 #pragma unroll
         for (int u = 0; u < kGemvUnroll; ++u) {
             const int64_t cc = c0 + 64 * u;
             const bool in = cc < chunks;
             wv[u] = in ? load16(wr + cc * 8) : u32x4_t{0u, 0u, 0u, 0u};
+            if constexpr (EPI == EPI_SILU_MUL) uv[u] = in ? load16(wu + cc * 8) : u32x4_t{0u, 0u, 0u, 0u};
             av[u] = in ? load16(a + cc * 8) : u32x4_t{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; ++u) acc = dot8<DT>(av[u], wv[u], acc);
+        for (int u = 0; u < kGemvUnroll; ++u) {
+            acc = dot8<DT>(av[u], wv[u], acc);
+            if constexpr (EPI == EPI_SILU_MUL) acc_up = dot8<DT>(av[u], uv[u], acc_up);
+        }
     }
     // Butterfly over the wave in a fixed order: every lane ends with the
     // same, deterministic sum.
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0 && row < n) store_elem<DT_OUT>(c, row, acc);
+    for (int off = 32; off >= 1; off >>= 1) {
+        acc += __shfl_xor(acc, off);
+        if constexpr (EPI == EPI_SILU_MUL) acc_up += __shfl_xor(acc_up, off);
+    }
+    if (lane == 0 && row < n) {
+        if constexpr (EPI == EPI_SILU_MUL) store_elem<DT_OUT>(c, row, silu_f32(acc) * acc_up);
+        else store_elem<DT_OUT>(c, row, acc);
+    }
 }
 
 template <int DT, int DT_OUT>
@@ -61,8 +74,14 @@ int launch_typed(const Problem& p, hipStream_t s) {
     const int64_t blocks = (p.n + kGemvRows - 1) / kGemvRows;
     if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "gemv_decode: grid too large");
     const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
-    hipLaunchKernelGGL((gemv_decode_kernel<DT, DT_OUT>), grid, block, 0, s, static_cast<const uint16_t*>(p.a),
-                       static_cast<const uint16_t*>(p.b), p.c, p.n, p.k, p.ldb);
+    const auto* ap = static_cast<const uint16_t*>(p.a);
+    const auto* wp = static_cast<const uint16_t*>(p.b);
+    if (p.epi == EPI_SILU_MUL)
+        hipLaunchKernelGGL((gemv_decode_kernel<DT, DT_OUT, EPI_SILU_MUL>), grid, block, 0, s, ap, wp, p.c, p.n, p.k,
+                           p.ldb);
+    else
+        hipLaunchKernelGGL((gemv_decode_kernel<DT, DT_OUT, EPI_NONE>), grid, block, 0, s, ap, wp, p.c, p.n, p.k,
+                           p.ldb);
     return check_launch("gemv_decode");
 }
 

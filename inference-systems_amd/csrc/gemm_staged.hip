@@ -70,7 +70,7 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES>
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI>
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
@@ -86,10 +86,15 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int AHEAD = STAGES - 1;    // tiles in flight ahead of the one multiplied
     static_assert(IPW * 8 * NW == ROWS && WM % 32 == 0 && WN % 32 == 0, "tile shape");
     static_assert(AHEAD >= 1 && AHEAD <= 3 && AHEAD * IPW < 64, "vmcnt range");
+    // EPI_SILU_MUL: the W rows of a tile alternate 32 gate rows and the 32 up
+    // rows of the same output columns, so block pair (2i, 2i + 1) of a wave
+    // holds gate and up values of one 32-column group in the same lanes.
+    static_assert(EPI == EPI_NONE || NI % 2 == 0, "gate/up pairs per wave");
+    constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;   // output columns per tile
 
     // LDS: the ring of K-tile stages, reused after the K loop for the C tile.
     constexpr int OB = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;     // output bytes
-    constexpr int PITCH = BN * OB + 16;                          // C-tile row pitch in LDS
+    constexpr int PITCH = BNO * OB + 16;                         // C-tile row pitch in LDS
     constexpr int STAGE_CHUNKS = ROWS * kChunks;
     constexpr int RING_BYTES = STAGES * STAGE_CHUNKS * 16;
     constexpr int LDS_BYTES = RING_BYTES > BM * PITCH ? RING_BYTES : BM * PITCH;
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     int tm, tn;
     grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const int64_t m0 = int64_t(tm) * BM;
-    const int64_t n0 = int64_t(tn) * BN;
+    const int64_t n0 = int64_t(tn) * BNO;   // first output column
 
     // DMA instruction j of this wave fills LDS rows 8 i .. 8 i + 7 of a stage,
     // i = wave * IPW + j; lane L writes row 8 i + L / 8, position L % 8, which
@@ -126,6 +131,10 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         koff[j] = chunk * 8;
         if (row < BM) {
             src[j] = a + min_i64(m0 + row, m - 1) * lda + koff[j];
+        } else if constexpr (EPI == EPI_SILU_MUL) {
+            const int wr = row - BM;
+            const int64_t col = n0 + 32 * (wr >> 6) + (wr & 31);     // output column of this row
+            src[j] = w + (((wr >> 5) & 1) ? n : 0) * ldb + min_i64(col, n - 1) * ldb + koff[j];
         } else {
             src[j] = w + min_i64(n0 + (row - BM), n - 1) * ldb + koff[j];
         }
@@ -237,20 +246,31 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // the 32 rows one store instruction touches spread over the banks), then
     // all 256 threads copy the tile out row by row, 16 bytes per lane, so
     // every global store instruction writes whole 512-byte row segments.
-    constexpr int CPR = BN * OB / 16;                            // 16-byte chunks per row
+    constexpr int CPR = BNO * OB / 16;                           // 16-byte chunks per row
     static_assert(NT % CPR == 0, "rows per copy pass");
     char* ctile = reinterpret_cast<char*>(ring);
     __syncthreads();   // every wave is done reading the last K-tile
+    constexpr int NIO = EPI == EPI_SILU_MUL ? NI / 2 : NI;     // 32-column output groups per wave
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
         const int row = wm * WM + 32 * j + r32;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
+        for (int i = 0; i < NIO; ++i) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int col = wn * WN + 32 * i + 8 * q + 4 * half;
-                const f32x16_t& v = acc[i][j];
-                const float x0 = v[4 * q], x1 = v[4 * q + 1], x2 = v[4 * q + 2], x3 = v[4 * q + 3];
+                const int col = wn * (NIO * 32) + 32 * i + 8 * q + 4 * half;
+                float x0, x1, x2, x3;
+                if constexpr (EPI == EPI_SILU_MUL) {
+                    const f32x16_t& g = acc[2 * i][j];
+                    const f32x16_t& u = acc[2 * i + 1][j];
+                    x0 = silu_f32(g[4 * q]) * u[4 * q];
+                    x1 = silu_f32(g[4 * q + 1]) * u[4 * q + 1];
+                    x2 = silu_f32(g[4 * q + 2]) * u[4 * q + 2];
+                    x3 = silu_f32(g[4 * q + 3]) * u[4 * q + 3];
+                } else {
+                    const f32x16_t& v = acc[i][j];
+                    x0 = v[4 * q]; x1 = v[4 * q + 1]; x2 = v[4 * q + 2]; x3 = v[4 * q + 3];
+                }
                 char* dst = ctile + row * PITCH + col * OB;
                 if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
                     *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{x0, x1, x2, x3};
@@ -264,7 +284,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int EPC = 16 / OB;                 // output elements per chunk
     constexpr int ROWS_PER_PASS = NT / CPR;
     const int chunk = tid % CPR;
-    if (c_vec && m0 + BM <= m && n0 + BN <= n) {
+    if (c_vec && m0 + BM <= m && n0 + BNO <= n) {
         // Interior tile (uniform branch): whole 16-byte chunks, no masks.
         static_assert(BM % ROWS_PER_PASS == 0, "copy passes");
 #pragma unroll
@@ -310,25 +330,34 @@ int choose_stages(int64_t m, int64_t n) {
     return tiles <= kCus ? 3 : 2;
 }
 
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES>
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI>
 int launch_tile(const Problem& p, hipStream_t s) {
-    const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
+    constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;
+    const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BNO - 1) / BNO;
     if (tiles_m * tiles_n > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "mfma_staged: grid too large");
     if (p.k > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "mfma_staged: k must be below 2^31");
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n)), block(WGM * WGN * 64);
     const int out_bytes = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;
     // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
     const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && ((p.ldc * out_bytes) % 16 == 0);
-    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES>), grid, block, 0, s,
+    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c,
                        p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec);
     return check_launch("mfma_staged");
 }
 
+template <int DT, int DT_OUT, int EPI>
+int launch_epi(const Problem& p, hipStream_t s) {
+    // A fused gate/up tile covers 64 output columns from 128 W rows.
+    const int64_t n_tiles = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
+    if (choose_stages(p.m, n_tiles) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI>(p, s);
+    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI>(p, s);
+}
+
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
-    if (choose_stages(p.m, p.n) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3>(p, s);
-    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2>(p, s);
+    if (p.epi == EPI_SILU_MUL) return launch_epi<DT, DT_OUT, EPI_SILU_MUL>(p, s);
+    return launch_epi<DT, DT_OUT, EPI_NONE>(p, s);
 }
 
 }  // namespace

@@ -158,6 +158,86 @@ def selected_kernel(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.
     return _lib.kernel_name(kid)
 
 
+# ---------------------------------------------------------------------------
+# Fused gate/up projection + SiLU-and-mul
+# ---------------------------------------------------------------------------
+def silu_mul_contract_reason(a: torch.Tensor, w: torch.Tensor,
+                             out_dtype: Optional[torch.dtype] = None) -> Optional[str]:
+    """Why the fused op cannot take these inputs, or None if it can: the
+    GEMM contract, half-precision inputs, an even number of W rows (gate
+    rows, then as many up rows) and rows readable as aligned 16-byte chunks."""
+    reason = contract_reason(a, w, out_dtype)
+    if reason is not None:
+        return reason
+    if a.dtype not in (torch.float16, torch.bfloat16):
+        return "the fused SiLU-and-mul takes float16 or bfloat16 inputs"
+    if w.shape[0] % 2:
+        return f"w must hold gate and up halves of equal height (got {w.shape[0]} rows)"
+    if a.shape[-1] % 8:
+        return f"K ({a.shape[-1]}) must be a multiple of 8 for the fused SiLU-and-mul"
+    if a.data_ptr() % 16 or w.data_ptr() % 16:
+        return "a and w must be 16-byte aligned for the fused SiLU-and-mul"
+    return None
+
+
+def _launch_silu_mul(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype],
+                     kernel: Optional[int] = None) -> torch.Tensor:
+    reason = silu_mul_contract_reason(a, w, out_dtype)
+    if reason is not None:
+        raise RuntimeError(f"nanovllm::gemm_silu_mul: {reason}")
+    out_dtype = a.dtype if out_dtype is None else out_dtype
+    k = a.shape[-1]
+    n = w.shape[0] // 2
+    m = a.numel() // k
+    out = torch.empty((*a.shape[:-1], n), dtype=out_dtype, device=a.device)
+    if m == 0 or n == 0:
+        return out
+    with torch.cuda.device(a.device):
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+        _lib.silu_mul_raw(a.data_ptr(), w.data_ptr(), out.data_ptr(), m, n, k, k, k, n, _CODE[a.dtype],
+                          _CODE[out_dtype], stream, kernel)
+    return out
+
+
+@torch.library.custom_op("nanovllm::gemm_silu_mul", mutates_args=())
+def _gemm_silu_mul_op(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    return _launch_silu_mul(a, w, out_dtype)
+
+
+@_gemm_silu_mul_op.register_fake
+def _gemm_silu_mul_fake(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    torch._check(w.dim() == 2)
+    torch._check(w.shape[0] % 2 == 0)
+    torch._check(a.shape[-1] == w.shape[1])
+    torch._check(a.dtype == w.dtype)
+    torch._check(a.device == w.device)
+    return a.new_empty((*a.shape[:-1], w.shape[0] // 2), dtype=a.dtype if out_dtype is None else out_dtype)
+
+
+def gemm_silu_mul(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """SiluAndMul(a @ w.T) in one launch: silu(a W_gate^T) * (a W_up^T) for
+    w = [W_gate; W_up] (the gate_up_proj weight)."""
+    return torch.ops.nanovllm.gemm_silu_mul(a, w, out_dtype)
+
+
+def gemm_silu_mul_with_kernel(a: torch.Tensor, w: torch.Tensor, kernel: int,
+                              out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """The fused op on one named kernel (raises if it cannot take the shape)."""
+    return _launch_silu_mul(a, w, out_dtype, kernel)
+
+
+def silu_mul_selected_kernel(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> str:
+    k = a.shape[-1]
+    n = w.shape[0] // 2
+    m = a.numel() // max(k, 1)
+    out_dtype = a.dtype if out_dtype is None else out_dtype
+    aligned = a.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0
+    kid = _lib.silu_mul_select(m, n, k, k, k, n, _CODE[a.dtype], _CODE[out_dtype], aligned)
+    if kid < 0:
+        raise RuntimeError(f"nanovllm::gemm_silu_mul: {_lib.last_error()}")
+    return _lib.kernel_name(kid)
+
+
 def validate_gemm_backend(backend: str) -> str:
     """Normalise a backend name (pattern of validate_gdn_decode_backend, gdn.py:13)."""
     value = str(backend).strip().lower()
@@ -195,3 +275,26 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     if bias is not None:
         y = y + bias.to(y.dtype)
     return y
+
+
+def _torch_silu_mul(x, weight):
+    """The reference composition: gate_up_proj then SiluAndMul
+    (nanovllm/models/qwen3_5.py:117, nanovllm/layers/activation.py:8-11)."""
+    gate, up = F.linear(x, weight).chunk(2, -1)
+    return F.silu(gate) * up
+
+
+def silu_mul_linear(x: torch.Tensor, weight: torch.Tensor, *, backend: Optional[str] = None) -> torch.Tensor:
+    """SiluAndMul(F.linear(x, weight)) with the backend switch of ``linear``:
+    ``torch`` runs the reference composition, ``hip`` the fused op (inputs
+    outside its contract raise), ``auto`` the fused op when the inputs
+    satisfy its contract and the composition otherwise."""
+    backend = validate_gemm_backend(backend) if backend is not None else default_backend()
+    if backend == "torch":
+        return _torch_silu_mul(x, weight)
+    reason = silu_mul_contract_reason(x, weight)
+    if reason is not None:
+        if backend == "auto":
+            return _torch_silu_mul(x, weight)
+        raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
+    return gemm_silu_mul(x, weight)

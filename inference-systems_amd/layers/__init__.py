@@ -1,5 +1,5 @@
-"""nano-vLLM layer mirrors whose matmul is the MI355X GEMM (see linear.py and
-gdn_projection.py)."""
+"""nano-vLLM layer mirrors whose matmul is the MI355X GEMM (see linear.py,
+gdn_projection.py and mlp.py)."""
 from .gdn_projection import GdnInputProjection
 from .linear import (
     ColumnParallelLinear,
@@ -11,6 +11,7 @@ from .linear import (
     ReplicatedLinear,
     RowParallelLinear,
 )
+from .mlp import Qwen35MLP
 
 __all__ = [
     "ColumnParallelLinear",
@@ -20,6 +21,7 @@ __all__ = [
     "MergedColumnParallelLinear",
     "ParallelLMHead",
     "QKVParallelLinear",
+    "Qwen35MLP",
     "ReplicatedLinear",
     "RowParallelLinear",
 ]

@@ -311,3 +311,77 @@ def repeats_for(flops: float, repeat_override: int = -1) -> int:
     if repeat_override > 0:
         return repeat_override
     return int(min(max(int(2.0e10 / max(flops, 1.0)), 10), 200))
+
+
+# ---------------------------------------------------------------------------
+# Fused gate/up projection and SiLU-and-mul
+# ---------------------------------------------------------------------------
+# The Qwen3.5 MLP computes down(SiluAndMul(gate_up(x))) (models/qwen3_5.py:105-118):
+# gate_up is a MergedColumnParallelLinear whose W is [W_gate; W_up]
+# (layers/linear.py:76-97) and SiluAndMul splits the output in two halves and
+# returns F.silu(x) * y (layers/activation.py:8-11).
+
+# max over x of |d/dx (x * sigmoid(x))|; the derivative peaks at 1.0998 near
+# x = 2.40 (and is bounded below by -0.0998), so 1.1 bounds |silu'|.
+SILU_SLOPE_BOUND = 1.1
+
+
+def silu_f64(x: np.ndarray) -> np.ndarray:
+    """x * sigmoid(x) = x / (1 + exp(-x)) in float64 (exp overflows to inf
+    for x < -709, where the quotient is -0 as it should be)."""
+    x = np.asarray(x, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return x / (1.0 + np.exp(-x))
+
+
+def silu_mul_f64(a64: np.ndarray, w64: np.ndarray):
+    """SiluAndMul(a @ W^T) for W = [W_gate; W_up] of shape [2n, K]: returns
+    (r, g, u) with g = a W_gate^T, u = a W_up^T and r = silu(g) * u, all
+    float64."""
+    w64 = np.asarray(w64, dtype=np.float64)
+    n = w64.shape[0] // 2
+    if w64.shape[0] != 2 * n:
+        raise ValueError("W must hold gate and up halves of equal height")
+    g = gemm_f64(a64, w64[:n])
+    u = gemm_f64(a64, w64[n:])
+    return silu_f64(g) * u, g, u
+
+
+def silu_mul_tolerance(r64, g64, u64, sg64, su64, k: int, dtype: str, ulps: float = 2.0) -> np.ndarray:
+    """Per-element bound for silu(g~) * u~ evaluated in fp32 from fp32
+    accumulations g~, u~ and rounded once to `dtype`.  With dg, du the fp32
+    accumulation bounds of g and u (sg, su their sums of |a w|), the mean
+    value theorem gives |silu(g~) u~ - silu(g) u| <= 1.1 dg (|u| + du) +
+    |silu(g)| du; the fp32 exp, divide and multiply add at most 16 * 2^-24
+    of the value; the output rounding is covered by `ulps` units in the last
+    place of `dtype` at the exact value."""
+    dg = fp32_accumulation_bound(sg64, k)
+    du = fp32_accumulation_bound(su64, k)
+    g64 = np.asarray(g64, dtype=np.float64)
+    u64 = np.asarray(u64, dtype=np.float64)
+    r64 = np.asarray(r64, dtype=np.float64)
+    prop = SILU_SLOPE_BOUND * dg * (np.abs(u64) + du) + np.abs(silu_f64(g64)) * du
+    evaluation = 16 * 2.0 ** -24 * (np.abs(r64) + prop)
+    return ulps * ulp_at(r64, dtype) + prop + evaluation
+
+
+# ---------------------------------------------------------------------------
+# Greedy token of the LM head
+# ---------------------------------------------------------------------------
+def greedy_tokens(logits: np.ndarray) -> np.ndarray:
+    """Greedy rows of Sampler.forward (layers/sampler.py:19-32): argmax of
+    the fp32 logits along the vocabulary, first index on ties (torch.argmax)."""
+    return np.argmax(np.asarray(logits), axis=-1)
+
+
+def greedy_token_admissible(token: np.ndarray, r64: np.ndarray, s64: np.ndarray, k: int) -> np.ndarray:
+    """True where `token` is a correct greedy choice for logits computed in
+    fp32: its exact logit is within twice the fp32 accumulation bound of
+    the exact maximum (two logits closer than their error bounds may
+    legitimately swap order)."""
+    r64 = np.asarray(r64, dtype=np.float64)
+    bound = fp32_accumulation_bound(s64, k)
+    rows = np.arange(r64.shape[0])
+    best = r64.max(axis=-1)
+    chosen = r64[rows, token]
+    return chosen >= best - bound[rows, token] - bound.max(axis=-1)

@@ -153,3 +153,58 @@ def test_no_vendor_kernel_id():
     # (gemm_bench.cu:260-273); here every id is one of the ladder's kernels.
     names = {L.kernel_name(i) for i in range(L.KERNEL_COUNT)}
     assert not any("blas" in nm for nm in names)
+
+
+# ---------------------------------------------------------------------------
+# Fused gate/up projection + SiLU-and-mul
+# ---------------------------------------------------------------------------
+def _expected_silu(m, n, k, lda, ldw, aligned):
+    if not (aligned and k % 8 == 0 and lda % 8 == 0 and ldw % 8 == 0):
+        return L.EUNSUPPORTED
+    if m == 1 and 2 * n * k * 2 <= 64 * 2 ** 20:
+        return L.KERNEL_GEMV_DECODE
+    return L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
+
+
+@pytest.mark.parametrize("din,dout", [(F16, F16), (F16, F32), (BF16, BF16), (BF16, F32)])
+def test_silu_mul_selection(din, dout):
+    for m, n, k, aligned, pad in itertools.product([1, 2, 32, 33, 2048], [1, 100, 3584, 75968],
+                                                   [8, 72, 1024, 1000, 7], (0, 1), (0, 2)):
+        lda, ldw = k + pad, k + pad
+        got = L.silu_mul_select(m, n, k, lda, ldw, n, din, dout, aligned)
+        assert got == _expected_silu(m, n, k, lda, ldw, aligned), (m, n, k, aligned, pad)
+        if got == L.EUNSUPPORTED:
+            assert "16-byte aligned" in L.last_error()
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    (dict(din=F32, dout=F32), L.EUNSUPPORTED, "silu_mul"),
+    (dict(din=BF16, dout=F16), L.EUNSUPPORTED, "silu_mul"),
+    (dict(k=0), L.EINVAL, "k must be positive"),
+    (dict(ldw=4), L.EINVAL, "ldw"),
+    (dict(ldc=3), L.EINVAL, "ldc"),
+    (dict(m=-1), L.EINVAL, "non-negative"),
+])
+def test_silu_mul_rejects_invalid(args, code, msg):
+    m, n, k = args.get("m", 4), args.get("n", 8), args.get("k", 16)
+    rc = L.silu_mul_select(m, n, k, args.get("lda", k), args.get("ldw", k), args.get("ldc", n),
+                           args.get("din", BF16), args.get("dout", BF16))
+    assert rc == code and msg in L.last_error()
+
+
+def test_silu_mul_validates_before_launch(lib):
+    assert lib.nanovllm_gemm_silu_mul(None, None, None, 0, 8, 16, 16, 16, 8, BF16, BF16, None) == L.OK
+    rc = lib.nanovllm_gemm_silu_mul(None, None, None, 4, 8, 16, 16, 16, 8, BF16, BF16, None)
+    assert rc == L.EINVAL and "non-null" in L.last_error()
+    dummy = 1 << 20
+    rc = lib.nanovllm_gemm_silu_mul_with_kernel(L.KERNEL_MFMA_DIRECT, dummy, dummy, dummy, 4, 8, 16, 16, 16, 8,
+                                                BF16, BF16, None)
+    assert rc == L.EUNSUPPORTED and "mfma_direct" in L.last_error()
+    rc = lib.nanovllm_gemm_silu_mul_with_kernel(L.KERNEL_GEMV_DECODE, dummy, dummy, dummy, 4, 8, 16, 16, 16, 8,
+                                                BF16, BF16, None)
+    assert rc == L.EUNSUPPORTED
+    rc = lib.nanovllm_gemm_silu_mul_with_kernel(99, dummy, dummy, dummy, 4, 8, 16, 16, 16, 8, BF16, BF16, None)
+    assert rc == L.EINVAL and "kernel id" in L.last_error()
+    # unaligned pointers: only the vector path exists for the fused op
+    rc = lib.nanovllm_gemm_silu_mul(dummy + 2, dummy, dummy, 4, 8, 16, 16, 16, 8, BF16, BF16, None)
+    assert rc == L.EUNSUPPORTED and "aligned" in L.last_error()

@@ -389,3 +389,88 @@ def test_output_rounding_ties_to_even(din):
             assert np.array_equal(got, want[:mm]), f"{L.kernel_name(kernel)}: {int((got != want[:mm]).sum())} differ"
             ran += 1
     assert ran >= 6   # direct x3, staged x3, splitk x2, gemv x1
+
+
+# ---------------------------------------------------------------------------
+# Fused gate/up projection + SiLU-and-mul
+# ---------------------------------------------------------------------------
+def _check_silu_mul(got: torch.Tensor, a: torch.Tensor, w: torch.Tensor, dout: torch.dtype, rows=None,
+                    min_within_2ulp=0.97):
+    """Bar: |out - R| <= silu_mul_tolerance (2 ulp of the output type at the
+    exact value R = silu(g) u, plus the propagated fp32 accumulation error of
+    g and u, plus the fp32 evaluation of silu and the product); for narrow
+    outputs also >= min_within_2ulp of the elements within 2 ulp of R rounded
+    once, for fp32 outputs relative Frobenius <= 1e-5."""
+    a64, w64 = a.double().numpy(), w.double().numpy()
+    if rows is not None:
+        a64, got = a64[rows], got[rows]
+    n = w64.shape[0] // 2
+    r, g, u = orc.silu_mul_f64(a64, w64)
+    tol = orc.silu_mul_tolerance(r, g, u, orc.abs_products_f64(a64, w64[:n]), orc.abs_products_f64(a64, w64[n:]),
+                                 a.shape[1], NAME[dout])
+    g64 = got.double().cpu().numpy()
+    assert np.isfinite(g64).all(), "non-finite output"
+    err = np.abs(g64 - r)
+    bad = err > tol
+    assert not bad.any(), f"{int(bad.sum())} elements outside tolerance; worst excess {float((err - tol).max()):.3g}"
+    if dout == torch.float32:
+        assert orc.rel_frobenius(g64, r) <= 1e-5
+    else:
+        ulps = orc.ulp_distance(_to_np_out(got, dout), orc.round_f64(r, NAME[dout]), NAME[dout])
+        assert float((ulps <= 2).mean()) >= min_within_2ulp
+
+
+SILU_SHAPES = [(1, 1, 8), (1, 37, 64), (5, 7, 72), (16, 100, 136), (31, 65, 264), (33, 129, 520),
+               (130, 300, 264), (257, 97, 1000)]
+SILU_KERNELS = [L.KERNEL_GEMV_DECODE, L.KERNEL_SPLITK_DECODE, L.KERNEL_MFMA_STAGED]
+SILU_PAIRS = [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32), (torch.float16, torch.float16),
+              (torch.float16, torch.float32)]
+
+
+@pytest.mark.parametrize("kernel", SILU_KERNELS, ids=lambda k: L.kernel_name(k))
+@pytest.mark.parametrize("din,dout", SILU_PAIRS, ids=lambda d: NAME[d])
+def test_silu_mul_every_rung_small(kernel, din, dout):
+    gen = torch.Generator().manual_seed(31)
+    ran = 0
+    for m, n, k in SILU_SHAPES:
+        if kernel == L.KERNEL_GEMV_DECODE and m != 1 or kernel == L.KERNEL_SPLITK_DECODE and m > 32:
+            continue
+        _say(f"silu_mul {L.kernel_name(kernel)} {NAME[din]}->{NAME[dout]} M={m} N={n} K={k}")
+        a = torch.randn((m, k), generator=gen).to(din)
+        w = (torch.randn((2 * n, k), generator=gen) * 0.1).to(din)
+        out = G.gemm_silu_mul_with_kernel(a.to(DEV), w.to(DEV), kernel, dout)
+        torch.cuda.synchronize()
+        assert out.shape == (m, n) and out.dtype == dout
+        _check_silu_mul(out.cpu(), a, w, dout)
+        ran += 1
+    assert ran > 0
+
+
+@pytest.mark.parametrize("m", [1, 4, 32, 2048])
+def test_silu_mul_qwen_mlp_shape(m):
+    """Qwen3.5-0.8B gate_up_proj (2 x 3584 rows, K = 1024) + SiluAndMul on
+    the kernel the selection table picks."""
+    gen = torch.Generator().manual_seed(50 + m)
+    a = torch.randn((m, 1024), generator=gen).bfloat16()
+    w = (torch.randn((7168, 1024), generator=gen) * 0.02).bfloat16()
+    ad, wd = a.to(DEV), w.to(DEV)
+    want = {1: "gemv_decode", 4: "splitk_decode", 32: "splitk_decode", 2048: "mfma_staged"}[m]
+    assert G.silu_mul_selected_kernel(ad, wd) == want
+    _say(f"silu_mul qwen mlp M={m} ({want})")
+    out = G.gemm_silu_mul(ad, wd)
+    torch.cuda.synchronize()
+    rows = None if m <= 32 else np.unique(np.concatenate([np.linspace(0, m - 1, 48).astype(int), [m - 1]]))
+    _check_silu_mul(out.cpu(), a, w, torch.bfloat16, rows=rows, min_within_2ulp=0.99)
+
+
+def test_silu_mul_contract_errors_on_gpu():
+    a = torch.randn(4, 64, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="equal height"):
+        G.gemm_silu_mul(a, torch.randn(7, 64, device=DEV, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        G.gemm_silu_mul(a.float(), torch.randn(8, 64, device=DEV))
+    # a contiguous view two bytes into its storage: rows are not 16-byte aligned
+    misaligned = torch.randn(4 * 64 + 1, device=DEV, dtype=torch.bfloat16)[1:].view(4, 64)
+    assert misaligned.is_contiguous() and misaligned.data_ptr() % 16 == 2
+    with pytest.raises(RuntimeError, match="aligned"):
+        G.gemm_silu_mul(misaligned, torch.randn(8, 64, device=DEV, dtype=torch.bfloat16))

@@ -107,6 +107,28 @@ def test_gdn_projection_matches_four_linears(dims):
         proj.weight.weight_loader(proj.weight, full["z"], "v")
 
 
+def test_qwen35_mlp_matches_reference_composition():
+    """down_proj(SiluAndMul(gate_up_proj(x))) of models/qwen3_5.py:117-118; on
+    CPU tensors the auto backend takes the reference composition."""
+    mlp = Lyr.Qwen35MLP(32, 48)
+    g = torch.Generator().manual_seed(3)
+    wg, wu, wd = torch.randn(48, 32, generator=g), torch.randn(48, 32, generator=g), torch.randn(32, 48, generator=g)
+    mlp.gate_up_proj.weight.weight_loader(mlp.gate_up_proj.weight, wg, 0)
+    mlp.gate_up_proj.weight.weight_loader(mlp.gate_up_proj.weight, wu, 1)
+    mlp.down_proj.weight.weight_loader(mlp.down_proj.weight, wd)
+    x = torch.randn(5, 32, generator=g)
+    ref = F.linear(F.silu(F.linear(x, wg)) * F.linear(x, wu), wd)
+    for backend in ("torch", "auto"):
+        mlp.gemm_backend = backend
+        assert mlp.gate_up_proj.gemm_backend == backend and mlp.down_proj.gemm_backend == backend
+        torch.testing.assert_close(mlp(x), ref)
+    with pytest.raises(ValueError, match="SiLU"):
+        Lyr.Qwen35MLP(32, 48, hidden_act="gelu")
+    mlp.gemm_backend = "hip"
+    with pytest.raises(RuntimeError, match="CUDA"):
+        mlp(x)
+
+
 def _tp_worker(rank, world, init_file, result_file):
     dist.init_process_group("gloo", init_method=f"file://{init_file}", rank=rank, world_size=world)
     try:

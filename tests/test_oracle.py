@@ -297,3 +297,81 @@ def test_reference_policy_matches_recorded_rows(dtype, label):
     repeats, dispatch = CSV_ROWS[(dtype, label)]
     assert orc.repeats_for(2.0 * m * n * k) == repeats
     assert orc.choose_path_reference(m, n, k, dtype) == dispatch
+
+
+# ---------------------------------------------------------------------------
+# Fused SiLU-and-mul oracle
+# ---------------------------------------------------------------------------
+def test_silu_closed_form_against_torch():
+    x = np.concatenate([np.linspace(-60, 60, 4001), [-1000.0, -745.0, 0.0, 745.0, 1000.0]])
+    want = torch.nn.functional.silu(torch.from_numpy(x)).numpy()
+    got = orc.silu_f64(x)
+    np.testing.assert_allclose(got, want, rtol=1e-15, atol=1e-300)
+    assert got[-5] == 0.0 and np.signbit(got[-5])      # -1000 * sigmoid(-1000) = -0
+
+
+def test_silu_slope_bound_brute_force():
+    # the propagation term of silu_mul_tolerance relies on |silu'| <= 1.1
+    x = np.linspace(-40, 40, 800001)
+    slope = np.diff(orc.silu_f64(x)) / np.diff(x)
+    assert slope.max() <= orc.SILU_SLOPE_BOUND and slope.max() > 1.099
+    assert slope.min() >= -orc.SILU_SLOPE_BOUND
+
+
+def test_silu_mul_matches_reference_composition():
+    """SiluAndMul(x) = F.silu(x[:, :n]) * x[:, n:] of the merged projection
+    output (layers/activation.py:8-11), here in float64."""
+    rng = np.random.default_rng(5)
+    a, w = rng.standard_normal((7, 48)), rng.standard_normal((2 * 20, 48)) * 0.2
+    r, g, u = orc.silu_mul_f64(a, w)
+    y = torch.from_numpy(a) @ torch.from_numpy(w).T
+    x1, x2 = y.chunk(2, -1)
+    # numpy and torch sum the float64 products in different orders
+    np.testing.assert_allclose(r, (torch.nn.functional.silu(x1) * x2).numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(g, x1.numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(u, x2.numpy(), rtol=1e-12, atol=1e-13)
+    with pytest.raises(ValueError):
+        orc.silu_mul_f64(a, w[:-1])
+
+
+def _fp32_fused(a, w, dtype):
+    """What a fused kernel computes: fp32 accumulation, silu and product in
+    fp32, one rounding to the output type."""
+    n = w.shape[0] // 2
+    a32, w32 = torch.from_numpy(a).float(), torch.from_numpy(w).float()
+    g, u = a32 @ w32[:n].T, a32 @ w32[n:].T
+    out = torch.nn.functional.silu(g) * u
+    return out.to(torch.bfloat16 if dtype == "bf16" else torch.float16).double().numpy()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_silu_mul_tolerance_accepts_fused_and_rejects_planted(dtype):
+    rng = np.random.default_rng(9)
+    k, n = 512, 96
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    a = torch.from_numpy(rng.standard_normal((33, k))).to(tdt).double().numpy()
+    w = torch.from_numpy(rng.standard_normal((2 * n, k)) * 0.1).to(tdt).double().numpy()
+    r, g, u = orc.silu_mul_f64(a, w)
+    sg = orc.abs_products_f64(a, w[:n])
+    su = orc.abs_products_f64(a, w[n:])
+    tol = orc.silu_mul_tolerance(r, g, u, sg, su, k, dtype)
+    assert (np.abs(_fp32_fused(a, w, dtype) - r) <= tol).all()
+    planted = {
+        "roles swapped": orc.silu_f64(u) * g,
+        "sigmoid without x": g * 0 + u / (1.0 + np.exp(-g)),
+        "gate/up rows paired off by one": orc.silu_f64(g) * np.roll(u, 1, axis=1),
+        "one K chunk dropped": orc.silu_mul_f64(a[:, 8:], w[:, 8:])[0],
+    }
+    for name, bad in planted.items():
+        assert (np.abs(bad - r) > tol).any(), name
+
+
+def test_greedy_tokens_first_index_on_ties_and_admissible():
+    logits = np.array([[1.0, 3.0, 3.0, -2.0], [0.5, 0.25, 0.5, 0.5]], dtype=np.float32)
+    np.testing.assert_array_equal(orc.greedy_tokens(logits), [1, 0])
+    np.testing.assert_array_equal(orc.greedy_tokens(logits), torch.from_numpy(logits).argmax(-1).numpy())
+    r = logits.astype(np.float64)
+    s = np.full_like(r, 1.0)
+    k = 1024   # bound = 1024 * 2^-24 = 6.1e-5
+    assert orc.greedy_token_admissible(np.array([2, 3]), r, s, k).all()        # ties are admissible
+    assert not orc.greedy_token_admissible(np.array([0, 1]), r, s, k).any()    # clearly smaller logits are not
