@@ -360,6 +360,44 @@ def main() -> int:
         extras["mlp_gate_up_silu_mul_bf16_n3584_k1024"] = s_rows
         del s_w
 
+        # ----------------------------- greedy LM head (argmax, no logits)
+        # Against the reference's path: fp32 logits [M, 151936] from the GEMM,
+        # then float_logits.argmax(dim=-1) (sampler.py:19-32) on the GPU.
+        lw = W.WORKLOADS["bf16_lm_head_n151936_k1024"]
+        _, l_w0 = W.make_inputs("bf16_lm_head_n151936_k1024", 1, device=dev)
+        l_ws = [l_w0, l_w0.clone()]
+        l_rows = []
+        for lm in (1, 32):
+            l_a, _ = W.make_inputs("bf16_lm_head_n151936_k1024", lm, device=dev)
+            l_tok = torch.empty(lm, dtype=torch.int64, device=dev)
+            l_val = torch.empty(lm, dtype=torch.float32, device=dev)
+            l_need = L.argmax_workspace_bytes(lm, lw.n, lw.k, lw.k, lw.k, L.BF16)
+            l_ws_buf = torch.empty(l_need, dtype=torch.uint8, device=dev)
+            l_logits = torch.empty(lm, lw.n, dtype=torch.float32, device=dev)
+
+            def greedy(wt, l_a=l_a, l_tok=l_tok, l_val=l_val, l_ws_buf=l_ws_buf, lm=lm, l_need=l_need):
+                args_ = (l_a.data_ptr(), wt.data_ptr(), l_tok.data_ptr(), l_val.data_ptr(), lm, lw.n, lw.k, lw.k,
+                         lw.k, L.BF16, l_ws_buf.data_ptr(), l_need)
+
+                def f():
+                    L.argmax_raw(*args_, torch.cuda.current_stream().cuda_stream)
+                return f
+
+            def logits_then_argmax(wt, l_a=l_a, l_logits=l_logits, lm=lm):
+                gemm = launcher(l_a, wt, l_logits, lm, lw.n, lw.k, L.B_NK, torch.bfloat16, torch.float32)
+
+                def f():
+                    gemm()
+                    l_logits.argmax(dim=-1)
+                return f
+            t_g = median_graph_ms(torch, [greedy(l_ws[i % 2]) for i in range(20)], trials=3)
+            t_l = median_graph_ms(torch, [logits_then_argmax(l_ws[i % 2]) for i in range(20)], trials=3)
+            l_rows.append({"m": lm, "greedy_us": round(t_g * 1e3, 3), "logits_then_argmax_us": round(t_l * 1e3, 3),
+                           "speedup": round(t_l / t_g, 3)})
+            log(f"lm head greedy M={lm}: fused {t_g * 1e3:.1f} us, fp32 logits + torch argmax {t_l * 1e3:.1f} us")
+        extras["lm_head_greedy_bf16_n151936_k1024"] = l_rows
+        del l_ws, l_w0
+
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:
         F = torch.nn.functional

@@ -174,6 +174,50 @@ int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k,
                                   int64_t lda, int64_t ldw, int64_t ldc,
                                   int dtype_in, int dtype_out, int aligned16);
 
+/*
+ * Greedy token of an LM head without its logits:
+ *
+ *     tokens[i] = argmax_j sum_k a[i,k] w[j,k],   j < n
+ *
+ * fp32 accumulation, first index on ties, NaN above every number (the
+ * rule of torch.argmax), token ids as int64; max_logits[i] (optional, may
+ * be NULL) receives the fp32 logit of the token.  Replaces the [m, n] fp32
+ * logits of ParallelLMHead (nanovllm/layers/embed_head.py:61) followed by
+ * the greedy branch of Sampler, float_logits.argmax(dim=-1)
+ * (nanovllm/layers/sampler.py:19-32).  `workspace` (8-byte aligned, device
+ * memory, contents scratch) must hold
+ * nanovllm_gemm_argmax_workspace_bytes() bytes; one call launches the GEMM
+ * pass and a small reduction pass on `stream`.  Inputs f16 or bf16 on the
+ * vector path (16-byte aligned a and w, k, lda and ldw multiples of 8).
+ */
+int nanovllm_gemm_argmax(const void* a, const void* w,
+                         int64_t* tokens, float* max_logits,
+                         int64_t m, int64_t n, int64_t k,
+                         int64_t lda, int64_t ldw, int dtype_in,
+                         void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/* Workspace bytes nanovllm_gemm_argmax needs for this problem (enough for
+ * any kernel that can run it), or a negative code.  Pure host function. */
+int64_t nanovllm_gemm_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k,
+                                             int64_t lda, int64_t ldw, int dtype_in);
+
+/* The greedy head forced onto one kernel (splitk_decode for m <= 32 or
+ * mfma_staged), for parity tests of both (gemm_bench.cu:396-416 pattern). */
+int nanovllm_gemm_argmax_with_kernel(int kernel_id,
+                                     const void* a, const void* w,
+                                     int64_t* tokens, float* max_logits,
+                                     int64_t m, int64_t n, int64_t k,
+                                     int64_t lda, int64_t ldw, int dtype_in,
+                                     void* workspace, int64_t workspace_bytes,
+                                     void* stream);
+
+/* Kernel id nanovllm_gemm_argmax() would run its GEMM pass on (or a
+ * negative code).  Pure host function (gemm_bench.cu:252-273 pattern). */
+int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k,
+                                int64_t lda, int64_t ldw, int dtype_in,
+                                int aligned16);
+
 /* Stable name of a kernel id ("fp32_tiled", "mfma_staged", ...), or
  * "unknown".  Mirrors path_name (gemm_bench.cu:275-282). */
 const char* nanovllm_gemm_kernel_name(int kernel_id);

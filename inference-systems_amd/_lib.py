@@ -44,6 +44,11 @@ SIGNATURES = {
     "nanovllm_gemm_silu_mul_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT,
                                                   _INT, _VP]),
     "nanovllm_gemm_silu_mul_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT]),
+    "nanovllm_gemm_argmax": (_INT, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP, _I64, _VP]),
+    "nanovllm_gemm_argmax_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _INT]),
+    "nanovllm_gemm_argmax_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP,
+                                                _I64, _VP]),
+    "nanovllm_gemm_argmax_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _INT, _INT]),
     "nanovllm_gemm_kernel_name": (ctypes.c_char_p, [_INT]),
     "nanovllm_gemm_last_error": (ctypes.c_char_p, []),
     "nanovllm_gemm_version": (_INT, []),
@@ -135,6 +140,28 @@ def silu_mul_raw(a_ptr, w_ptr, c_ptr, m, n, k, lda, ldw, ldc, dtype_in, dtype_ou
         rc = lib.nanovllm_gemm_silu_mul_with_kernel(kernel, a_ptr, w_ptr, c_ptr, m, n, k, lda, ldw, ldc, dtype_in,
                                                     dtype_out, stream)
     check(rc, "nanovllm_gemm_silu_mul")
+
+
+def argmax_workspace_bytes(m, n, k, lda, ldw, dtype_in) -> int:
+    """Workspace bytes of the greedy head (negative code if invalid)."""
+    return load().nanovllm_gemm_argmax_workspace_bytes(m, n, k, lda, ldw, dtype_in)
+
+
+def argmax_select(m, n, k, lda, ldw, dtype_in, aligned16=True) -> int:
+    return load().nanovllm_gemm_argmax_select(m, n, k, lda, ldw, dtype_in, int(bool(aligned16)))
+
+
+def argmax_raw(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in, ws_ptr, ws_bytes, stream,
+               kernel: int | None = None) -> None:
+    """Enqueue the greedy LM head (GEMM pass + reduction) on `stream`; raise on error."""
+    lib = load()
+    if kernel is None:
+        rc = lib.nanovllm_gemm_argmax(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in, ws_ptr,
+                                      ws_bytes, stream)
+    else:
+        rc = lib.nanovllm_gemm_argmax_with_kernel(kernel, a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw,
+                                                  dtype_in, ws_ptr, ws_bytes, stream)
+    check(rc, "nanovllm_gemm_argmax")
 
 
 def gemm_raw(a_ptr, b_ptr, c_ptr, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, stream,

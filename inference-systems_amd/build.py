@@ -41,6 +41,7 @@ SOURCES = [
     "gemm_staged.hip",
     "gemm_decode.hip",
     "gemm_gemv.hip",
+    "gemm_argmax.hip",
 ]
 
 

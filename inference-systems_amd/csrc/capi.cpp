@@ -201,6 +201,82 @@ int silu_mul_entry(int forced_kernel, const void* a, const void* w, void* c, int
     return run(kernel, p, static_cast<hipStream_t>(stream));
 }
 
+// ---------------------------------------------------------------------------
+// Greedy LM head: token = argmax_j (a W^T)[i, j] per row, without writing the
+// logits.  Partial keys per workgroup go to a caller-provided workspace.
+// ---------------------------------------------------------------------------
+int validate_argmax(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int din) {
+    if (din != NANOVLLM_GEMM_F16 && din != NANOVLLM_GEMM_BF16)
+        return set_error(din >= NANOVLLM_GEMM_F32 && din <= NANOVLLM_GEMM_BF16 ? NANOVLLM_GEMM_EUNSUPPORTED
+                                                                               : NANOVLLM_GEMM_EINVAL,
+                         "argmax takes float16 or bfloat16 inputs (dtype code %d)", din);
+    if (m < 0) return set_error(NANOVLLM_GEMM_EINVAL, "m must be non-negative (m=%lld)", (long long)m);
+    if (n < 1 || n > INT64_C(0xFFFFFFFF))
+        return set_error(NANOVLLM_GEMM_EINVAL, "n must be in [1, 2^32) (n=%lld)", (long long)n);
+    if (k < 1) return set_error(NANOVLLM_GEMM_EINVAL, "k must be positive (k=%lld)", (long long)k);
+    if (lda < k) return set_error(NANOVLLM_GEMM_EINVAL, "lda (%lld) must be >= k (%lld)", (long long)lda, (long long)k);
+    if (ldw < k) return set_error(NANOVLLM_GEMM_EINVAL, "ldw (%lld) must be >= k (%lld)", (long long)ldw, (long long)k);
+    return NANOVLLM_GEMM_OK;
+}
+
+bool supports_argmax(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldw, int aligned16) {
+    if (!vector_ok(k, lda, ldw, NANOVLLM_GEMM_B_NK, aligned16)) return false;
+    if (kernel_id == NANOVLLM_GEMM_KERNEL_SPLITK_DECODE) return m <= kDecodeMaxM;
+    return kernel_id == NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
+}
+
+int select_argmax(int64_t m, int64_t k, int64_t lda, int64_t ldw, int aligned16) {
+    if (!vector_ok(k, lda, ldw, NANOVLLM_GEMM_B_NK, aligned16))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "argmax needs 16-byte aligned a and w with k, lda and ldw multiples of 8 "
+                         "(k=%lld lda=%lld ldw=%lld)",
+                         (long long)k, (long long)lda, (long long)ldw);
+    return m <= kDecodeMaxM ? NANOVLLM_GEMM_KERNEL_SPLITK_DECODE : NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
+}
+
+// Bytes of partial keys any kernel that can run the problem writes: one
+// 8-byte key per row of A per workgroup along N (split-K workgroups cover at
+// least 16 columns, staged tiles 128).
+int64_t argmax_workspace_bytes(int64_t m, int64_t n) {
+    const int64_t cols_per_block = m <= kDecodeMaxM ? 16 : 128;
+    return ((n + cols_per_block - 1) / cols_per_block) * m * int64_t(sizeof(uint64_t));
+}
+
+int argmax_entry(int forced_kernel, const void* a, const void* w, int64_t* tokens, float* logits, int64_t m,
+                 int64_t n, int64_t k, int64_t lda, int64_t ldw, int din, void* workspace, int64_t workspace_bytes,
+                 void* stream) {
+    g_last_error.clear();
+    int rc = validate_argmax(m, n, k, lda, ldw, din);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m == 0) return NANOVLLM_GEMM_OK;
+    if (a == nullptr || w == nullptr || tokens == nullptr || workspace == nullptr)
+        return set_error(NANOVLLM_GEMM_EINVAL, "a, w, tokens and workspace must be non-null device pointers");
+    if (reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
+        return set_error(NANOVLLM_GEMM_EINVAL, "workspace must be 8-byte aligned");
+    const int64_t need = argmax_workspace_bytes(m, n);
+    if (workspace_bytes < need)
+        return set_error(NANOVLLM_GEMM_EINVAL, "workspace of %lld bytes is too small: this problem needs %lld",
+                         (long long)workspace_bytes, (long long)need);
+    const int al = aligned16_of(a, w);
+    int kernel = forced_kernel;
+    if (kernel < 0) {
+        kernel = select_argmax(m, k, lda, ldw, al);
+        if (kernel < 0) return kernel;
+    } else if (!supports_argmax(kernel, m, k, lda, ldw, al)) {
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "kernel %s cannot run argmax for this problem (m=%lld n=%lld k=%lld)",
+                         nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);
+    }
+    int64_t blocks = 0;
+    Problem p{a, w, nullptr, m, n, k, lda, ldw, n, NANOVLLM_GEMM_B_NK, din, NANOVLLM_GEMM_F32};
+    p.epi = EPI_ARGMAX;
+    p.keys = static_cast<uint64_t*>(workspace);
+    p.key_blocks = &blocks;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = run(kernel, p, s);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    return launch_argmax_finalize(p.keys, blocks, m, tokens, logits, s);
+}
+
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -288,8 +364,42 @@ int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k, int64_t lda, 
     return nvg::select_silu_mul(m, n, k, lda, ldw, aligned16);
 }
 
+int64_t nanovllm_gemm_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
+                                             int dtype_in) {
+    nvg::g_last_error.clear();
+    const int rc = nvg::validate_argmax(m, n, k, lda, ldw, dtype_in);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    return nvg::argmax_workspace_bytes(m, n);
+}
+
+int nanovllm_gemm_argmax(const void* a, const void* w, int64_t* tokens, float* max_logits, int64_t m, int64_t n,
+                         int64_t k, int64_t lda, int64_t ldw, int dtype_in, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+    return nvg::argmax_entry(-1, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, workspace, workspace_bytes,
+                             stream);
+}
+
+int nanovllm_gemm_argmax_with_kernel(int kernel_id, const void* a, const void* w, int64_t* tokens,
+                                     float* max_logits, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
+                                     int dtype_in, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
+        nvg::g_last_error.clear();
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+    return nvg::argmax_entry(kernel_id, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, workspace,
+                             workspace_bytes, stream);
+}
+
+int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int dtype_in,
+                                int aligned16) {
+    nvg::g_last_error.clear();
+    const int rc = nvg::validate_argmax(m, n, k, lda, ldw, dtype_in);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    return nvg::select_argmax(m, k, lda, ldw, aligned16);
+}
+
 const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
 
-int nanovllm_gemm_version(void) { return (1 << 16) | 1; }
+int nanovllm_gemm_version(void) { return (1 << 16) | 2; }
 
 }  // extern "C"

@@ -1,0 +1,64 @@
+// Final step of the greedy LM head (EPI_ARGMAX): each workgroup of the GEMM
+// left one key per row of A (argmax_key of its best column); this kernel
+// takes the maximum key of each row over all workgroups and decodes it into
+// the token id and its logit.  It stands in for Sampler's greedy branch,
+// float_logits.argmax(dim=-1) (nanovllm/layers/sampler.py:19-32), which
+// reads back the [M, vocab] fp32 logits the GEMM wrote.
+#include "gemm_common.hpp"
+
+namespace nvg {
+namespace {
+
+// One workgroup per row; a row's keys are contiguous ([m, blocks]).  Each
+// thread issues kFinalizeUnroll independent loads per round, so the ~9500
+// keys of a 151936-entry vocabulary take three rounds of memory latency.
+constexpr int kFinalizeThreads = 1024;
+constexpr int kFinalizeUnroll = 4;
+
+__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(
+    const uint64_t* __restrict__ keys, int64_t blocks, int64_t m, int64_t* __restrict__ tokens,
+    float* __restrict__ logits) {
+    __shared__ uint64_t best_of_wave[kFinalizeThreads / 64];
+    const int64_t row = blockIdx.x;
+    const uint64_t* rk = keys + row * blocks;
+    uint64_t best = 0;
+    for (int64_t b0 = threadIdx.x; b0 < blocks; b0 += kFinalizeThreads * kFinalizeUnroll) {
+        uint64_t k[kFinalizeUnroll];
+#pragma unroll
+        for (int u = 0; u < kFinalizeUnroll; ++u) {
+            const int64_t b = b0 + int64_t(u) * kFinalizeThreads;
+            k[u] = b < blocks ? rk[b] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kFinalizeUnroll; ++u) best = k[u] > best ? k[u] : best;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), off))) << 32) |
+                           uint64_t(uint32_t(__shfl_xor(int(best & 0xFFFFFFFFu), off)));
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) best_of_wave[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int wv = 1; wv < kFinalizeThreads / 64; ++wv) best = best_of_wave[wv] > best ? best_of_wave[wv] : best;
+        tokens[row] = int64_t(0xFFFFFFFFu - uint32_t(best & 0xFFFFFFFFu));
+        if (logits != nullptr) {
+            const uint32_t ordered = uint32_t(best >> 32);
+            const uint32_t bits = (ordered & 0x80000000u) ? (ordered & 0x7FFFFFFFu) : ~ordered;
+            logits[row] = __builtin_bit_cast(float, bits);
+        }
+    }
+}
+
+}  // namespace
+
+int launch_argmax_finalize(const uint64_t* keys, int64_t blocks, int64_t m, int64_t* tokens, float* logits,
+                           hipStream_t s) {
+    if (m > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "argmax: too many rows");
+    hipLaunchKernelGGL(argmax_finalize_kernel, dim3(static_cast<uint32_t>(m)), dim3(kFinalizeThreads), 0, s, keys,
+                       blocks, m, tokens, logits);
+    return check_launch("argmax_finalize");
+}
+
+}  // namespace nvg

@@ -21,8 +21,13 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 // SiluAndMul of a gate/up projection: W = [W_gate; W_up] has 2n rows, output
 // column j is silu(a . W_gate[j]) * (a . W_up[j]), computed in fp32 from the
 // fp32 accumulators and rounded once.
+// EPI_ARGMAX is the greedy token of an LM head: no output matrix; each
+// workgroup writes, per row of A, one 64-bit key (argmax_key) of the best
+// column it computed into a workspace of [M, workgroups along N] keys,
+// reduced by launch_argmax_finalize.
 constexpr int EPI_NONE = 0;
 constexpr int EPI_SILU_MUL = 1;
+constexpr int EPI_ARGMAX = 2;
 
 // One GEMM problem as it crosses the C ABI (see include/nanovllm_gemm.h).
 struct Problem {
@@ -35,6 +40,8 @@ struct Problem {
     int dtype_in;
     int dtype_out;
     int epi = EPI_NONE;   // EPI_SILU_MUL: n output columns from 2n rows of b
+    uint64_t* keys = nullptr;         // EPI_ARGMAX: [m, workgroups along N] partial keys
+    int64_t* key_blocks = nullptr;    // EPI_ARGMAX: set by the launcher to its workgroups along N
 };
 
 constexpr int kWave = 64;
@@ -128,6 +135,19 @@ __device__ __forceinline__ float silu_f32(float x) {
     return x / (1.0f + expf(-x));
 }
 
+// Greedy-argmax key: the fp32 logit mapped to an unsigned integer with the
+// same order (sign-magnitude to offset binary) in the high word, and
+// 0xFFFFFFFF - column in the low word, so the largest key is the largest
+// logit and, among equal logits, the first column (torch.argmax's rule).
+// Key 0 is below every real key.
+__device__ __forceinline__ uint64_t argmax_key(float v, int64_t col) {
+    // -0 ranks equal to +0, and every NaN ranks above every number (as in
+    // torch.argmax): both are canonicalised first.
+    const uint32_t b = v != v ? 0x7FC00000u : (v == 0.0f ? 0u : __builtin_bit_cast(uint32_t, v));
+    const uint32_t ordered = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (uint64_t(ordered) << 32) | uint64_t(0xFFFFFFFFu - uint32_t(col));
+}
+
 // Integer minimum.  The device `min` overload set has no exact match for
 // 64-bit integers here and resolves to a double-precision one, which costs
 // a dozen f64 instructions per call.
@@ -173,6 +193,12 @@ int launch_mfma_direct(const Problem& p, hipStream_t s);
 int launch_mfma_staged(const Problem& p, hipStream_t s);
 int launch_splitk_decode(const Problem& p, hipStream_t s);
 int launch_gemv_decode(const Problem& p, hipStream_t s);
+
+// Reduces `blocks` partial keys per row ([m, blocks], from an EPI_ARGMAX
+// launch) to the greedy token of each row (int64) and, if `logits` is not
+// null, its logit.
+int launch_argmax_finalize(const uint64_t* keys, int64_t blocks, int64_t m, int64_t* tokens, float* logits,
+                           hipStream_t s);
 
 // Records a message for nanovllm_gemm_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...);

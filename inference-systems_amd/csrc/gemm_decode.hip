@@ -27,7 +27,7 @@ constexpr int kDecStep = 32;   // K elements per MFMA
 template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
-    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc) {
+    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys) {
     __shared__ float red[WAVES][RG][MG][16][16];
 
     const int lane = threadIdx.x & 63;
@@ -37,7 +37,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
 
     // EPI_SILU_MUL: W-row groups pair up, group 2s holding gate rows and
     // group 2s + 1 the up rows of the same 16 output columns.
-    static_assert(EPI == EPI_NONE || RG % 2 == 0, "gate/up group pairs");
+    static_assert(EPI != EPI_SILU_MUL || RG % 2 == 0, "gate/up group pairs");
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;   // 16-column output groups per workgroup
     const int64_t n0 = int64_t(blockIdx.x) * 16 * OG;         // first output column
     const uint16_t* wp[RG];
@@ -94,6 +94,34 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
             for (int v = 0; v < 4; ++v) red[wave][r][g][4 * grp + v][i16] = acc[r][g][v];
     __syncthreads();
 
+    if constexpr (EPI == EPI_ARGMAX) {
+        // Per row of A, the best of this workgroup's 16 * RG columns: the
+        // sums go to LDS, then one thread per row scans them.
+        __shared__ float vals[MG * 16][16 * RG + 1];
+        for (int e = threadIdx.x; e < RG * MG * 256; e += WAVES * 64) {
+            const int r = e / (MG * 256);
+            const int g = (e / 256) % MG;
+            const int nn = e & 15;
+            const int mm = (e >> 4) & 15;
+            float sum = red[0][r][g][nn][mm];
+#pragma unroll
+            for (int wv = 1; wv < WAVES; ++wv) sum += red[wv][r][g][nn][mm];
+            vals[g * 16 + mm][16 * r + nn] = sum;
+        }
+        __syncthreads();
+        const int row = threadIdx.x;
+        if (row < MG * 16 && row < m) {
+            uint64_t best = 0;
+            for (int cc = 0; cc < 16 * RG; ++cc) {
+                if (n0 + cc >= n) break;
+                const uint64_t key = argmax_key(vals[row][cc], n0 + cc);
+                best = key > best ? key : best;
+            }
+            keys[row * int64_t(gridDim.x) + blockIdx.x] = best;
+        }
+        return;
+    }
+
     // Sum the per-wave partials in wave order (deterministic) and store.
     for (int e = threadIdx.x; e < OG * MG * 256; e += WAVES * 64) {
         const int o = e / (MG * 256);
@@ -125,9 +153,10 @@ int launch_cfg(const Problem& p, hipStream_t s) {
     const int64_t blocks = (p.n + 16 * OG - 1) / (16 * OG);
     if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
     const dim3 grid(static_cast<uint32_t>(blocks)), block(WAVES * 64);
+    if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
     hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, MG, RG, WAVES, UNROLL, EPI>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
-                       p.lda, p.ldb, p.ldc);
+                       p.lda, p.ldb, p.ldc, p.keys);
     return check_launch("splitk_decode");
 }
 
@@ -154,6 +183,24 @@ int launch_silu_mul(const Problem& p, hipStream_t s) {
     return launch_cfg<DT, DT_OUT, 2, 2, 8, 2, EPI_SILU_MUL>(p, s);
 }
 
+// Greedy LM head: the plain configurations, writing partial keys instead of
+// the fp32 logits.
+template <int DT>
+int launch_argmax(const Problem& p, hipStream_t s) {
+    constexpr int F = NANOVLLM_GEMM_F32;
+    const bool wide = p.n >= kWideN && p.m > 1;
+    if (p.m <= 8) {
+        if (wide) return launch_cfg<DT, F, 1, 4, 4, 4, EPI_ARGMAX>(p, s);
+        return launch_cfg<DT, F, 1, 1, 4, 8, EPI_ARGMAX>(p, s);
+    }
+    if (p.m <= 16) {
+        if (wide) return launch_cfg<DT, F, 1, 4, 4, 4, EPI_ARGMAX>(p, s);
+        return launch_cfg<DT, F, 1, 2, 8, 2, EPI_ARGMAX>(p, s);
+    }
+    if (wide) return launch_cfg<DT, F, 2, 4, 4, 4, EPI_ARGMAX>(p, s);
+    return launch_cfg<DT, F, 2, 2, 8, 2, EPI_ARGMAX>(p, s);
+}
+
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
     if (p.epi == EPI_SILU_MUL) return launch_silu_mul<DT, DT_OUT>(p, s);
@@ -173,6 +220,10 @@ int launch_typed(const Problem& p, hipStream_t s) {
 }  // namespace
 
 int launch_splitk_decode(const Problem& p, hipStream_t s) {
+    if (p.epi == EPI_ARGMAX) {
+        if (p.dtype_in == NANOVLLM_GEMM_BF16) return launch_argmax<NANOVLLM_GEMM_BF16>(p, s);
+        return launch_argmax<NANOVLLM_GEMM_F16>(p, s);
+    }
     if (p.dtype_in == NANOVLLM_GEMM_BF16) {
         if (p.dtype_out == NANOVLLM_GEMM_BF16) return launch_typed<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_BF16>(p, s);
         return launch_typed<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_F32>(p, s);

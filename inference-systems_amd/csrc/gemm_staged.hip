@@ -74,7 +74,7 @@ template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int 
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n, int c_vec) {
+    int tiles_m, int tiles_n, int c_vec, uint64_t* __restrict__ keys) {
     constexpr int NW = WGM * WGN;        // waves, in a WGM x WGN grid
     constexpr int NT = NW * 64;          // threads
     constexpr int WM = BM / WGM;         // wave tile rows (M)
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // EPI_SILU_MUL: the W rows of a tile alternate 32 gate rows and the 32 up
     // rows of the same output columns, so block pair (2i, 2i + 1) of a wave
     // holds gate and up values of one 32-column group in the same lanes.
-    static_assert(EPI == EPI_NONE || NI % 2 == 0, "gate/up pairs per wave");
+    static_assert(EPI != EPI_SILU_MUL || NI % 2 == 0, "gate/up pairs per wave");
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;   // output columns per tile
 
     // LDS: the ring of K-tile stages, reused after the K loop for the C tile.
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // inside the K loop shares the LDS counter with the fragment reads and
     // completes out of order, which would turn every fragment wait into
     // lgkmcnt(0).
-    asm volatile("" :: "s"(c), "s"(ldc), "s"(c_vec), "s"(m), "s"(n));
+    asm volatile("" :: "s"(c), "s"(ldc), "s"(c_vec), "s"(m), "s"(n), "s"(keys));
 
     int tm, tn;
     grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
@@ -281,6 +281,25 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         }
     }
     __syncthreads();
+    if constexpr (EPI == EPI_ARGMAX) {
+        // Greedy LM head: per row of the tile, the best of its BN columns
+        // (two threads per row, 64 columns each), one key per row.
+        static_assert(OB == 4 && NT == 2 * BM, "fp32 tile, two threads per row");
+        const int r = tid >> 1, h = tid & 1;
+        const float* rowp = reinterpret_cast<const float*>(ctile + r * PITCH);
+        uint64_t best = 0;
+        for (int cc = 0; cc < BN / 2; ++cc) {
+            const int col = h * (BN / 2) + cc;
+            if (n0 + col >= n) break;
+            const uint64_t key = argmax_key(rowp[col], n0 + col);
+            best = key > best ? key : best;
+        }
+        const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), 1))) << 32) |
+                               uint64_t(uint32_t(__shfl_xor(int(best & 0xFFFFFFFFu), 1)));
+        best = other > best ? other : best;
+        if (h == 0 && m0 + r < m) keys[(m0 + r) * int64_t(tiles_n) + tn] = best;
+        return;
+    }
     constexpr int EPC = 16 / OB;                 // output elements per chunk
     constexpr int ROWS_PER_PASS = NT / CPR;
     const int chunk = tid % CPR;
@@ -340,9 +359,10 @@ int launch_tile(const Problem& p, hipStream_t s) {
     const int out_bytes = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;
     // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
     const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && ((p.ldc * out_bytes) % 16 == 0);
+    if (EPI == EPI_ARGMAX) *p.key_blocks = tiles_n;
     hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c,
-                       p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec);
+                       p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec, p.keys);
     return check_launch("mfma_staged");
 }
 
@@ -363,6 +383,11 @@ int launch_typed(const Problem& p, hipStream_t s) {
 }  // namespace
 
 int launch_mfma_staged(const Problem& p, hipStream_t s) {
+    if (p.epi == EPI_ARGMAX) {
+        constexpr int F = NANOVLLM_GEMM_F32;
+        if (p.dtype_in == NANOVLLM_GEMM_BF16) return launch_epi<NANOVLLM_GEMM_BF16, F, EPI_ARGMAX>(p, s);
+        return launch_epi<NANOVLLM_GEMM_F16, F, EPI_ARGMAX>(p, s);
+    }
     if (p.dtype_in == NANOVLLM_GEMM_BF16) {
         if (p.dtype_out == NANOVLLM_GEMM_BF16) return launch_typed<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_BF16>(p, s);
         return launch_typed<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_F32>(p, s);

@@ -238,6 +238,71 @@ def silu_mul_selected_kernel(a: torch.Tensor, w: torch.Tensor, out_dtype: Option
     return _lib.kernel_name(kid)
 
 
+# ---------------------------------------------------------------------------
+# Greedy LM head: argmax of a @ w.T per row without the logits
+# ---------------------------------------------------------------------------
+def argmax_contract_reason(a: torch.Tensor, w: torch.Tensor) -> Optional[str]:
+    """Why the greedy head cannot take these inputs, or None if it can."""
+    reason = contract_reason(a, w, torch.float32 if a.dtype != torch.float32 else None)
+    if reason is not None:
+        return reason
+    if a.dtype not in (torch.float16, torch.bfloat16):
+        return "the greedy head takes float16 or bfloat16 inputs"
+    if w.shape[0] < 1:
+        return "w must have at least one row (vocabulary entry)"
+    if a.shape[-1] % 8:
+        return f"K ({a.shape[-1]}) must be a multiple of 8 for the greedy head"
+    if a.data_ptr() % 16 or w.data_ptr() % 16:
+        return "a and w must be 16-byte aligned for the greedy head"
+    return None
+
+
+def _launch_argmax(a: torch.Tensor, w: torch.Tensor, kernel: Optional[int] = None):
+    reason = argmax_contract_reason(a, w)
+    if reason is not None:
+        raise RuntimeError(f"nanovllm::gemm_argmax: {reason}")
+    k = a.shape[-1]
+    n = w.shape[0]
+    m = a.numel() // k
+    tokens = torch.empty(a.shape[:-1], dtype=torch.int64, device=a.device)
+    logits = torch.empty(a.shape[:-1], dtype=torch.float32, device=a.device)
+    if m == 0:
+        return tokens, logits
+    need = _lib.argmax_workspace_bytes(m, n, k, k, k, _CODE[a.dtype])
+    _lib.check(need if need < 0 else _lib.OK, "nanovllm_gemm_argmax_workspace_bytes")
+    workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+    with torch.cuda.device(a.device):
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+        _lib.argmax_raw(a.data_ptr(), w.data_ptr(), tokens.data_ptr(), logits.data_ptr(), m, n, k, k, k,
+                        _CODE[a.dtype], workspace.data_ptr(), need, stream, kernel)
+    return tokens, logits
+
+
+@torch.library.custom_op("nanovllm::gemm_argmax", mutates_args=())
+def _gemm_argmax_op(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return _launch_argmax(a, w)
+
+
+@_gemm_argmax_op.register_fake
+def _gemm_argmax_fake(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    torch._check(w.dim() == 2)
+    torch._check(a.shape[-1] == w.shape[1])
+    torch._check(a.dtype == w.dtype)
+    torch._check(a.device == w.device)
+    return (a.new_empty(a.shape[:-1], dtype=torch.int64), a.new_empty(a.shape[:-1], dtype=torch.float32))
+
+
+def gemm_argmax(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(argmax_j (a @ w.T)[..., j], that maximum in fp32), without the logits;
+    ties go to the first index, as in torch.argmax."""
+    return torch.ops.nanovllm.gemm_argmax(a, w)
+
+
+def gemm_argmax_with_kernel(a: torch.Tensor, w: torch.Tensor, kernel: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The greedy head with its GEMM pass on one named kernel."""
+    return _launch_argmax(a, w, kernel)
+
+
 def validate_gemm_backend(backend: str) -> str:
     """Normalise a backend name (pattern of validate_gdn_decode_backend, gdn.py:13)."""
     value = str(backend).strip().lower()
@@ -298,3 +363,22 @@ def silu_mul_linear(x: torch.Tensor, weight: torch.Tensor, *, backend: Optional[
             return _torch_silu_mul(x, weight)
         raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
     return gemm_silu_mul(x, weight)
+
+
+def greedy_linear(x: torch.Tensor, weight: torch.Tensor, *,
+                  backend: Optional[str] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(argmax, max) of F.linear(x, weight) in fp32 along the last dim, with
+    the backend switch of ``linear``: ``torch`` computes the fp32 logits and
+    takes torch.argmax (Sampler's greedy branch, sampler.py:19-32), ``hip``
+    runs the fused greedy head, ``auto`` the fused head when its contract
+    holds."""
+    backend = validate_gemm_backend(backend) if backend is not None else default_backend()
+    if backend != "torch":
+        reason = argmax_contract_reason(x, weight)
+        if reason is None:
+            return gemm_argmax(x, weight)
+        if backend == "hip":
+            raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
+    logits = F.linear(x, weight).float()
+    tokens = logits.argmax(dim=-1)
+    return tokens, logits.gather(-1, tokens.unsqueeze(-1)).squeeze(-1)

@@ -20,6 +20,7 @@ import torch
 import torch.distributed as dist
 from torch import nn
 
+from ..kernels import greedy_linear
 from ..kernels import linear as gemm_linear
 
 
@@ -188,6 +189,33 @@ class ParallelLMHead(nn.Module):
             dist.gather(logits, all_logits, 0)
             logits = torch.cat(all_logits, -1) if self.tp_rank == 0 else None
         return logits
+
+    def greedy(self, x: torch.Tensor, last_indices: Optional[torch.Tensor] = None):
+        """Greedy tokens without the logits: the temperature-0 branch of
+        Sampler (nanovllm/layers/sampler.py:19-32, argmax of the fp32 logits,
+        first index on ties) applied to this head's output.  Returns (token
+        ids int64, their fp32 logits); on the HIP path one fused launch
+        replaces the [M, vocab] logits write and the argmax read-back.  With
+        tensor parallelism every rank finds the best token of its vocabulary
+        shard and rank 0 keeps the best pair, the lower rank on equal logits
+        (the first index of the gathered logits); other ranks return None."""
+        if last_indices is not None:
+            x = x[last_indices].contiguous()
+        tokens, values = greedy_linear(x, self.weight, backend=self.gemm_backend)
+        if self.tp_size > 1:
+            tokens = tokens + self.vocab_start_idx
+            rank0 = self.tp_rank == 0
+            all_tokens = [torch.empty_like(tokens) for _ in range(self.tp_size)] if rank0 else None
+            all_values = [torch.empty_like(values) for _ in range(self.tp_size)] if rank0 else None
+            dist.gather(tokens, all_tokens, 0)
+            dist.gather(values, all_values, 0)
+            if not rank0:
+                return None, None
+            stacked_values = torch.stack(all_values, 0)
+            best = stacked_values.argmax(0, keepdim=True)
+            tokens = torch.stack(all_tokens, 0).gather(0, best).squeeze(0)
+            values = stacked_values.gather(0, best).squeeze(0)
+        return tokens, values
 
 
 class GemmLinear(nn.Linear):

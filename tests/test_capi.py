@@ -208,3 +208,49 @@ def test_silu_mul_validates_before_launch(lib):
     # unaligned pointers: only the vector path exists for the fused op
     rc = lib.nanovllm_gemm_silu_mul(dummy + 2, dummy, dummy, 4, 8, 16, 16, 16, 8, BF16, BF16, None)
     assert rc == L.EUNSUPPORTED and "aligned" in L.last_error()
+
+
+# ---------------------------------------------------------------------------
+# Greedy LM head (argmax without logits)
+# ---------------------------------------------------------------------------
+def test_argmax_workspace_and_selection():
+    for m, n in itertools.product([1, 7, 32, 33, 512], [1, 15, 16, 17, 151936]):
+        cols = 16 if m <= 32 else 128
+        assert L.argmax_workspace_bytes(m, n, 1024, 1024, 1024, BF16) == -(-n // cols) * m * 8
+        want = L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
+        assert L.argmax_select(m, n, 1024, 1024, 1024, BF16, True) == want
+        assert L.argmax_select(m, n, 1024, 1024, 1024, F16, False) == L.EUNSUPPORTED
+    assert L.argmax_select(4, 100, 1000 + 4, 1004, 1004, BF16, True) == L.EUNSUPPORTED   # k % 8 != 0
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    (dict(din=F32), L.EUNSUPPORTED, "float16 or bfloat16"),
+    (dict(din=9), L.EINVAL, "float16 or bfloat16"),
+    (dict(n=0), L.EINVAL, "n must be in"),
+    (dict(n=2 ** 32), L.EINVAL, "n must be in"),
+    (dict(k=0), L.EINVAL, "k must be positive"),
+    (dict(ldw=8), L.EINVAL, "ldw"),
+    (dict(m=-2), L.EINVAL, "non-negative"),
+])
+def test_argmax_rejects_invalid(args, code, msg):
+    m, n, k = args.get("m", 4), args.get("n", 64), args.get("k", 16)
+    rc = L.argmax_workspace_bytes(m, n, k, args.get("lda", k), args.get("ldw", k), args.get("din", BF16))
+    assert rc == code and msg in L.last_error()
+
+
+def test_argmax_validates_before_launch(lib):
+    assert lib.nanovllm_gemm_argmax(None, None, None, None, 0, 64, 16, 16, 16, BF16, None, 0, None) == L.OK
+    rc = lib.nanovllm_gemm_argmax(None, None, None, None, 4, 64, 16, 16, 16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "non-null" in L.last_error()
+    dummy = 1 << 20
+    need = L.argmax_workspace_bytes(4, 64, 16, 16, 16, BF16)
+    rc = lib.nanovllm_gemm_argmax(dummy, dummy, dummy, None, 4, 64, 16, 16, 16, BF16, dummy, need - 8, None)
+    assert rc == L.EINVAL and f"needs {need}" in L.last_error()
+    rc = lib.nanovllm_gemm_argmax(dummy, dummy, dummy, None, 4, 64, 16, 16, 16, BF16, dummy + 4, need, None)
+    assert rc == L.EINVAL and "8-byte aligned" in L.last_error()
+    rc = lib.nanovllm_gemm_argmax_with_kernel(L.KERNEL_GEMV_DECODE, dummy, dummy, dummy, None, 4, 64, 16, 16, 16,
+                                              BF16, dummy, need, None)
+    assert rc == L.EUNSUPPORTED and "gemv_decode" in L.last_error()
+    rc = lib.nanovllm_gemm_argmax_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, None, 33, 64, 16, 16, 16,
+                                              BF16, dummy, 10 ** 6, None)
+    assert rc == L.EUNSUPPORTED

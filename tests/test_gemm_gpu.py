@@ -474,3 +474,71 @@ def test_silu_mul_contract_errors_on_gpu():
     assert misaligned.is_contiguous() and misaligned.data_ptr() % 16 == 2
     with pytest.raises(RuntimeError, match="aligned"):
         G.gemm_silu_mul(misaligned, torch.randn(8, 64, device=DEV, dtype=torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# Greedy LM head (argmax without logits)
+# ---------------------------------------------------------------------------
+ARGMAX_CASES = [(L.KERNEL_SPLITK_DECODE, m) for m in (1, 5, 17, 32)] + [(L.KERNEL_MFMA_STAGED, m) for m in (1, 33, 300)]
+
+
+@pytest.mark.parametrize("kernel,m", ARGMAX_CASES, ids=[f"{L.kernel_name(k)}-M{m}" for k, m in ARGMAX_CASES])
+@pytest.mark.parametrize("n", [1000, 70001])
+@pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_argmax_equals_argmax_of_own_logits(kernel, m, n, din):
+    """The greedy head and the fp32-output GEMM on the same kernel compute the
+    same fp32 logits, so the tokens are exactly torch.argmax of those logits
+    (first index on ties; rows 3 and n - 2 of W are copies of row 1, so some
+    logits tie exactly) and the values exactly the chosen logits; the tokens
+    are also admissible against the float64 logits."""
+    gen = torch.Generator().manual_seed(m * 7 + n)
+    k = 256
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    w[3] = w[1]
+    w[n - 2] = w[1]
+    a[0] = w[1] * 4        # row 0's best token is 1, tied with 3 and n - 2
+    ad, wd = a.to(DEV), w.to(DEV)
+    _say(f"argmax {L.kernel_name(kernel)} {NAME[din]} M={m} N={n}")
+    tokens, values = G.gemm_argmax_with_kernel(ad, wd, kernel)
+    logits = G.gemm_with_kernel(ad, wd, kernel, torch.float32)
+    torch.cuda.synchronize()
+    assert tokens.dtype == torch.int64 and values.dtype == torch.float32
+    assert torch.equal(tokens, logits.argmax(-1))
+    assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
+    assert int(tokens[0]) == 1
+    a64, w64 = a.double().numpy(), w.double().numpy()
+    r = orc.gemm_f64(a64, w64)
+    assert orc.greedy_token_admissible(tokens.cpu().numpy(), r, orc.abs_products_f64(a64, w64), k).all()
+
+
+@pytest.mark.parametrize("m", [1, 32])
+def test_argmax_lm_head_shape_and_graph(m):
+    """Qwen3.5 LM head (151936 x 1024): the selected path, then captured in a
+    HIP graph (workspace from the graph's pool) and replayed."""
+    gen = torch.Generator().manual_seed(70 + m)
+    a = torch.randn((m, 1024), generator=gen).bfloat16().to(DEV)
+    w = (torch.randn((151936, 1024), generator=gen) * 0.02).bfloat16().to(DEV)
+    _say(f"argmax lm head M={m}")
+    tokens, values = G.gemm_argmax(a, w)
+    logits = G.gemm(a, w, torch.float32)      # same splitk configuration at these shapes
+    torch.cuda.synchronize()
+    assert torch.equal(tokens, logits.argmax(-1))
+    assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
+    a_static = a.clone()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        G.gemm_argmax(a_static, w)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        t_static, v_static = G.gemm_argmax(a_static, w)
+    for step in range(3):
+        x = torch.randn((m, 1024), generator=gen).bfloat16().to(DEV)
+        a_static.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        t_eager, v_eager = G.gemm_argmax(x, w)
+        torch.cuda.synchronize()
+        assert torch.equal(t_static, t_eager) and torch.equal(v_static, v_eager), f"replay {step}"

@@ -107,6 +107,25 @@ def test_gdn_projection_matches_four_linears(dims):
         proj.weight.weight_loader(proj.weight, full["z"], "v")
 
 
+def test_lm_head_greedy_matches_argmax_of_logits():
+    """Sampler's greedy branch: argmax of the fp32 logits, first index on ties
+    (two vocabulary rows are duplicated so their logits tie exactly)."""
+    head = Lyr.ParallelLMHead(50, 16)
+    w = torch.randn(50, 16, generator=torch.Generator().manual_seed(4))
+    w[31] = w[7]
+    head.weight.weight_loader(head.weight, w)
+    head.gemm_backend = "auto"
+    x = torch.randn(6, 16)
+    x[2] = w[7] * 3.0           # row 2 prefers token 7, tied with token 31
+    tokens, values = head.greedy(x)
+    logits = head(x)
+    assert torch.equal(tokens, logits.argmax(-1))
+    assert int(tokens[2]) == 7
+    torch.testing.assert_close(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
+    t2, _ = head.greedy(torch.randn(9, 16), last_indices=torch.tensor([0, 8]))
+    assert t2.shape == (2,)
+
+
 def test_qwen35_mlp_matches_reference_composition():
     """down_proj(SiluAndMul(gate_up_proj(x))) of models/qwen3_5.py:117-118; on
     CPU tensors the auto backend takes the reference composition."""
@@ -175,6 +194,23 @@ def _tp_worker(rank, world, init_file, result_file):
         proj.gemm_backend = "auto"
         xg = torch.randn(3, 8)
         ok = ok and torch.allclose(torch.cat(proj(xg), dim=-1), F.linear(xg, want), rtol=1e-6, atol=1e-5)
+        # Greedy head across vocabulary shards: the best token overall, the
+        # lower shard on a tie (token 5 of rank 0 and token 25 of rank 1
+        # have equal logits).
+        gh = Lyr.ParallelLMHead(40, k)
+        wt = torch.randn(40, k, generator=torch.Generator().manual_seed(12))
+        wt[25] = wt[5]
+        gh.weight.weight_loader(gh.weight, wt)
+        gh.gemm_backend = "auto"
+        xt = torch.randn(4, k, generator=torch.Generator().manual_seed(13))
+        xt[1] = wt[5] * 2.0
+        gt, gv = gh.greedy(xt)
+        if rank == 0:
+            full = F.linear(xt, wt)
+            ok = ok and torch.equal(gt, full.argmax(-1)) and int(gt[1]) == 5
+            ok = ok and torch.allclose(gv, full.max(-1).values, rtol=1e-6, atol=1e-6)
+        else:
+            ok = ok and gt is None and gv is None
         with open(f"{result_file}.{rank}", "w") as fh:
             fh.write("ok" if ok else "mismatch")
     finally:
@@ -185,6 +221,8 @@ def test_tensor_parallel_two_ranks_gloo():
     with tempfile.TemporaryDirectory() as tmp:
         init_file = os.path.join(tmp, "init")
         result = os.path.join(tmp, "result")
-        mp.start_processes(_tp_worker, args=(2, init_file, result), nprocs=2, start_method="fork")
+        # spawn, not fork: earlier tests in this process may have started
+        # torch's OpenMP pool, and a forked child entering it can deadlock.
+        mp.start_processes(_tp_worker, args=(2, init_file, result), nprocs=2, start_method="spawn")
         for r in range(2):
             assert open(f"{result}.{r}").read() == "ok", f"rank {r}"

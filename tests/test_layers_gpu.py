@@ -183,3 +183,20 @@ def test_qwen35_mlp_fused_graph_capture(m):
     mlp.gemm_backend = "torch"
     ref = mlp(x).float()
     assert torch.allclose(eager.float(), ref, rtol=0.05, atol=0.02)
+
+
+@torch.inference_mode()
+@pytest.mark.parametrize("m", [1, 8, 32])
+def test_lm_head_greedy_hip(m):
+    """ParallelLMHead.greedy on the HIP path equals the argmax of the head's
+    own fp32 logits (same kernel configuration for the Qwen3.5 vocabulary)."""
+    gen = torch.Generator().manual_seed(80 + m)
+    head = _init(Lyr.ParallelLMHead(151936, 1024), gen).to(DEV, torch.bfloat16)
+    head.gemm_backend = "hip"
+    x = torch.randn(m + 3, 1024, generator=gen).bfloat16().to(DEV)
+    last = torch.arange(m, device=DEV) + 3
+    tokens, values = head.greedy(x, last)
+    logits = head(x, last)
+    torch.cuda.synchronize()
+    assert torch.equal(tokens, logits.argmax(-1))
+    assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
