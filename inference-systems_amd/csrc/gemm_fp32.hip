@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     for (int v = 0; v < 16; ++v) {
         const int64_t row = m0 + wm * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
         const int64_t col = n0 + bj;
-        if (row < m && col < n) c[row * ldc + col] = acc[v];
+        if (row < m && col < n) __builtin_nontemporal_store(acc[v], c + row * ldc + col);
     }
 }
 

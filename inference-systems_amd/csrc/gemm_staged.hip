@@ -246,6 +246,10 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // the 32 rows one store instruction touches spread over the banks), then
     // all 256 threads copy the tile out row by row, 16 bytes per lane, so
     // every global store instruction writes whole 512-byte row segments.
+    // The copy-out stores are non-temporal: C is written once and not read
+    // back by this launch, so it is kept out of L2 where it would evict the
+    // A and W tiles other workgroups still read (2048 x 4096 x 1024 bf16:
+    // 21.4 -> 19.6 us).
     constexpr int CPR = BNO * OB / 16;                           // 16-byte chunks per row
     static_assert(NT % CPR == 0, "rows per copy pass");
     char* ctile = reinterpret_cast<char*>(ring);
@@ -310,7 +314,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         for (int pass = 0; pass < BM / ROWS_PER_PASS; ++pass) {
             const int r = tid / CPR + pass * ROWS_PER_PASS;
             const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ctile + r * PITCH + chunk * 16);
-            *reinterpret_cast<u32x4_t*>(static_cast<char*>(c) + ((m0 + r) * ldc + n0 + chunk * EPC) * OB) = val;
+            __builtin_nontemporal_store(
+                val, reinterpret_cast<u32x4_t*>(static_cast<char*>(c) + ((m0 + r) * ldc + n0 + chunk * EPC) * OB));
         }
         return;
     }
@@ -321,7 +326,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ctile + r * PITCH + chunk * 16);
         char* gdst = static_cast<char*>(c) + (grow * ldc + gcol) * OB;
         if (c_vec && gcol + EPC <= n) {
-            *reinterpret_cast<u32x4_t*>(gdst) = val;
+            __builtin_nontemporal_store(val, reinterpret_cast<u32x4_t*>(gdst));
         } else {
             const int valid = int(min_i64(EPC, n - gcol));
             if constexpr (OB == 4) {
