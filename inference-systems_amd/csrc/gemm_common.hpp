@@ -124,6 +124,38 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c
     }
 }
 
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their no-wait maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const u32x4_t* p) {
+    typedef const __attribute__((address_space(3))) u32x4_t* lds_ptr;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)p));
+}
+
+// One global_load_lds_dwordx4: lane L copies 16 bytes from its `src` to LDS
+// bytes lds + 16 L .. lds + 16 L + 15 (lds must be wave-uniform).
+//
+// Written as inline assembly rather than __builtin_amdgcn_global_load_lds:
+// the compiler models that builtin as pending on both the vector-memory and
+// the LDS counters, so while a prefetch is in flight every wait it inserts
+// for a fragment ds_read becomes lgkmcnt(0), which drains the reads of the
+// next K-step too and serialises LDS reads with the MFMAs.  On gfx950 the
+// instruction completes on vmcnt alone (measured: lgkmcnt(0) after it does
+// not wait for the data), so the kernels wait on vmcnt explicitly before
+// reading what it wrote.  Nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // 16-byte global load.
 __device__ __forceinline__ u32x4_t load16(const void* p) {
     return *static_cast<const u32x4_t*>(p);

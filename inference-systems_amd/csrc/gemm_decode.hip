@@ -2,17 +2,28 @@
 // with W[N,K] in the nn.Linear layout.  At these shapes the work is
 // streaming W once from HBM (N*K*2 bytes) while A (M*K*2 bytes, at most
 // 64 KiB) stays in L2.  Design:
-//   * one workgroup per 16 rows of W (4 waves; M <= 8), per 32 rows (8
-//     waves; 8 < M <= 32, so each A fragment serves two W row groups) or,
-//     for very wide W, per 64 rows (4 waves); the waves split K, taking
-//     32-element K-steps round robin, so together they read contiguous runs
-//     of each W row;
-//   * each lane issues its W loads for several K-steps (8 x 16 B for K = 1024
-//     with 4 waves) before the first MFMA, so W is in flight almost at once;
-//   * v_mfma_f32_16x16x32 with W as the first operand (16 rows of W) and up
-//     to two 16-row groups of A as the second; rows of A past M are zero;
-//   * the four per-wave partial tiles are summed in LDS in a fixed order
-//     (deterministic, no atomics, no workspace) and written once.
+//   * one workgroup per 16 * RG rows of W; its waves split K, taking
+//     64-element lines (128 bytes of a row) round robin, LPB lines at a time;
+//   * W and A reach LDS by global_load_lds_dwordx4 in whole 128-byte lines:
+//     one instruction copies one line of each of 8 rows.  The MFMA fragment
+//     layout (lane l holds row l % 16) would have each load instruction touch
+//     16 rows x 64 bytes; on MI355X a load instruction costs by the cache
+//     lines it touches, and a 12.6 MB W streamed as whole lines takes
+//     ~0.8 us less than as half lines (4.05 against 4.85 us, same grid);
+//   * lane L of a copy writes LDS slot L, row L / 8, and fetches chunk
+//     (L % 8) ^ (L / 8) of its row's line, so a fragment read (16 rows, one
+//     chunk) hits 8 distinct 16-byte slots in every group of 8 lanes;
+//   * each wave reads back only what it copied (no barrier in the K loop),
+//     v_mfma_f32_16x16x32 with W as the first operand (16 rows of W) and up
+//     to two 16-row groups of A as the second; rows of A past M repeat row
+//     M - 1 and their outputs are not stored;
+//   * line L is accumulated into K partition L % PARTS, each wave owning
+//     PARTS / WAVES partitions, and the partition sums are added in LDS in
+//     partition order (deterministic, no atomics, no workspace) and written
+//     once.  The order of every sum depends on PARTS alone, so all
+//     configurations with PARTS = 16 (every W of fewer than 65536 rows)
+//     give bit-identical results for a given row of A and row of W, whatever
+//     N: a merged projection equals its separate parts.
 // It replaces the reference's cuBLAS fallback for decode shapes and the
 // M == 16 direct-WMMA special case (cuda_kernels/gemm/src/gemm_bench.cu:260-273).
 #include "gemm_common.hpp"
@@ -20,109 +31,184 @@
 namespace nvg {
 namespace {
 
-constexpr int kDecStep = 32;   // K elements per MFMA
+constexpr int kLine = 64;   // K elements per line: 128 bytes = 8 chunks of 16 bytes
 
-// RG groups of 16 W rows per workgroup, WAVES waves splitting K round robin,
-// MG groups of 16 A rows, UNROLL K-steps whose loads are issued together.
-template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL, int EPI>
+// Source of the K-tail chunks: 16 zero bytes in global memory.
+__device__ u32x4_t g_decode_zero = {0u, 0u, 0u, 0u};
+
+// RG groups of 16 W rows per workgroup, AROWS rows of A copied per line
+// (8, 16 or 32: M rounded up), WAVES waves splitting K, LPB lines per wave
+// in flight at once, PARTS K partitions (a multiple of WAVES).
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys) {
-    __shared__ float red[WAVES][RG][MG][16][16];
+    static_assert(AROWS == 8 || AROWS == 16 || AROWS == 32, "rows of A per line");
+    constexpr int MG = AROWS == 32 ? 2 : 1;   // 16-row groups of A in the MFMA
+    constexpr int IW = 2 * RG;                 // W copies per line (8 rows each)
+    constexpr int IA = AROWS / 8;              // A copies per line
+    constexpr int IL = IW + IA;
+    static_assert(LPB * IL < 64, "vmcnt range");
+    static_assert(PARTS % WAVES == 0, "whole partitions per wave");
+    constexpr int PW = PARTS / WAVES;                  // partitions per wave
+    constexpr int ROUND = LPB > PW ? LPB : PW;         // lines per wave per loop trip
+    static_assert(ROUND % LPB == 0 && ROUND % PW == 0, "copy batches and partitions tile a trip");
+    // Per wave: LPB lines x IL copies x 64 lanes x 16 bytes.  After the K
+    // loop a wave's region holds its partition sums for the final addition.
+    constexpr int REGION = LPB * IL * 64;
+    static_assert(PW * RG * MG * 256 <= 4 * REGION, "partition tiles fit in a wave's region");
+    __shared__ u32x4_t buf[WAVES][REGION];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int i16 = lane & 15;   // W row (first operand) / A row (second operand)
-    const int grp = lane >> 4;   // which 8-element chunk of the 32-wide K-step
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i16 = lane & 15;   // fragment row (W: first operand, A: second)
+    const int grp = lane >> 4;   // fragment chunk within the 32-wide K-step
+    const int r8 = lane >> 3;    // copy: row within the instruction's 8
+    const int chunk = (lane & 7) ^ r8;   // copy: chunk of the line this lane fetches
 
     // EPI_SILU_MUL: W-row groups pair up, group 2s holding gate rows and
     // group 2s + 1 the up rows of the same 16 output columns.
     static_assert(EPI != EPI_SILU_MUL || RG % 2 == 0, "gate/up group pairs");
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;   // 16-column output groups per workgroup
     const int64_t n0 = int64_t(blockIdx.x) * 16 * OG;         // first output column
-    const uint16_t* wp[RG];
+    const uint16_t* wsrc[IW];
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
+    for (int h = 0; h < IW; ++h) {
+        const int r = h >> 1;
+        const int64_t rr = 8 * (h & 1) + r8;
         if constexpr (EPI == EPI_SILU_MUL)
-            wp[r] = w + ((r & 1) ? n : 0) * ldb + min_i64(n0 + 16 * (r >> 1) + i16, n - 1) * ldb + grp * 8;
+            wsrc[h] = w + ((r & 1) ? n : 0) * ldb + min_i64(n0 + 16 * (r >> 1) + rr, n - 1) * ldb + chunk * 8;
         else
-            wp[r] = w + min_i64(n0 + 16 * r + i16, n - 1) * ldb + grp * 8;
+            wsrc[h] = w + min_i64(n0 + 16 * r + rr, n - 1) * ldb + chunk * 8;
     }
-    const uint16_t* ap[MG];
-    bool a_in[MG];
+    const uint16_t* asrc[IA];
 #pragma unroll
-    for (int g = 0; g < MG; ++g) {
-        const int64_t arow = g * 16 + i16;
-        a_in[g] = arow < m;
-        ap[g] = a + (a_in[g] ? arow : 0) * lda + grp * 8;
+    for (int h = 0; h < IA; ++h) asrc[h] = a + min_i64(8 * h + r8, m - 1) * lda + chunk * 8;
+    const void* zero = &g_decode_zero;
+    asm volatile("" : "+s"(zero));
+
+    // Fragment slots: row i16 of a 16-row group sits in copy 2 g + i16 / 8,
+    // slot 8 (i16 % 8) + (chunk ^ (i16 % 8)), for chunk grp (first 32-wide
+    // K-step of the line) and 4 + grp (second).
+    const int x = i16 & 7, hi = i16 >> 3;
+    const int slot0 = 8 * x + (grp ^ x), slot1 = 8 * x + ((4 + grp) ^ x);
+
+    const int64_t lines = (k + kLine - 1) / kLine;
+    const uint32_t base = lds_address(&buf[wave][0]);
+    f32x4_t acc[PW][RG][MG];
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int r = 0; r < RG; ++r)
+#pragma unroll
+            for (int g = 0; g < MG; ++g) acc[q][r][g] = f32x4_t{};
+
+    // Wave w takes lines w + WAVES j, j = 0, 1, ...: line j of a trip goes to
+    // partition w + WAVES (j % PW), in batches of LPB copied together.
+    for (int64_t l0 = wave; l0 < lines; l0 += int64_t(WAVES) * ROUND) {
+#pragma unroll
+        for (int bt = 0; bt < ROUND / LPB; ++bt) {
+            if (l0 + int64_t(WAVES) * (bt * LPB) >= lines) break;
+#pragma unroll
+            for (int t = 0; t < LPB; ++t) {
+                const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
+                if (line >= lines) break;
+                const uint32_t dst = base + uint32_t(t * IL) * 1024u;
+                const int64_t koff = line * kLine;
+                if (koff + kLine <= k) {
+#pragma unroll
+                    for (int h = 0; h < IW; ++h) dma16(wsrc[h] + koff, dst + 1024u * h);
+#pragma unroll
+                    for (int h = 0; h < IA; ++h) dma16(asrc[h] + koff, dst + 1024u * (IW + h));
+                } else {
+                    // K tail (K % 8 == 0): chunks past K copy zeros into W and A.
+                    const bool in_k = koff + chunk * 8 < k;
+#pragma unroll
+                    for (int h = 0; h < IW; ++h)
+                        dma16(in_k ? static_cast<const void*>(wsrc[h] + koff) : zero, dst + 1024u * h);
+#pragma unroll
+                    for (int h = 0; h < IA; ++h)
+                        dma16(in_k ? static_cast<const void*>(asrc[h] + koff) : zero, dst + 1024u * (IW + h));
+                }
+            }
+            wait_vmcnt<0>();
+#pragma unroll
+            for (int t = 0; t < LPB; ++t) {
+                if (l0 + int64_t(WAVES) * (bt * LPB + t) >= lines) break;
+                const int q = (bt * LPB + t) % PW;   // compile-time after unrolling
+                const u32x4_t* lb = &buf[wave][t * IL * 64];
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const int slot = st ? slot1 : slot0;
+                    u32x4_t wf[RG], af[MG];
+#pragma unroll
+                    for (int r = 0; r < RG; ++r) wf[r] = lb[(2 * r + hi) * 64 + slot];
+#pragma unroll
+                    for (int g = 0; g < MG; ++g) af[g] = lb[(IW + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot];
+#pragma unroll
+                    for (int r = 0; r < RG; ++r)
+#pragma unroll
+                        for (int g = 0; g < MG; ++g)
+                            acc[q][r][g] = mfma_16x16x32<DT>(wf[r], af[g], acc[q][r][g]);
+                }
+            }
+            // The next lines' copies overwrite the slots just read.
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
     }
 
-    const int64_t steps = (k + kDecStep - 1) / kDecStep;
-    f32x4_t acc[RG][MG];
+    // acc[q][r][g][v] is D[n = 4*(l/16) + v][m = l%16] of W-row group r,
+    // A-row group g, in partition wave + WAVES q.  Each wave writes its
+    // partition tiles to its own region (its last reads of it completed at
+    // the wait above); partition p then sits in wave p % WAVES, slot
+    // p / WAVES.  Within a 16 x 16 tile, (n, m) is stored at 16 n + (m ^ n):
+    // the writes (16 lanes along m) and the reads below (16 lanes along n)
+    // both hit 16 distinct banks.
+    auto part = [&](int wv, int q, int r, int g, int nn, int mm) -> float& {
+        return reinterpret_cast<float*>(&buf[wv][0])[(((q * RG + r) * MG + g) * 16 + nn) * 16 + (mm ^ nn)];
+    };
 #pragma unroll
-    for (int r = 0; r < RG; ++r)
+    for (int q = 0; q < PW; ++q)
 #pragma unroll
-        for (int g = 0; g < MG; ++g) acc[r][g] = f32x4_t{};
-
-    for (int64_t s0 = wave; s0 < steps; s0 += WAVES * UNROLL) {
-        u32x4_t wf[RG][UNROLL];
-        u32x4_t af[MG][UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            const int64_t ks = (s0 + WAVES * u) * kDecStep;
-            const bool in_k = ks + grp * 8 < k;  // K % 8 == 0: a chunk is all in or all out
-#pragma unroll
-            for (int r = 0; r < RG; ++r) wf[r][u] = in_k ? load16(wp[r] + ks) : u32x4_t{0u, 0u, 0u, 0u};
+        for (int r = 0; r < RG; ++r)
 #pragma unroll
             for (int g = 0; g < MG; ++g)
-                af[g][u] = (in_k && a_in[g]) ? load16(ap[g] + ks) : u32x4_t{0u, 0u, 0u, 0u};
-        }
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-            for (int r = 0; r < RG; ++r)
-#pragma unroll
-                for (int g = 0; g < MG; ++g) acc[r][g] = mfma_16x16x32<DT>(wf[r][u], af[g][u], acc[r][g]);
-    }
-
-    // acc[r][g][v] is D[n = 4*(l/16) + v][m = l%16] of W-row group r, A-row group g.
-#pragma unroll
-    for (int r = 0; r < RG; ++r)
-#pragma unroll
-        for (int g = 0; g < MG; ++g)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) red[wave][r][g][4 * grp + v][i16] = acc[r][g][v];
+                for (int v = 0; v < 4; ++v) part(wave, q, r, g, 4 * grp + v, i16) = acc[q][r][g][v];
     __syncthreads();
+    // Sum of the partitions in partition order.
+    auto total = [&](int r, int g, int nn, int mm) {
+        float sum = part(0, 0, r, g, nn, mm);
+#pragma unroll
+        for (int pp = 1; pp < PARTS; ++pp) sum += part(pp % WAVES, pp / WAVES, r, g, nn, mm);
+        return sum;
+    };
 
     if constexpr (EPI == EPI_ARGMAX) {
-        // Per row of A, the best of this workgroup's 16 * RG columns: the
-        // sums go to LDS, then one thread per row scans them.
-        __shared__ float vals[MG * 16][16 * RG + 1];
-        for (int e = threadIdx.x; e < RG * MG * 256; e += WAVES * 64) {
-            const int r = e / (MG * 256);
-            const int g = (e / 256) % MG;
-            const int nn = e & 15;
-            const int mm = (e >> 4) & 15;
-            float sum = red[0][r][g][nn][mm];
+        // Per row of A, the best of this workgroup's 16 * RG columns: TPR
+        // adjacent threads per row each take every TPR-th column, then a
+        // butterfly over those lanes (keys order by value, then by lowest
+        // column, so the result does not depend on the split).
+        constexpr int ROWS = MG * 16;
+        constexpr int TPR = WAVES * 64 / ROWS;
+        static_assert(TPR >= 1 && TPR <= 64 && (TPR & (TPR - 1)) == 0, "a row's threads share a wave");
+        const int row = threadIdx.x / TPR, sub = threadIdx.x % TPR;
+        uint64_t best = 0;
+        for (int cc = sub; cc < 16 * RG; cc += TPR) {
+            if (n0 + cc >= n) break;
+            const uint64_t key = argmax_key(total(cc >> 4, row >> 4, cc & 15, row & 15), n0 + cc);
+            best = key > best ? key : best;
+        }
 #pragma unroll
-            for (int wv = 1; wv < WAVES; ++wv) sum += red[wv][r][g][nn][mm];
-            vals[g * 16 + mm][16 * r + nn] = sum;
+        for (int off = TPR / 2; off >= 1; off >>= 1) {
+            const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), off))) << 32) |
+                                   uint64_t(uint32_t(__shfl_xor(int(best & 0xFFFFFFFFu), off)));
+            best = other > best ? other : best;
         }
-        __syncthreads();
-        const int row = threadIdx.x;
-        if (row < MG * 16 && row < m) {
-            uint64_t best = 0;
-            for (int cc = 0; cc < 16 * RG; ++cc) {
-                if (n0 + cc >= n) break;
-                const uint64_t key = argmax_key(vals[row][cc], n0 + cc);
-                best = key > best ? key : best;
-            }
-            keys[row * int64_t(gridDim.x) + blockIdx.x] = best;
-        }
+        if (sub == 0 && row < m) keys[row * int64_t(gridDim.x) + blockIdx.x] = best;
         return;
     }
 
-    // Sum the per-wave partials in wave order (deterministic) and store.
     for (int e = threadIdx.x; e < OG * MG * 256; e += WAVES * 64) {
         const int o = e / (MG * 256);
         const int g = (e / 256) % MG;
@@ -130,91 +216,152 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
         const int mm = (e >> 4) & 15;
         const int64_t row = g * 16 + mm;
         const int64_t col = n0 + 16 * o + nn;
-        if constexpr (EPI == EPI_SILU_MUL) {
-            float gate = red[0][2 * o][g][nn][mm], up = red[0][2 * o + 1][g][nn][mm];
-#pragma unroll
-            for (int wv = 1; wv < WAVES; ++wv) {
-                gate += red[wv][2 * o][g][nn][mm];
-                up += red[wv][2 * o + 1][g][nn][mm];
-            }
-            if (row < m && col < n) store_elem<DT_OUT>(c, row * ldc + col, silu_f32(gate) * up);
-        } else {
-            float sum = red[0][o][g][nn][mm];
-#pragma unroll
-            for (int wv = 1; wv < WAVES; ++wv) sum += red[wv][o][g][nn][mm];
-            if (row < m && col < n) store_elem<DT_OUT>(c, row * ldc + col, sum);
-        }
+        if (row >= m || col >= n) continue;
+        if constexpr (EPI == EPI_SILU_MUL)
+            store_elem<DT_OUT>(c, row * ldc + col, silu_f32(total(2 * o, g, nn, mm)) * total(2 * o + 1, g, nn, mm));
+        else
+            store_elem<DT_OUT>(c, row * ldc + col, total(o, g, nn, mm));
     }
 }
 
-template <int DT, int DT_OUT, int MG, int RG, int WAVES, int UNROLL, int EPI = EPI_NONE>
+// M = 1 on very wide W (the LM head): 16 W rows per 4-wave workgroup, the
+// MFMA fragments loaded straight into registers, eight 16-byte loads per
+// lane in flight.  Its loads touch 16 half-lines each, but with ~9500
+// workgroups at full occupancy it keeps more bytes in flight than the
+// LDS-staged kernel can (N = 151936: 48.4 us, 80% of HBM, against 50.9 us
+// for the best LDS-staged configuration).  EPI_NONE or EPI_ARGMAX.
+constexpr int kRegWaves = 4, kRegUnroll = 8, kRegStep = 32;
+
+template <int DT, int DT_OUT, int EPI>
+__global__ __launch_bounds__(kRegWaves * 64) void splitk_regs_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
+    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys) {
+    static_assert(EPI != EPI_SILU_MUL, "gate/up pairs need the LDS-staged kernel");
+    __shared__ float red[kRegWaves][16][16];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int i16 = lane & 15;
+    const int grp = lane >> 4;
+    const int64_t n0 = int64_t(blockIdx.x) * 16;
+    const uint16_t* wp = w + min_i64(n0 + i16, n - 1) * ldb + grp * 8;
+    const bool a_in = i16 < m;
+    const uint16_t* ap = a + (a_in ? i16 : 0) * lda + grp * 8;
+    const int64_t steps = (k + kRegStep - 1) / kRegStep;
+    f32x4_t acc = f32x4_t{};
+    for (int64_t s0 = wave; s0 < steps; s0 += kRegWaves * kRegUnroll) {
+        u32x4_t wf[kRegUnroll], af[kRegUnroll];
+#pragma unroll
+        for (int u = 0; u < kRegUnroll; ++u) {
+            const int64_t ks = (s0 + kRegWaves * u) * kRegStep;
+            const bool in_k = ks + grp * 8 < k;   // K % 8 == 0: a chunk is all in or all out
+            wf[u] = in_k ? load16(wp + ks) : u32x4_t{0u, 0u, 0u, 0u};
+            af[u] = (in_k && a_in) ? load16(ap + ks) : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < kRegUnroll; ++u) acc = mfma_16x16x32<DT>(wf[u], af[u], acc);
+    }
+    // acc[v] is D[n = 4 (l / 16) + v][m = l % 16].
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][4 * grp + v][i16] = acc[v];
+    __syncthreads();
+    // One thread per (column nn, row mm) of the 16 x 16 tile.
+    const int nn = threadIdx.x & 15, mm = threadIdx.x >> 4;
+    float sum = red[0][nn][mm];
+#pragma unroll
+    for (int wv = 1; wv < kRegWaves; ++wv) sum += red[wv][nn][mm];
+    if constexpr (EPI == EPI_ARGMAX) {
+        // Per row of A, the best of the workgroup's 16 columns: a 16-lane
+        // max over the keys of one row (lanes 16 mm .. 16 mm + 15).
+        uint64_t best = n0 + nn < n ? argmax_key(sum, n0 + nn) : 0;
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) {
+            const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), off))) << 32) |
+                                   uint64_t(uint32_t(__shfl_xor(int(best & 0xFFFFFFFFu), off)));
+            best = other > best ? other : best;
+        }
+        if (nn == 0 && mm < m) keys[mm * int64_t(gridDim.x) + blockIdx.x] = best;
+    } else {
+        if (mm < m && n0 + nn < n) store_elem<DT_OUT>(c, mm * ldc + n0 + nn, sum);
+    }
+}
+
+template <int DT, int DT_OUT, int EPI>
+int launch_regs(const Problem& p, hipStream_t s) {
+    if (p.m > 16) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above the configuration's rows");
+    const int64_t blocks = (p.n + 15) / 16;
+    if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
+    if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
+    hipLaunchKernelGGL((splitk_regs_kernel<DT, DT_OUT, EPI>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kRegWaves * 64), 0, s, static_cast<const uint16_t*>(p.a),
+                       static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k, p.lda, p.ldb, p.ldc, p.keys);
+    return check_launch("splitk_decode");
+}
+
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI>
 int launch_cfg(const Problem& p, hipStream_t s) {
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;
+    if (p.m > AROWS) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above the configuration's rows");
     const int64_t blocks = (p.n + 16 * OG - 1) / (16 * OG);
     if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
     const dim3 grid(static_cast<uint32_t>(blocks)), block(WAVES * 64);
     if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
-    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, MG, RG, WAVES, UNROLL, EPI>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
                        p.lda, p.ldb, p.ldc, p.keys);
     return check_launch("splitk_decode");
 }
 
-// Configurations measured on MI355X, K = 1024.
-//   N = 6144: up to 8 rows of A, 16 W rows per 4-wave workgroup; beyond that
-//   32 W rows per 8-wave workgroup, which reads each A fragment once for two
-//   W row groups (M = 16: 5.9 us, M = 32: 7.2 us).
-//   N >= 65536 (LM head, 151936 rows): every workgroup reads all of A from
-//   L2, so for M > 1 a workgroup takes 64 W rows with 4 waves, which cuts
-//   that traffic 4x against 16 rows (M = 8 / 16 / 32: 61 / 66 / 76 us,
-//   against 64 / 70 / 81 us); M = 1 keeps the 16-row workgroups (51 us).
+// Configurations measured on MI355X.  AROWS is M rounded up to 8, 16 or 32;
+// "rows" counts the W rows read (2 N for SiLU-and-mul).
+//   * rows < 65536: 32 W rows per 8-wave workgroup, one line per wave in
+//     flight; N = 6144, K = 1024, M = 1 / 4 / 8 / 16 / 32: 4.42 / 4.48 /
+//     4.62 / 4.96 / 5.99 us (the register-loading kernel: 4.91 / 5.15 /
+//     5.42 / 5.87 / 7.25 us).  With at most 2048 rows (N = 1024, K = 3584,
+//     the down and output projections) 16 rows per workgroup give twice the
+//     workgroups, with 16 waves along K up to M = 16 (M = 1 / 16 / 32: 4.7 /
+//     6.6 / 8.5 us, against 7.0 / 9.0 / 11.7 us with 32 rows).
+//   * rows >= 65536 (the LM head, N = 151936, K = 1024): M = 1 runs the
+//     register-loading kernel (48.4 us); M = 8 / 16 / 32: 53.5 / 57.5 /
+//     63.9 us (61.2 / 65.7 / 75.8 us with register loading).
 constexpr int64_t kWideN = 65536;
 
-// Fused gate/up + SiLU-and-mul: W-row groups come in gate/up pairs, so the
-// workgroups take 2 (or, for very wide W, 4) groups of 16 rows.
-template <int DT, int DT_OUT>
-int launch_silu_mul(const Problem& p, hipStream_t s) {
-    const bool wide = 2 * p.n >= kWideN;
-    if (p.m <= 16) {
-        if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4, EPI_SILU_MUL>(p, s);
-        return launch_cfg<DT, DT_OUT, 1, 2, 4, 4, EPI_SILU_MUL>(p, s);
+template <int DT, int DT_OUT, int EPI, int AROWS>
+int launch_rows(const Problem& p, hipStream_t s) {
+    const int64_t rows = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
+    if (rows >= kWideN) {
+        if constexpr (EPI != EPI_SILU_MUL && AROWS == 8)
+            if (p.m == 1) return launch_regs<DT, DT_OUT, EPI>(p, s);
+        if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 8, 4, 1, 4, EPI>(p, s);
+        else if constexpr (AROWS == 16) return launch_cfg<DT, DT_OUT, 16, 2, 8, 1, 8, EPI>(p, s);
+        else return launch_cfg<DT, DT_OUT, 8, 2, 8, 2, 8, EPI>(p, s);
     }
-    if (wide) return launch_cfg<DT, DT_OUT, 2, 4, 4, 4, EPI_SILU_MUL>(p, s);
-    return launch_cfg<DT, DT_OUT, 2, 2, 8, 2, EPI_SILU_MUL>(p, s);
+    if constexpr (EPI != EPI_SILU_MUL) {
+        if (rows <= 2048) {
+            if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 1, 8, 1, 16, EPI>(p, s);
+            else return launch_cfg<DT, DT_OUT, AROWS, 1, 16, 1, 16, EPI>(p, s);
+        }
+    }
+    return launch_cfg<DT, DT_OUT, AROWS, 2, 8, 1, 16, EPI>(p, s);
+}
+
+template <int DT, int DT_OUT, int EPI>
+int launch_epi(const Problem& p, hipStream_t s) {
+    if (p.m <= 8) return launch_rows<DT, DT_OUT, EPI, 8>(p, s);
+    if (p.m <= 16) return launch_rows<DT, DT_OUT, EPI, 16>(p, s);
+    return launch_rows<DT, DT_OUT, EPI, 32>(p, s);
+}
+
+template <int DT, int DT_OUT>
+int launch_typed(const Problem& p, hipStream_t s) {
+    if (p.epi == EPI_SILU_MUL) return launch_epi<DT, DT_OUT, EPI_SILU_MUL>(p, s);
+    return launch_epi<DT, DT_OUT, EPI_NONE>(p, s);
 }
 
 // Greedy LM head: the plain configurations, writing partial keys instead of
 // the fp32 logits.
 template <int DT>
 int launch_argmax(const Problem& p, hipStream_t s) {
-    constexpr int F = NANOVLLM_GEMM_F32;
-    const bool wide = p.n >= kWideN && p.m > 1;
-    if (p.m <= 8) {
-        if (wide) return launch_cfg<DT, F, 1, 4, 4, 4, EPI_ARGMAX>(p, s);
-        return launch_cfg<DT, F, 1, 1, 4, 8, EPI_ARGMAX>(p, s);
-    }
-    if (p.m <= 16) {
-        if (wide) return launch_cfg<DT, F, 1, 4, 4, 4, EPI_ARGMAX>(p, s);
-        return launch_cfg<DT, F, 1, 2, 8, 2, EPI_ARGMAX>(p, s);
-    }
-    if (wide) return launch_cfg<DT, F, 2, 4, 4, 4, EPI_ARGMAX>(p, s);
-    return launch_cfg<DT, F, 2, 2, 8, 2, EPI_ARGMAX>(p, s);
-}
-
-template <int DT, int DT_OUT>
-int launch_typed(const Problem& p, hipStream_t s) {
-    if (p.epi == EPI_SILU_MUL) return launch_silu_mul<DT, DT_OUT>(p, s);
-    const bool wide = p.n >= kWideN && p.m > 1;
-    if (p.m <= 8) {
-        if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4>(p, s);
-        return launch_cfg<DT, DT_OUT, 1, 1, 4, 8>(p, s);
-    }
-    if (p.m <= 16) {
-        if (wide) return launch_cfg<DT, DT_OUT, 1, 4, 4, 4>(p, s);
-        return launch_cfg<DT, DT_OUT, 1, 2, 8, 2>(p, s);
-    }
-    if (wide) return launch_cfg<DT, DT_OUT, 2, 4, 4, 4>(p, s);
-    return launch_cfg<DT, DT_OUT, 2, 2, 8, 2>(p, s);
+    return launch_epi<DT, NANOVLLM_GEMM_F32, EPI_ARGMAX>(p, s);
 }
 
 }  // namespace

@@ -193,9 +193,10 @@ def test_staged_ring_depths_ragged(m, n, din, dout):
 
 @pytest.mark.parametrize("m", [1, 5, 13, 29])
 def test_splitk_wide_n_ragged(m):
-    """splitk_decode takes 64 W rows per workgroup when N >= 65536 and M > 1
-    (16 rows for M = 1); a ragged N leaves the last workgroup partly past N
-    (clamped loads, masked stores)."""
+    """splitk_decode on N >= 65536: M = 1 takes the register-loading kernel
+    (16 W rows per workgroup), M <= 16 32 rows and M <= 32 128 rows per
+    workgroup of the LDS-staged kernel; a ragged N leaves the last workgroup
+    partly past N (clamped copies, masked stores)."""
     n, k = 70001, 256
     _say(f"splitk wide N={n} M={m} K={k}")
     gen = torch.Generator().manual_seed(m)
@@ -204,6 +205,27 @@ def test_splitk_wide_n_ragged(m):
     out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_SPLITK_DECODE, torch.float32, L.B_NK)
     torch.cuda.synchronize()
     _check_tolerance(out.cpu(), a, w, L.B_NK, torch.float32)
+
+
+SPLITK_CONFIG_CASES = [(1000, 3592, m) for m in (1, 9, 20, 32)] + [(3000, 1000, m) for m in (1, 7, 16, 25)]
+
+
+@pytest.mark.parametrize("n,k,m", SPLITK_CONFIG_CASES, ids=[f"N{n}-K{k}-M{m}" for n, k, m in SPLITK_CONFIG_CASES])
+@pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
+                         ids=["bf16", "f16-f32"])
+def test_splitk_configs_ragged(n, k, m, din, dout):
+    """The LDS-staged splitk_decode configurations below the LM head: at most
+    2048 W rows (16 rows per workgroup, 16 or 8 waves) and above (32 rows, 8
+    waves), every A-row count (8, 16, 32), a ragged N and a K that ends in a
+    partial 64-element line (3592 = 56 x 64 + 8, 1000 = 15 x 64 + 40), so
+    the last line copies zeros past K into both W and A."""
+    _say(f"splitk config N={n} K={k} M={m} {NAME[din]}->{NAME[dout]}")
+    gen = torch.Generator().manual_seed(n + k + m)
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_SPLITK_DECODE, dout, L.B_NK)
+    torch.cuda.synchronize()
+    _check_tolerance(out.cpu(), a, w, L.B_NK, dout)
 
 
 # ---------------------------------------------------------------------------
@@ -461,6 +483,21 @@ def test_silu_mul_qwen_mlp_shape(m):
     torch.cuda.synchronize()
     rows = None if m <= 32 else np.unique(np.concatenate([np.linspace(0, m - 1, 48).astype(int), [m - 1]]))
     _check_silu_mul(out.cpu(), a, w, torch.bfloat16, rows=rows, min_within_2ulp=0.99)
+
+
+@pytest.mark.parametrize("m", [3, 20])
+def test_silu_mul_splitk_wide(m):
+    """Fused SiLU-and-mul on splitk_decode with 2 N >= 65536 W rows (the wide
+    configurations, gate/up group pairs in 32- and 128-row workgroups),
+    ragged N and K."""
+    n, k = 33001, 136
+    _say(f"silu_mul splitk wide M={m} N={n} K={k}")
+    gen = torch.Generator().manual_seed(90 + m)
+    a = torch.randn((m, k), generator=gen).bfloat16()
+    w = (torch.randn((2 * n, k), generator=gen) * 0.1).bfloat16()
+    out = G.gemm_silu_mul_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_SPLITK_DECODE, torch.bfloat16)
+    torch.cuda.synchronize()
+    _check_silu_mul(out.cpu(), a, w, torch.bfloat16)
 
 
 def test_silu_mul_contract_errors_on_gpu():
