@@ -173,7 +173,9 @@ int select_silu_mul(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, i
                          "silu_mul needs 16-byte aligned a and w with k, lda and ldw multiples of 8 "
                          "(k=%lld lda=%lld ldw=%lld)",
                          (long long)k, (long long)lda, (long long)ldw);
-    if (m == 1 && 2 * n * k * 2 <= kGemvMaxWBytes) return NANOVLLM_GEMM_KERNEL_GEMV_DECODE;
+    // M = 1 included: on the Qwen3.5-0.8B gate_up_proj (2 x 3584 rows, K =
+    // 1024) splitk_decode's whole-line copies take 4.9 us against 5.2 us for
+    // gemv_decode streaming the gate and up rows.
     if (m <= kDecodeMaxM) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
     return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
 }

@@ -161,8 +161,6 @@ def test_no_vendor_kernel_id():
 def _expected_silu(m, n, k, lda, ldw, aligned):
     if not (aligned and k % 8 == 0 and lda % 8 == 0 and ldw % 8 == 0):
         return L.EUNSUPPORTED
-    if m == 1 and 2 * n * k * 2 <= 64 * 2 ** 20:
-        return L.KERNEL_GEMV_DECODE
     return L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
 
 

@@ -476,7 +476,7 @@ def test_silu_mul_qwen_mlp_shape(m):
     a = torch.randn((m, 1024), generator=gen).bfloat16()
     w = (torch.randn((7168, 1024), generator=gen) * 0.02).bfloat16()
     ad, wd = a.to(DEV), w.to(DEV)
-    want = {1: "gemv_decode", 4: "splitk_decode", 32: "splitk_decode", 2048: "mfma_staged"}[m]
+    want = {1: "splitk_decode", 4: "splitk_decode", 32: "splitk_decode", 2048: "mfma_staged"}[m]
     assert G.silu_mul_selected_kernel(ad, wd) == want
     _say(f"silu_mul qwen mlp M={m} ({want})")
     out = G.gemm_silu_mul(ad, wd)
