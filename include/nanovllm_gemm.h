@@ -220,6 +220,100 @@ int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k,
                                 int64_t lda, int64_t ldw, int dtype_in,
                                 int aligned16);
 
+/* Gated-attention output projection: the output gate of Qwen3.5 gated
+ * attention applied to A in front of o_proj,
+ *     c = (a * sigmoid(gate)) w^T
+ * replacing `output * torch.sigmoid(gate)` and `self.o_proj(...)`
+ * (nanovllm/models/qwen3_5.py:95-96).  As there, sigmoid(gate) is rounded to
+ * the input type and so is the product, before the GEMM accumulates in
+ * fp32.  The gate is read through q_proj's head-strided view
+ * (qwen3_5.py:81-86): element (i, k) at
+ *     gate[i * ldg + (k / group) * group_stride + k % group]
+ * (group = head_dim, group_stride = 2 head_dim for q_gate; a contiguous
+ * [m, k] gate is group = group_stride = k).  For m <= 32 and group a
+ * multiple of 64 the gate is applied inside the split-K decode kernel (one
+ * launch, no workspace); otherwise a gate kernel writes the gated operand to
+ * the workspace (nanovllm_gemm_gated_workspace_bytes() bytes) and the GEMM
+ * the selection table picks reads it.  Inputs f16 or bf16, output the input
+ * type or f32, on the vector path (16-byte aligned a, gate and w; k, lda,
+ * ldg, group, group_stride and ldw multiples of 8).  Asynchronous, no
+ * allocation, capturable. */
+int nanovllm_gemm_gated(const void* a, const void* gate, const void* w, void* c,
+                        int64_t m, int64_t n, int64_t k,
+                        int64_t lda, int64_t ldg, int64_t group, int64_t group_stride,
+                        int64_t ldw, int64_t ldc,
+                        int dtype_in, int dtype_out,
+                        void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
+/* Workspace bytes nanovllm_gemm_gated needs with any kernel that can run
+ * the problem (the fused gate uses none: workspace may then be null), or a
+ * negative code.  Pure host function. */
+int64_t nanovllm_gemm_gated_workspace_bytes(int64_t m, int64_t k, int64_t group, int dtype_in);
+
+/* The gated GEMM forced onto one kernel: splitk_decode runs the fused gate
+ * (m <= 32, group % 64 == 0), any other id runs the gate kernel and that
+ * GEMM kernel (gemm_bench.cu:396-416 pattern). */
+int nanovllm_gemm_gated_with_kernel(int kernel_id,
+                                    const void* a, const void* gate, const void* w, void* c,
+                                    int64_t m, int64_t n, int64_t k,
+                                    int64_t lda, int64_t ldg, int64_t group, int64_t group_stride,
+                                    int64_t ldw, int64_t ldc,
+                                    int dtype_in, int dtype_out,
+                                    void* workspace, int64_t workspace_bytes,
+                                    void* stream);
+
+/* The gate alone: out[i, k] = round(a[i, k] * round(sigmoid(gate(i, k)))),
+ * the same bits the fused path feeds its GEMM (qwen3_5.py:95).  Same layout
+ * rules as nanovllm_gemm_gated; out has leading dimension ldo. */
+int nanovllm_sigmoid_gate(const void* a, const void* gate, void* out,
+                          int64_t m, int64_t k,
+                          int64_t lda, int64_t ldg, int64_t group, int64_t group_stride,
+                          int64_t ldo, int dtype, void* stream);
+
+/* Residual add + zero-centred RMSNorm in front of a projection, replacing
+ * `hidden_states, residual = norm(hidden_states, residual)` followed by the
+ * projection (nanovllm/models/qwen3_5.py:157-159 and 200-203 with
+ * Qwen3_5RMSNorm, nanovllm/layers/layernorm.py:131-142):
+ *     s = h + residual  (fp32),  residual_out = round(s),
+ *     c[i, j] = rsqrt(mean_k s[i, k]^2 + eps) * sum_k round(s[i, k] (1 + w_norm[k])) w[j, k]
+ * The reference rounds s * rsqrt(...) * (1 + w_norm) to the input type and
+ * then multiplies; here the per-row scale is applied to the fp32 sum, so the
+ * operand is rounded before scaling (one rounding per element either way).
+ * silu_mul = 1 fuses SiluAndMul as nanovllm_gemm_silu_mul does: w is
+ * [W_gate; W_up] with 2n rows and c[i, j] = silu(g) u of the scaled sums.
+ * For m <= 32 the add and the norm run inside the split-K decode kernel
+ * (one launch, no workspace); otherwise a prologue kernel writes the
+ * operand and the row scales to the workspace
+ * (nanovllm_gemm_add_rmsnorm_workspace_bytes()) and mfma_staged scales its
+ * output rows.  Inputs f16 or bf16 (h, residual, w_norm and w alike), output
+ * the input type or f32; 16-byte aligned h, residual, w_norm, w and
+ * residual_out, with k, ldh, ldr, ldres and ldw multiples of 8.
+ * Asynchronous, no allocation, capturable. */
+int nanovllm_gemm_add_rmsnorm(const void* h, const void* residual, const void* norm_weight, float eps,
+                              const void* w, void* c, void* residual_out,
+                              int64_t m, int64_t n, int64_t k,
+                              int64_t ldh, int64_t ldr, int64_t ldw, int64_t ldc, int64_t ldres,
+                              int silu_mul, int dtype_in, int dtype_out,
+                              void* workspace, int64_t workspace_bytes,
+                              void* stream);
+
+/* Workspace bytes nanovllm_gemm_add_rmsnorm needs with either kernel (the
+ * fused norm, m <= 32, uses none: workspace may then be null), or a
+ * negative code.  Pure host function. */
+int64_t nanovllm_gemm_add_rmsnorm_workspace_bytes(int64_t m, int64_t k, int dtype_in);
+
+/* nanovllm_gemm_add_rmsnorm forced onto splitk_decode (fused, m <= 32) or
+ * mfma_staged (prologue kernel + row-scaled GEMM). */
+int nanovllm_gemm_add_rmsnorm_with_kernel(int kernel_id,
+                                          const void* h, const void* residual, const void* norm_weight, float eps,
+                                          const void* w, void* c, void* residual_out,
+                                          int64_t m, int64_t n, int64_t k,
+                                          int64_t ldh, int64_t ldr, int64_t ldw, int64_t ldc, int64_t ldres,
+                                          int silu_mul, int dtype_in, int dtype_out,
+                                          void* workspace, int64_t workspace_bytes,
+                                          void* stream);
+
 /* Stable name of a kernel id ("fp32_tiled", "mfma_staged", ...), or
  * "unknown".  Mirrors path_name (gemm_bench.cu:275-282). */
 const char* nanovllm_gemm_kernel_name(int kernel_id);

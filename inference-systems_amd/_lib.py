@@ -34,6 +34,7 @@ OK, EINVAL, EUNSUPPORTED, ELAUNCH = 0, -1, -2, -3
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _VP = ctypes.c_void_p
+_F32 = ctypes.c_float
 SIGNATURES = {
     "nanovllm_gemm": (_INT, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _VP]),
     "nanovllm_gemm_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT,
@@ -49,6 +50,15 @@ SIGNATURES = {
     "nanovllm_gemm_argmax_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP,
                                                 _I64, _VP]),
     "nanovllm_gemm_argmax_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _INT, _INT]),
+    "nanovllm_gemm_gated": (_INT, [_VP, _VP, _VP, _VP] + [_I64] * 9 + [_INT, _INT, _VP, _I64, _VP]),
+    "nanovllm_gemm_gated_workspace_bytes": (_I64, [_I64, _I64, _I64, _INT]),
+    "nanovllm_gemm_gated_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP] + [_I64] * 9 + [_INT, _INT, _VP, _I64, _VP]),
+    "nanovllm_sigmoid_gate": (_INT, [_VP, _VP, _VP] + [_I64] * 7 + [_INT, _VP]),
+    "nanovllm_gemm_add_rmsnorm": (_INT, [_VP, _VP, _VP, _F32, _VP, _VP, _VP] + [_I64] * 8
+                                  + [_INT, _INT, _INT, _VP, _I64, _VP]),
+    "nanovllm_gemm_add_rmsnorm_workspace_bytes": (_I64, [_I64, _I64, _INT]),
+    "nanovllm_gemm_add_rmsnorm_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _F32, _VP, _VP, _VP] + [_I64] * 8
+                                              + [_INT, _INT, _INT, _VP, _I64, _VP]),
     "nanovllm_gemm_kernel_name": (ctypes.c_char_p, [_INT]),
     "nanovllm_gemm_last_error": (ctypes.c_char_p, []),
     "nanovllm_gemm_version": (_INT, []),
@@ -174,3 +184,40 @@ def gemm_raw(a_ptr, b_ptr, c_ptr, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dt
         rc = lib.nanovllm_gemm_with_kernel(kernel, a_ptr, b_ptr, c_ptr, m, n, k, lda, ldb, ldc, b_layout, dtype_in,
                                            dtype_out, stream)
     check(rc, "nanovllm_gemm")
+
+
+def gated_workspace_bytes(m, k, group, dtype_in) -> int:
+    """Workspace bytes of the gated GEMM (0 when the gate is fused; negative code if invalid)."""
+    return load().nanovllm_gemm_gated_workspace_bytes(m, k, group, dtype_in)
+
+
+def gated_raw(a_ptr, gate_ptr, w_ptr, c_ptr, m, n, k, lda, ldg, group, group_stride, ldw, ldc, dtype_in, dtype_out,
+              ws_ptr, ws_bytes, stream, kernel: int | None = None) -> None:
+    """Enqueue the gated-attention output projection on `stream`; raise on error."""
+    lib = load()
+    args = (a_ptr, gate_ptr, w_ptr, c_ptr, m, n, k, lda, ldg, group, group_stride, ldw, ldc, dtype_in, dtype_out,
+            ws_ptr, ws_bytes, stream)
+    rc = lib.nanovllm_gemm_gated(*args) if kernel is None else lib.nanovllm_gemm_gated_with_kernel(kernel, *args)
+    check(rc, "nanovllm_gemm_gated")
+
+
+def sigmoid_gate_raw(a_ptr, gate_ptr, out_ptr, m, k, lda, ldg, group, group_stride, ldo, dtype, stream) -> None:
+    """Enqueue the standalone output gate on `stream`; raise on error."""
+    check(load().nanovllm_sigmoid_gate(a_ptr, gate_ptr, out_ptr, m, k, lda, ldg, group, group_stride, ldo, dtype,
+                                       stream), "nanovllm_sigmoid_gate")
+
+
+def add_rmsnorm_workspace_bytes(m, k, dtype_in) -> int:
+    """Workspace bytes of the add + RMSNorm GEMM (0 for m <= 32; negative code if invalid)."""
+    return load().nanovllm_gemm_add_rmsnorm_workspace_bytes(m, k, dtype_in)
+
+
+def add_rmsnorm_raw(h_ptr, r_ptr, nw_ptr, eps, w_ptr, c_ptr, res_ptr, m, n, k, ldh, ldr, ldw, ldc, ldres, silu_mul,
+                    dtype_in, dtype_out, ws_ptr, ws_bytes, stream, kernel: int | None = None) -> None:
+    """Enqueue the residual add + RMSNorm + projection on `stream`; raise on error."""
+    lib = load()
+    args = (h_ptr, r_ptr, nw_ptr, eps, w_ptr, c_ptr, res_ptr, m, n, k, ldh, ldr, ldw, ldc, ldres, int(silu_mul),
+            dtype_in, dtype_out, ws_ptr, ws_bytes, stream)
+    rc = (lib.nanovllm_gemm_add_rmsnorm(*args) if kernel is None
+          else lib.nanovllm_gemm_add_rmsnorm_with_kernel(kernel, *args))
+    check(rc, "nanovllm_gemm_add_rmsnorm")

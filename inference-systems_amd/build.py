@@ -42,6 +42,7 @@ SOURCES = [
     "gemm_decode.hip",
     "gemm_gemv.hip",
     "gemm_argmax.hip",
+    "gemm_prologue.hip",
 ]
 
 

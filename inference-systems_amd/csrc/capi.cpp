@@ -279,6 +279,184 @@ int argmax_entry(int forced_kernel, const void* a, const void* w, int64_t* token
     return launch_argmax_finalize(p.keys, blocks, m, tokens, logits, s);
 }
 
+// ---------------------------------------------------------------------------
+// GEMMs with a prologue on A: the gated-attention output gate before o_proj
+// and the residual add + zero-centred RMSNorm before a projection.  For
+// M <= 32 the prologue runs inside splitk_decode (one launch); otherwise a
+// prologue kernel writes the operand to the workspace and the GEMM reads it.
+// ---------------------------------------------------------------------------
+bool aligned16_ptr(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int64_t round_up_256(int64_t x) { return (x + 255) / 256 * 256; }
+
+int validate_prologue_dtypes(int din, int dout, const char* what) {
+    if (din != NANOVLLM_GEMM_F16 && din != NANOVLLM_GEMM_BF16)
+        return set_error(din >= NANOVLLM_GEMM_F32 && din <= NANOVLLM_GEMM_BF16 ? NANOVLLM_GEMM_EUNSUPPORTED
+                                                                               : NANOVLLM_GEMM_EINVAL,
+                         "%s takes float16 or bfloat16 inputs (dtype code %d)", what, din);
+    if (dout != din && dout != NANOVLLM_GEMM_F32)
+        return set_error(dout >= NANOVLLM_GEMM_F32 && dout <= NANOVLLM_GEMM_BF16 ? NANOVLLM_GEMM_EUNSUPPORTED
+                                                                                 : NANOVLLM_GEMM_EINVAL,
+                         "%s writes the input dtype or float32 (dtype codes in %d, out %d)", what, din, dout);
+    return NANOVLLM_GEMM_OK;
+}
+
+// Sizes and strides of the gated GEMM; the vector path's alignment is
+// checked separately (gated_vector_ok).
+int validate_gated(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldg, int64_t group, int64_t group_stride,
+                   int64_t ldw, int64_t ldc, int din, int dout) {
+    int rc = validate_prologue_dtypes(din, dout, "gemm_gated");
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m < 0 || n < 0) return set_error(NANOVLLM_GEMM_EINVAL, "m and n must be non-negative (m=%lld, n=%lld)",
+                                         (long long)m, (long long)n);
+    if (k < 1) return set_error(NANOVLLM_GEMM_EINVAL, "k must be positive (k=%lld)", (long long)k);
+    if (group < 1 || k % group != 0)
+        return set_error(NANOVLLM_GEMM_EINVAL, "group (%lld) must divide k (%lld)", (long long)group, (long long)k);
+    if (group_stride < group)
+        return set_error(NANOVLLM_GEMM_EINVAL, "group_stride (%lld) must be >= group (%lld)", (long long)group_stride,
+                         (long long)group);
+    const int64_t gate_row = (k / group - 1) * group_stride + group;   // elements one gate row spans
+    if (ldg < gate_row)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldg (%lld) must be >= %lld, the span of one gate row",
+                         (long long)ldg, (long long)gate_row);
+    if (lda < k) return set_error(NANOVLLM_GEMM_EINVAL, "lda (%lld) must be >= k (%lld)", (long long)lda, (long long)k);
+    if (ldw < k) return set_error(NANOVLLM_GEMM_EINVAL, "ldw (%lld) must be >= k (%lld)", (long long)ldw, (long long)k);
+    if (ldc < n || ldc < 1)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldc (%lld) must be >= n (%lld)", (long long)ldc, (long long)n);
+    return NANOVLLM_GEMM_OK;
+}
+
+bool gated_vector_ok(int64_t k, int64_t lda, int64_t ldg, int64_t group, int64_t group_stride, int64_t ldw,
+                     int aligned16) {
+    return vector_ok(k, lda, ldw, NANOVLLM_GEMM_B_NK, aligned16) && ldg % 8 == 0 && group % 8 == 0 &&
+           group_stride % 8 == 0;
+}
+
+// The fused path copies whole 64-element lines of the gate, so a line must
+// not straddle two gate groups.
+bool gated_fused(int64_t m, int64_t group) { return m <= kDecodeMaxM && group % 64 == 0; }
+
+// Enough for any kernel that can run the problem (the fused gate uses none).
+int64_t gated_workspace_bytes(int64_t m, int64_t k) { return round_up_256(m * k * 2); }
+
+int gated_entry(int forced_kernel, const void* a, const void* gate, const void* w, void* c, int64_t m, int64_t n,
+                int64_t k, int64_t lda, int64_t ldg, int64_t group, int64_t group_stride, int64_t ldw, int64_t ldc,
+                int din, int dout, void* workspace, int64_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    int rc = validate_gated(m, n, k, lda, ldg, group, group_stride, ldw, ldc, din, dout);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m == 0 || n == 0) return NANOVLLM_GEMM_OK;
+    if (a == nullptr || gate == nullptr || w == nullptr || c == nullptr)
+        return set_error(NANOVLLM_GEMM_EINVAL, "a, gate, w and c must be non-null device pointers");
+    const int al = aligned16_ptr(a) && aligned16_ptr(gate) && aligned16_ptr(w);
+    if (!gated_vector_ok(k, lda, ldg, group, group_stride, ldw, al))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "gemm_gated needs 16-byte aligned a, gate and w with k, lda, ldg, group, group_stride "
+                         "and ldw multiples of 8");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool fused = forced_kernel < 0 ? gated_fused(m, group) : forced_kernel == NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+    if (fused) {
+        if (!gated_fused(m, group))
+            return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                             "the fused gate runs in splitk_decode for m <= 32 and group a multiple of 64 "
+                             "(m=%lld group=%lld)", (long long)m, (long long)group);
+        Problem p{a, w, c, m, n, k, lda, ldw, ldc, NANOVLLM_GEMM_B_NK, din, dout};
+        p.pro = PRO_GATE;
+        p.a2 = gate;
+        p.lda2 = ldg;
+        p.group = group;
+        p.group_stride = group_stride;
+        return launch_splitk_decode(p, s);
+    }
+    // The gated operand goes to the workspace (leading dimension k), then the
+    // GEMM the table (or the caller) picks for it.
+    const int64_t need = round_up_256(m * k * 2);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16_ptr(workspace))
+        return set_error(NANOVLLM_GEMM_EINVAL,
+                         "this problem needs a 16-byte aligned workspace of %lld bytes (got %lld)", (long long)need,
+                         (long long)workspace_bytes);
+    int kernel = forced_kernel < 0 ? select(m, n, k, k, ldw, NANOVLLM_GEMM_B_NK, din, 1) : forced_kernel;
+    if (forced_kernel >= NANOVLLM_GEMM_KERNEL_COUNT || !supports(kernel, m, k, k, ldw, NANOVLLM_GEMM_B_NK, din, 1))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "kernel %s cannot run the gated GEMM (m=%lld n=%lld k=%lld)",
+                         nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);
+    rc = launch_gate_prologue(a, lda, gate, ldg, group, group_stride, workspace, k, m, k, din, s);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    const Problem p{workspace, w, c, m, n, k, k, ldw, ldc, NANOVLLM_GEMM_B_NK, din, dout};
+    return run(kernel, p, s);
+}
+
+int validate_add_norm(int64_t m, int64_t n, int64_t k, int64_t ldh, int64_t ldr, int64_t ldw, int64_t ldc,
+                      int64_t ldres, float eps, int din, int dout) {
+    int rc = validate_prologue_dtypes(din, dout, "gemm_add_rmsnorm");
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m < 0) return set_error(NANOVLLM_GEMM_EINVAL, "m must be non-negative (m=%lld)", (long long)m);
+    if (n < 1) return set_error(NANOVLLM_GEMM_EINVAL, "n must be positive (n=%lld)", (long long)n);
+    if (k < 1) return set_error(NANOVLLM_GEMM_EINVAL, "k must be positive (k=%lld)", (long long)k);
+    if (!(eps >= 0.0f) || eps > 1.0f) return set_error(NANOVLLM_GEMM_EINVAL, "eps must be in [0, 1]");
+    if (ldh < k || ldr < k || ldres < k)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldh, ldr and ldres (%lld, %lld, %lld) must be >= k (%lld)",
+                         (long long)ldh, (long long)ldr, (long long)ldres, (long long)k);
+    if (ldw < k) return set_error(NANOVLLM_GEMM_EINVAL, "ldw (%lld) must be >= k (%lld)", (long long)ldw, (long long)k);
+    if (ldc < n || ldc < 1)
+        return set_error(NANOVLLM_GEMM_EINVAL, "ldc (%lld) must be >= n (%lld)", (long long)ldc, (long long)n);
+    return NANOVLLM_GEMM_OK;
+}
+
+// Operand y at the start of the workspace (leading dimension k), then the
+// fp32 row scales; enough for either kernel (the fused norm uses none).
+int64_t add_norm_workspace_bytes(int64_t m, int64_t k) { return round_up_256(m * k * 2) + round_up_256(m * 4); }
+
+int add_norm_entry(int forced_kernel, const void* h, const void* r, const void* norm_w, float eps, const void* w,
+                   void* c, void* res_out, int64_t m, int64_t n, int64_t k, int64_t ldh, int64_t ldr, int64_t ldw,
+                   int64_t ldc, int64_t ldres, int silu_mul, int din, int dout, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    int rc = validate_add_norm(m, n, k, ldh, ldr, ldw, ldc, ldres, eps, din, dout);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m == 0) return NANOVLLM_GEMM_OK;
+    if (h == nullptr || r == nullptr || norm_w == nullptr || w == nullptr || res_out == nullptr || c == nullptr)
+        return set_error(NANOVLLM_GEMM_EINVAL, "h, residual, norm_weight, w, c and residual_out must be non-null");
+    const bool al = aligned16_ptr(h) && aligned16_ptr(r) && aligned16_ptr(norm_w) && aligned16_ptr(w) &&
+                    aligned16_ptr(res_out);
+    if (!(al && k % 8 == 0 && ldh % 8 == 0 && ldr % 8 == 0 && ldres % 8 == 0 && ldw % 8 == 0))
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "gemm_add_rmsnorm needs 16-byte aligned h, residual, norm_weight, w and residual_out "
+                         "with k, ldh, ldr, ldres and ldw multiples of 8");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool fused = forced_kernel < 0 ? m <= kDecodeMaxM : forced_kernel == NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+    if (fused) {
+        if (m > kDecodeMaxM)
+            return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "the fused norm runs in splitk_decode for m <= 32 (m=%lld)",
+                             (long long)m);
+        Problem p{h, w, c, m, n, k, ldh, ldw, ldc, NANOVLLM_GEMM_B_NK, din, dout};
+        p.epi = silu_mul ? EPI_SILU_MUL : EPI_NONE;
+        p.pro = PRO_ADD_NORM;
+        p.a2 = r;
+        p.lda2 = ldr;
+        p.norm_w = norm_w;
+        p.eps = eps;
+        p.res_out = res_out;
+        p.ldres = ldres;
+        return launch_splitk_decode(p, s);
+    }
+    if (forced_kernel >= 0 && forced_kernel != NANOVLLM_GEMM_KERNEL_MFMA_STAGED)
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "gemm_add_rmsnorm runs on splitk_decode or mfma_staged, not %s",
+                         nanovllm_gemm_kernel_name(forced_kernel));
+    const int64_t y_bytes = round_up_256(m * k * 2);
+    const int64_t need = y_bytes + round_up_256(m * 4);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16_ptr(workspace))
+        return set_error(NANOVLLM_GEMM_EINVAL,
+                         "this problem needs a 16-byte aligned workspace of %lld bytes (got %lld)", (long long)need,
+                         (long long)workspace_bytes);
+    float* scale = reinterpret_cast<float*>(static_cast<char*>(workspace) + y_bytes);
+    rc = launch_add_norm_prologue(h, ldh, r, ldr, norm_w, eps, workspace, k, res_out, ldres, scale, m, k, din, s);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    Problem p{workspace, w, c, m, n, k, k, ldw, ldc, NANOVLLM_GEMM_B_NK, din, dout};
+    p.epi = silu_mul ? EPI_SILU_MUL : EPI_NONE;
+    p.row_scale = scale;
+    return launch_mfma_staged(p, s);
+}
+
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -400,8 +578,88 @@ int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k, int64_t lda, in
     return nvg::select_argmax(m, k, lda, ldw, aligned16);
 }
 
+int64_t nanovllm_gemm_gated_workspace_bytes(int64_t m, int64_t k, int64_t group, int dtype_in) {
+    nvg::g_last_error.clear();
+    const int rc = nvg::validate_prologue_dtypes(dtype_in, dtype_in, "gemm_gated");
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m < 0 || k < 1 || group < 1 || k % group != 0)
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "need m >= 0, k >= 1 and a group dividing k (m=%lld k=%lld "
+                              "group=%lld)", (long long)m, (long long)k, (long long)group);
+    return nvg::gated_workspace_bytes(m, k);
+}
+
+int nanovllm_gemm_gated(const void* a, const void* gate, const void* w, void* c, int64_t m, int64_t n, int64_t k,
+                        int64_t lda, int64_t ldg, int64_t group, int64_t group_stride, int64_t ldw, int64_t ldc,
+                        int dtype_in, int dtype_out, void* workspace, int64_t workspace_bytes, void* stream) {
+    return nvg::gated_entry(-1, a, gate, w, c, m, n, k, lda, ldg, group, group_stride, ldw, ldc, dtype_in, dtype_out,
+                            workspace, workspace_bytes, stream);
+}
+
+int nanovllm_gemm_gated_with_kernel(int kernel_id, const void* a, const void* gate, const void* w, void* c,
+                                    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldg, int64_t group,
+                                    int64_t group_stride, int64_t ldw, int64_t ldc, int dtype_in, int dtype_out,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+    if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
+        nvg::g_last_error.clear();
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+    return nvg::gated_entry(kernel_id, a, gate, w, c, m, n, k, lda, ldg, group, group_stride, ldw, ldc, dtype_in,
+                            dtype_out, workspace, workspace_bytes, stream);
+}
+
+int nanovllm_sigmoid_gate(const void* a, const void* gate, void* out, int64_t m, int64_t k, int64_t lda,
+                          int64_t ldg, int64_t group, int64_t group_stride, int64_t ldo, int dtype, void* stream) {
+    nvg::g_last_error.clear();
+    int rc = nvg::validate_gated(m, 0, k, lda, ldg, group, group_stride, k, 1, dtype, dtype);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (ldo < k) return nvg::set_error(NANOVLLM_GEMM_EINVAL, "ldo (%lld) must be >= k (%lld)", (long long)ldo,
+                                       (long long)k);
+    if (m == 0) return NANOVLLM_GEMM_OK;
+    if (a == nullptr || gate == nullptr || out == nullptr)
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "a, gate and out must be non-null device pointers");
+    const int al = nvg::aligned16_ptr(a) && nvg::aligned16_ptr(gate) && nvg::aligned16_ptr(out);
+    if (!nvg::gated_vector_ok(k, lda, ldg, group, group_stride, k, al) || ldo % 8 != 0)
+        return nvg::set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                              "sigmoid_gate needs 16-byte aligned a, gate and out with k, lda, ldg, group, "
+                              "group_stride and ldo multiples of 8");
+    return nvg::launch_gate_prologue(a, lda, gate, ldg, group, group_stride, out, ldo, m, k, dtype,
+                                     static_cast<hipStream_t>(stream));
+}
+
+int64_t nanovllm_gemm_add_rmsnorm_workspace_bytes(int64_t m, int64_t k, int dtype_in) {
+    nvg::g_last_error.clear();
+    const int rc = nvg::validate_prologue_dtypes(dtype_in, dtype_in, "gemm_add_rmsnorm");
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (m < 0 || k < 1)
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "need m >= 0 and k >= 1 (m=%lld k=%lld)", (long long)m,
+                              (long long)k);
+    return nvg::add_norm_workspace_bytes(m, k);
+}
+
+int nanovllm_gemm_add_rmsnorm(const void* h, const void* residual, const void* norm_weight, float eps, const void* w,
+                              void* c, void* residual_out, int64_t m, int64_t n, int64_t k, int64_t ldh, int64_t ldr,
+                              int64_t ldw, int64_t ldc, int64_t ldres, int silu_mul, int dtype_in, int dtype_out,
+                              void* workspace, int64_t workspace_bytes, void* stream) {
+    return nvg::add_norm_entry(-1, h, residual, norm_weight, eps, w, c, residual_out, m, n, k, ldh, ldr, ldw, ldc,
+                               ldres, silu_mul, dtype_in, dtype_out, workspace, workspace_bytes, stream);
+}
+
+int nanovllm_gemm_add_rmsnorm_with_kernel(int kernel_id, const void* h, const void* residual,
+                                          const void* norm_weight, float eps, const void* w, void* c,
+                                          void* residual_out, int64_t m, int64_t n, int64_t k, int64_t ldh,
+                                          int64_t ldr, int64_t ldw, int64_t ldc, int64_t ldres, int silu_mul,
+                                          int dtype_in, int dtype_out, void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
+    if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
+        nvg::g_last_error.clear();
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+    return nvg::add_norm_entry(kernel_id, h, residual, norm_weight, eps, w, c, residual_out, m, n, k, ldh, ldr, ldw,
+                               ldc, ldres, silu_mul, dtype_in, dtype_out, workspace, workspace_bytes, stream);
+}
+
 const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
 
-int nanovllm_gemm_version(void) { return (1 << 16) | 2; }
+int nanovllm_gemm_version(void) { return (1 << 16) | 3; }
 
 }  // extern "C"

@@ -29,6 +29,17 @@ constexpr int EPI_NONE = 0;
 constexpr int EPI_SILU_MUL = 1;
 constexpr int EPI_ARGMAX = 2;
 
+// Prologues on A.  PRO_GATE is the gated-attention output gate: A is used as
+// a * sigmoid(g), the sigmoid rounded to the element type and the product
+// rounded again (the reference's two element-type tensor ops).  PRO_ADD_NORM
+// is the residual add and zero-centred RMSNorm in front of a projection: with
+// s = h + r in fp32, the GEMM runs on y = round(s * (1 + w)) and output row i
+// is scaled by rsqrt(mean_k s[i][k]^2 + eps) after the sum; round(s) is the
+// new residual.
+constexpr int PRO_NONE = 0;
+constexpr int PRO_GATE = 1;
+constexpr int PRO_ADD_NORM = 2;
+
 // One GEMM problem as it crosses the C ABI (see include/nanovllm_gemm.h).
 struct Problem {
     const void* a;
@@ -42,6 +53,19 @@ struct Problem {
     int epi = EPI_NONE;   // EPI_SILU_MUL: n output columns from 2n rows of b
     uint64_t* keys = nullptr;         // EPI_ARGMAX: [m, workgroups along N] partial keys
     int64_t* key_blocks = nullptr;    // EPI_ARGMAX: set by the launcher to its workgroups along N
+    const float* row_scale = nullptr; // mfma_staged, EPI_NONE / EPI_SILU_MUL: output row i (both
+                                      // sums of a SiLU pair) times row_scale[i] before rounding
+    int pro = PRO_NONE;
+    // PRO_GATE: gate element (i, k) at a2[i * lda2 + (k / group) * group_stride + k % group].
+    // PRO_ADD_NORM: residual r[i, k] at a2[i * lda2 + k]; norm weight norm_w[k];
+    // the new residual round(h + r) goes to res_out[i * ldres + k].
+    const void* a2 = nullptr;
+    int64_t lda2 = 0;
+    int64_t group = 0, group_stride = 0;
+    const void* norm_w = nullptr;
+    float eps = 0.0f;
+    void* res_out = nullptr;
+    int64_t ldres = 0;
 };
 
 constexpr int kWave = 64;
@@ -167,6 +191,50 @@ __device__ __forceinline__ float silu_f32(float x) {
     return x / (1.0f + expf(-x));
 }
 
+// sigmoid(x) = 1 / (1 + e^-x) in fp32 (library exp, IEEE divide).
+__device__ __forceinline__ float sigmoid_f32(float x) {
+    return 1.0f / (1.0f + expf(-x));
+}
+
+// PRO_GATE on 8 packed elements: round(a * round(sigmoid(g))), each product
+// and sigmoid in fp32, rounding to nearest even in the element type.
+template <int DT>
+__device__ __forceinline__ u32x4_t gate8(u32x4_t a, u32x4_t g) {
+    u32x4_t out;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t sg = pack2<DT>(sigmoid_f32(half_to_f32<DT>(uint16_t(g[q]))),
+                                      sigmoid_f32(half_to_f32<DT>(uint16_t(g[q] >> 16))));
+        out[q] = pack2<DT>(half_to_f32<DT>(uint16_t(a[q])) * half_to_f32<DT>(uint16_t(sg)),
+                           half_to_f32<DT>(uint16_t(a[q] >> 16)) * half_to_f32<DT>(uint16_t(sg >> 16)));
+    }
+    return out;
+}
+
+// PRO_ADD_NORM on 8 packed elements of h, r and the norm weight w: with
+// s = h + r in fp32, adds s^2 to ss in element order, returns round(s) (the
+// new residual) in res and round(s * (1 + w)) (the GEMM operand).
+template <int DT>
+__device__ __forceinline__ u32x4_t add_norm8(u32x4_t h, u32x4_t r, u32x4_t w, float& ss, u32x4_t& res) {
+    u32x4_t y;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float s0 = half_to_f32<DT>(uint16_t(h[q])) + half_to_f32<DT>(uint16_t(r[q]));
+        const float s1 = half_to_f32<DT>(uint16_t(h[q] >> 16)) + half_to_f32<DT>(uint16_t(r[q] >> 16));
+        ss = __builtin_fmaf(s0, s0, ss);
+        ss = __builtin_fmaf(s1, s1, ss);
+        res[q] = pack2<DT>(s0, s1);
+        y[q] = pack2<DT>(s0 * (1.0f + half_to_f32<DT>(uint16_t(w[q]))),
+                         s1 * (1.0f + half_to_f32<DT>(uint16_t(w[q] >> 16))));
+    }
+    return y;
+}
+
+// rsqrt(ss / k + eps) in fp32 (IEEE divide and square root).
+__device__ __forceinline__ float norm_scale(float ss, int64_t k, float eps) {
+    return 1.0f / sqrtf(ss / static_cast<float>(k) + eps);
+}
+
 // Greedy-argmax key: the fp32 logit mapped to an unsigned integer with the
 // same order (sign-magnitude to offset binary) in the high word, and
 // 0xFFFFFFFF - column in the low word, so the largest key is the largest
@@ -229,6 +297,14 @@ int launch_gemv_decode(const Problem& p, hipStream_t s);
 // Reduces `blocks` partial keys per row ([m, blocks], from an EPI_ARGMAX
 // launch) to the greedy token of each row (int64) and, if `logits` is not
 // null, its logit.
+// Standalone prologues (gemm_prologue.hip): the GEMM operand written to a
+// buffer, for the problems the fused decode kernel does not take.
+int launch_gate_prologue(const void* a, int64_t lda, const void* g, int64_t ldg, int64_t group,
+                         int64_t group_stride, void* out, int64_t ldo, int64_t m, int64_t k, int dtype,
+                         hipStream_t s);
+int launch_add_norm_prologue(const void* h, int64_t ldh, const void* r, int64_t ldr, const void* w, float eps,
+                             void* y, int64_t ldy, void* res, int64_t ldres, float* scale, int64_t m, int64_t k,
+                             int dtype, hipStream_t s);
 int launch_argmax_finalize(const uint64_t* keys, int64_t blocks, int64_t m, int64_t* tokens, float* logits,
                            hipStream_t s);
 

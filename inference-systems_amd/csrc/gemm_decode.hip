@@ -36,18 +36,34 @@ constexpr int kLine = 64;   // K elements per line: 128 bytes = 8 chunks of 16 b
 // Source of the K-tail chunks: 16 zero bytes in global memory.
 __device__ u32x4_t g_decode_zero = {0u, 0u, 0u, 0u};
 
+// Operands of the prologues (PRO_GATE, PRO_ADD_NORM; see gemm_common.hpp).
+struct ProArgs {
+    const uint16_t* a2;      // gate or residual, leading dimension lda2
+    int64_t lda2;
+    int64_t group, group_stride;   // PRO_GATE: k -> (k / group) * group_stride + k % group
+    const uint16_t* norm_w;  // PRO_ADD_NORM: [K] zero-centred weight
+    float eps;
+    uint16_t* res_out;       // PRO_ADD_NORM: round(h + r), leading dimension ldres
+    int64_t ldres;
+};
+
 // RG groups of 16 W rows per workgroup, AROWS rows of A copied per line
 // (8, 16 or 32: M rounded up), WAVES waves splitting K, LPB lines per wave
-// in flight at once, PARTS K partitions (a multiple of WAVES).
-template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI>
+// in flight at once, PARTS K partitions (a multiple of WAVES), PRO the
+// prologue on A.
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO>
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
-    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys) {
+    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
+    ProArgs pro) {
     static_assert(AROWS == 8 || AROWS == 16 || AROWS == 32, "rows of A per line");
     constexpr int MG = AROWS == 32 ? 2 : 1;   // 16-row groups of A in the MFMA
     constexpr int IW = 2 * RG;                 // W copies per line (8 rows each)
     constexpr int IA = AROWS / 8;              // A copies per line
-    constexpr int IL = IW + IA;
+    constexpr int IP = PRO == PRO_NONE ? 0 : IA;   // gate or residual copies per line
+    constexpr int IL = IW + IA + IP;
+    static_assert(PRO == PRO_NONE || EPI == EPI_NONE || (PRO == PRO_ADD_NORM && EPI == EPI_SILU_MUL),
+                  "prologues come with the plain store (and the norm also with SiLU-and-mul)");
     static_assert(LPB * IL < 64, "vmcnt range");
     static_assert(PARTS % WAVES == 0, "whole partitions per wave");
     constexpr int PW = PARTS / WAVES;                  // partitions per wave
@@ -58,6 +74,8 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     constexpr int REGION = LPB * IL * 64;
     static_assert(PW * RG * MG * 256 <= 4 * REGION, "partition tiles fit in a wave's region");
     __shared__ u32x4_t buf[WAVES][REGION];
+    // PRO_ADD_NORM: per wave, the sum of s^2 over its lines, per row of A.
+    __shared__ float sspart[PRO == PRO_ADD_NORM ? WAVES : 1][MG * 16];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -84,6 +102,9 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* asrc[IA];
 #pragma unroll
     for (int h = 0; h < IA; ++h) asrc[h] = a + min_i64(8 * h + r8, m - 1) * lda + chunk * 8;
+    const uint16_t* psrc[IP > 0 ? IP : 1];
+#pragma unroll
+    for (int h = 0; h < IP; ++h) psrc[h] = pro.a2 + min_i64(8 * h + r8, m - 1) * pro.lda2 + chunk * 8;
     const void* zero = &g_decode_zero;
     asm volatile("" : "+s"(zero));
 
@@ -96,6 +117,9 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const int64_t lines = (k + kLine - 1) / kLine;
     const uint32_t base = lds_address(&buf[wave][0]);
     f32x4_t acc[PW][RG][MG];
+    float ss[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g) ss[g] = 0.0f;
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -109,17 +133,28 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
 #pragma unroll
         for (int bt = 0; bt < ROUND / LPB; ++bt) {
             if (l0 + int64_t(WAVES) * (bt * LPB) >= lines) break;
+            u32x4_t nwv[LPB][2];   // PRO_ADD_NORM: the norm weight at the lane's two fragment chunks
 #pragma unroll
             for (int t = 0; t < LPB; ++t) {
                 const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
                 if (line >= lines) break;
                 const uint32_t dst = base + uint32_t(t * IL) * 1024u;
                 const int64_t koff = line * kLine;
+                // PRO_GATE: a line never straddles a gate group (group % 64 == 0).
+                int64_t pk = koff;
+                if constexpr (PRO == PRO_GATE) pk = (koff / pro.group) * pro.group_stride + koff % pro.group;
+                if constexpr (PRO == PRO_ADD_NORM) {
+#pragma unroll
+                    for (int st = 0; st < 2; ++st)
+                        nwv[t][st] = load16(pro.norm_w + min_i64(koff + (4 * st + grp) * 8, k - 8));
+                }
                 if (koff + kLine <= k) {
 #pragma unroll
                     for (int h = 0; h < IW; ++h) dma16(wsrc[h] + koff, dst + 1024u * h);
 #pragma unroll
                     for (int h = 0; h < IA; ++h) dma16(asrc[h] + koff, dst + 1024u * (IW + h));
+#pragma unroll
+                    for (int h = 0; h < IP; ++h) dma16(psrc[h] + pk, dst + 1024u * (IW + IA + h));
                 } else {
                     // K tail (K % 8 == 0): chunks past K copy zeros into W and A.
                     const bool in_k = koff + chunk * 8 < k;
@@ -129,12 +164,16 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
 #pragma unroll
                     for (int h = 0; h < IA; ++h)
                         dma16(in_k ? static_cast<const void*>(asrc[h] + koff) : zero, dst + 1024u * (IW + h));
+#pragma unroll
+                    for (int h = 0; h < IP; ++h)
+                        dma16(in_k ? static_cast<const void*>(psrc[h] + pk) : zero, dst + 1024u * (IW + IA + h));
                 }
             }
             wait_vmcnt<0>();
 #pragma unroll
             for (int t = 0; t < LPB; ++t) {
-                if (l0 + int64_t(WAVES) * (bt * LPB + t) >= lines) break;
+                const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
+                if (line >= lines) break;
                 const int q = (bt * LPB + t) % PW;   // compile-time after unrolling
                 const u32x4_t* lb = &buf[wave][t * IL * 64];
 #pragma unroll
@@ -145,6 +184,28 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                     for (int r = 0; r < RG; ++r) wf[r] = lb[(2 * r + hi) * 64 + slot];
 #pragma unroll
                     for (int g = 0; g < MG; ++g) af[g] = lb[(IW + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot];
+                    if constexpr (PRO == PRO_GATE) {
+#pragma unroll
+                        for (int g = 0; g < MG; ++g)
+                            af[g] = gate8<DT>(af[g], lb[(IW + IA + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot]);
+                    }
+                    if constexpr (PRO == PRO_ADD_NORM) {
+                        // Element k of this fragment chunk; chunks past K are zero in h and r.
+                        const int64_t kc = line * kLine + (4 * st + grp) * 8;
+                        const bool in_k = kc < k;
+                        const u32x4_t wv = in_k ? nwv[t][st] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+                        for (int g = 0; g < MG; ++g) {
+                            u32x4_t res;
+                            af[g] = add_norm8<DT>(af[g], lb[(IW + IA + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot],
+                                                  wv, ss[g], res);
+                            // Workgroup 0 writes the new residual (each element once: rows
+                            // 8..15 of an 8-row copy repeat rows 0..7).
+                            const int64_t row = 16 * g + i16;
+                            if (blockIdx.x == 0 && in_k && row < m && (AROWS != 8 || i16 < 8))
+                                *reinterpret_cast<u32x4_t*>(pro.res_out + row * pro.ldres + kc) = res;
+                        }
+                    }
 #pragma unroll
                     for (int r = 0; r < RG; ++r)
 #pragma unroll
@@ -175,6 +236,17 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
             for (int g = 0; g < MG; ++g)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) part(wave, q, r, g, 4 * grp + v, i16) = acc[q][r][g][v];
+    if constexpr (PRO == PRO_ADD_NORM) {
+        // The wave's sum of s^2 per row: its 4 lanes of a row (one per
+        // fragment chunk) added by a butterfly, the same sum in every lane.
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+            float v = ss[g];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (grp == 0) sspart[wave][16 * g + i16] = v;
+        }
+    }
     __syncthreads();
     // Sum of the partitions in partition order.
     auto total = [&](int r, int g, int nn, int mm) {
@@ -217,10 +289,26 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
         const int64_t row = g * 16 + mm;
         const int64_t col = n0 + 16 * o + nn;
         if (row >= m || col >= n) continue;
-        if constexpr (EPI == EPI_SILU_MUL)
-            store_elem<DT_OUT>(c, row * ldc + col, silu_f32(total(2 * o, g, nn, mm)) * total(2 * o + 1, g, nn, mm));
-        else
+        // PRO_ADD_NORM: the row's scale, from the waves' sums of s^2 in wave order.
+        float rs = 1.0f;
+        if constexpr (PRO == PRO_ADD_NORM) {
+            float sum_sq = sspart[0][row];
+#pragma unroll
+            for (int wv = 1; wv < WAVES; ++wv) sum_sq += sspart[wv][row];
+            rs = norm_scale(sum_sq, k, pro.eps);
+        }
+        if constexpr (EPI == EPI_SILU_MUL) {
+            float gate = total(2 * o, g, nn, mm), up = total(2 * o + 1, g, nn, mm);
+            if constexpr (PRO == PRO_ADD_NORM) {
+                gate *= rs;
+                up *= rs;
+            }
+            store_elem<DT_OUT>(c, row * ldc + col, silu_f32(gate) * up);
+        } else if constexpr (PRO == PRO_ADD_NORM) {
+            store_elem<DT_OUT>(c, row * ldc + col, total(o, g, nn, mm) * rs);
+        } else {
             store_elem<DT_OUT>(c, row * ldc + col, total(o, g, nn, mm));
+        }
     }
 }
 
@@ -297,7 +385,7 @@ int launch_regs(const Problem& p, hipStream_t s) {
     return check_launch("splitk_decode");
 }
 
-template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI>
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO = PRO_NONE>
 int launch_cfg(const Problem& p, hipStream_t s) {
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;
     if (p.m > AROWS) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above the configuration's rows");
@@ -305,9 +393,11 @@ int launch_cfg(const Problem& p, hipStream_t s) {
     if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
     const dim3 grid(static_cast<uint32_t>(blocks)), block(WAVES * 64);
     if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
-    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI>), grid, block, 0, s,
+    const ProArgs pro{static_cast<const uint16_t*>(p.a2), p.lda2, p.group, p.group_stride,
+                      static_cast<const uint16_t*>(p.norm_w), p.eps, static_cast<uint16_t*>(p.res_out), p.ldres};
+    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI, PRO>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
-                       p.lda, p.ldb, p.ldc, p.keys);
+                       p.lda, p.ldb, p.ldc, p.keys, pro);
     return check_launch("splitk_decode");
 }
 
@@ -321,39 +411,46 @@ int launch_cfg(const Problem& p, hipStream_t s) {
 //     workgroups, with 16 waves along K up to M = 16 (M = 1 / 16 / 32: 4.7 /
 //     6.6 / 8.5 us, against 7.0 / 9.0 / 11.7 us with 32 rows).
 //   * rows >= 65536 (the LM head, N = 151936, K = 1024): M = 1 runs the
-//     register-loading kernel (48.4 us); M = 8 / 16 / 32: 53.5 / 57.5 /
-//     63.9 us (61.2 / 65.7 / 75.8 us with register loading).
+//     register-loading kernel (48.4 us; with a prologue, the M <= 8
+//     configuration); M = 8 / 16 / 32: 53.5 / 57.5 / 63.9 us (61.2 / 65.7 /
+//     75.8 us with register loading).
+// A prologue adds its own copies per line to the same configurations.
 constexpr int64_t kWideN = 65536;
 
-template <int DT, int DT_OUT, int EPI, int AROWS>
+template <int DT, int DT_OUT, int EPI, int AROWS, int PRO>
 int launch_rows(const Problem& p, hipStream_t s) {
     const int64_t rows = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
     if (rows >= kWideN) {
-        if constexpr (EPI != EPI_SILU_MUL && AROWS == 8)
+        if constexpr (EPI != EPI_SILU_MUL && PRO == PRO_NONE && AROWS == 8)
             if (p.m == 1) return launch_regs<DT, DT_OUT, EPI>(p, s);
-        if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 8, 4, 1, 4, EPI>(p, s);
-        else if constexpr (AROWS == 16) return launch_cfg<DT, DT_OUT, 16, 2, 8, 1, 8, EPI>(p, s);
-        else return launch_cfg<DT, DT_OUT, 8, 2, 8, 2, 8, EPI>(p, s);
+        if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 8, 4, 1, 4, EPI, PRO>(p, s);
+        else if constexpr (AROWS == 16) return launch_cfg<DT, DT_OUT, 16, 2, 8, 1, 8, EPI, PRO>(p, s);
+        else return launch_cfg<DT, DT_OUT, 8, 2, 8, 2, 8, EPI, PRO>(p, s);
     }
     if constexpr (EPI != EPI_SILU_MUL) {
         if (rows <= 2048) {
-            if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 1, 8, 1, 16, EPI>(p, s);
-            else return launch_cfg<DT, DT_OUT, AROWS, 1, 16, 1, 16, EPI>(p, s);
+            if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 1, 8, 1, 16, EPI, PRO>(p, s);
+            else return launch_cfg<DT, DT_OUT, AROWS, 1, 16, 1, 16, EPI, PRO>(p, s);
         }
     }
-    return launch_cfg<DT, DT_OUT, AROWS, 2, 8, 1, 16, EPI>(p, s);
+    return launch_cfg<DT, DT_OUT, AROWS, 2, 8, 1, 16, EPI, PRO>(p, s);
 }
 
-template <int DT, int DT_OUT, int EPI>
+template <int DT, int DT_OUT, int EPI, int PRO = PRO_NONE>
 int launch_epi(const Problem& p, hipStream_t s) {
-    if (p.m <= 8) return launch_rows<DT, DT_OUT, EPI, 8>(p, s);
-    if (p.m <= 16) return launch_rows<DT, DT_OUT, EPI, 16>(p, s);
-    return launch_rows<DT, DT_OUT, EPI, 32>(p, s);
+    if (p.m <= 8) return launch_rows<DT, DT_OUT, EPI, 8, PRO>(p, s);
+    if (p.m <= 16) return launch_rows<DT, DT_OUT, EPI, 16, PRO>(p, s);
+    return launch_rows<DT, DT_OUT, EPI, 32, PRO>(p, s);
 }
 
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
-    if (p.epi == EPI_SILU_MUL) return launch_epi<DT, DT_OUT, EPI_SILU_MUL>(p, s);
+    if (p.epi == EPI_SILU_MUL) {
+        if (p.pro == PRO_ADD_NORM) return launch_epi<DT, DT_OUT, EPI_SILU_MUL, PRO_ADD_NORM>(p, s);
+        return launch_epi<DT, DT_OUT, EPI_SILU_MUL>(p, s);
+    }
+    if (p.pro == PRO_GATE) return launch_epi<DT, DT_OUT, EPI_NONE, PRO_GATE>(p, s);
+    if (p.pro == PRO_ADD_NORM) return launch_epi<DT, DT_OUT, EPI_NONE, PRO_ADD_NORM>(p, s);
     return launch_epi<DT, DT_OUT, EPI_NONE>(p, s);
 }
 

@@ -38,11 +38,13 @@ __device__ u32x4_t g_zero_chunk = {0u, 0u, 0u, 0u};
 __device__ __forceinline__ int lds_swizzle(int row) { return (row >> 1) & 7; }
 
 
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI>
+// RS: output row i is multiplied by row_scale[i] before rounding (with
+// EPI_NONE or EPI_SILU_MUL, where it scales both sums of a pair).
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS>
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n, int c_vec, uint64_t* __restrict__ keys) {
+    int tiles_m, int tiles_n, int c_vec, uint64_t* __restrict__ keys, const float* __restrict__ row_scale) {
     constexpr int NW = WGM * WGN;        // waves, in a WGM x WGN grid
     constexpr int NT = NW * 64;          // threads
     constexpr int WM = BM / WGM;         // wave tile rows (M)
@@ -58,6 +60,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // rows of the same output columns, so block pair (2i, 2i + 1) of a wave
     // holds gate and up values of one 32-column group in the same lanes.
     static_assert(EPI != EPI_SILU_MUL || NI % 2 == 0, "gate/up pairs per wave");
+    static_assert(!RS || EPI != EPI_ARGMAX, "row scale with a stored output");
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;   // output columns per tile
 
     // LDS: the ring of K-tile stages, reused after the K loop for the C tile.
@@ -80,7 +83,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // inside the K loop shares the LDS counter with the fragment reads and
     // completes out of order, which would turn every fragment wait into
     // lgkmcnt(0).
-    asm volatile("" :: "s"(c), "s"(ldc), "s"(c_vec), "s"(m), "s"(n), "s"(keys));
+    asm volatile("" :: "s"(c), "s"(ldc), "s"(c_vec), "s"(m), "s"(n), "s"(keys), "s"(row_scale));
 
     int tm, tn;
     grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
@@ -226,6 +229,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
         const int row = wm * WM + 32 * j + r32;
+        float rs = 1.0f;
+        if constexpr (RS) rs = row_scale[min_i64(m0 + row, m - 1)];
 #pragma unroll
         for (int i = 0; i < NIO; ++i) {
 #pragma unroll
@@ -235,13 +240,23 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
                 if constexpr (EPI == EPI_SILU_MUL) {
                     const f32x16_t& g = acc[2 * i][j];
                     const f32x16_t& u = acc[2 * i + 1][j];
-                    x0 = silu_f32(g[4 * q]) * u[4 * q];
-                    x1 = silu_f32(g[4 * q + 1]) * u[4 * q + 1];
-                    x2 = silu_f32(g[4 * q + 2]) * u[4 * q + 2];
-                    x3 = silu_f32(g[4 * q + 3]) * u[4 * q + 3];
+                    if constexpr (RS) {
+                        x0 = silu_f32(g[4 * q] * rs) * (u[4 * q] * rs);
+                        x1 = silu_f32(g[4 * q + 1] * rs) * (u[4 * q + 1] * rs);
+                        x2 = silu_f32(g[4 * q + 2] * rs) * (u[4 * q + 2] * rs);
+                        x3 = silu_f32(g[4 * q + 3] * rs) * (u[4 * q + 3] * rs);
+                    } else {
+                        x0 = silu_f32(g[4 * q]) * u[4 * q];
+                        x1 = silu_f32(g[4 * q + 1]) * u[4 * q + 1];
+                        x2 = silu_f32(g[4 * q + 2]) * u[4 * q + 2];
+                        x3 = silu_f32(g[4 * q + 3]) * u[4 * q + 3];
+                    }
                 } else {
                     const f32x16_t& v = acc[i][j];
                     x0 = v[4 * q]; x1 = v[4 * q + 1]; x2 = v[4 * q + 2]; x3 = v[4 * q + 3];
+                    if constexpr (RS) {
+                        x0 *= rs; x1 *= rs; x2 *= rs; x3 *= rs;
+                    }
                 }
                 char* dst = ctile + row * PITCH + col * OB;
                 if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
@@ -322,7 +337,7 @@ int choose_stages(int64_t m, int64_t n) {
     return tiles <= kCus ? 3 : 2;
 }
 
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI>
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS>
 int launch_tile(const Problem& p, hipStream_t s) {
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;
     const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BNO - 1) / BNO;
@@ -333,22 +348,27 @@ int launch_tile(const Problem& p, hipStream_t s) {
     // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
     const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && ((p.ldc * out_bytes) % 16 == 0);
     if (EPI == EPI_ARGMAX) *p.key_blocks = tiles_n;
-    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI>), grid, block, 0, s,
+    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI, RS>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c,
-                       p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec, p.keys);
+                       p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec, p.keys,
+                       p.row_scale);
     return check_launch("mfma_staged");
 }
 
-template <int DT, int DT_OUT, int EPI>
+template <int DT, int DT_OUT, int EPI, int RS = 0>
 int launch_epi(const Problem& p, hipStream_t s) {
     // A fused gate/up tile covers 64 output columns from 128 W rows.
     const int64_t n_tiles = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
-    if (choose_stages(p.m, n_tiles) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI>(p, s);
-    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI>(p, s);
+    if (choose_stages(p.m, n_tiles) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI, RS>(p, s);
+    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS>(p, s);
 }
 
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
+    if (p.row_scale != nullptr) {
+        if (p.epi == EPI_SILU_MUL) return launch_epi<DT, DT_OUT, EPI_SILU_MUL, 1>(p, s);
+        return launch_epi<DT, DT_OUT, EPI_NONE, 1>(p, s);
+    }
     if (p.epi == EPI_SILU_MUL) return launch_epi<DT, DT_OUT, EPI_SILU_MUL>(p, s);
     return launch_epi<DT, DT_OUT, EPI_NONE>(p, s);
 }

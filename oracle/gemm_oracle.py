@@ -21,7 +21,11 @@ path (paths relative to the reference repo):
     compare_result (gemm_wmma.cu:209-247), check_result (common.cuh:18-31);
   * the dispatch policy supports_wmma / choose_path (gemm_bench.cu:252-273),
     the shape table kDefaultShapes (gemm_bench.cu:45-57) and the repeat
-    rule (gemm_bench.cu:371-379).
+    rule (gemm_bench.cu:371-379);
+  * next to the GEMM (nanovllm/): SiluAndMul (layers/activation.py:8-11),
+    the greedy sampler's argmax (layers/sampler.py:19-32), the output gate
+    of gated attention (models/qwen3_5.py:95) and the residual add +
+    zero-centred RMSNorm (layers/layernorm.py:131-142).
 
 Pinning (what fixes each function independently of this file): the KAT
 results are checked against exact integer arithmetic and against the
@@ -357,6 +361,11 @@ def silu_mul_tolerance(r64, g64, u64, sg64, su64, k: int, dtype: str, ulps: floa
     place of `dtype` at the exact value."""
     dg = fp32_accumulation_bound(sg64, k)
     du = fp32_accumulation_bound(su64, k)
+    return silu_mul_bound(r64, g64, u64, dg, du, dtype, ulps)
+
+
+def silu_mul_bound(r64, g64, u64, dg, du, dtype: str, ulps: float = 2.0) -> np.ndarray:
+    """silu_mul_tolerance for given error bounds dg, du of the two sums."""
     g64 = np.asarray(g64, dtype=np.float64)
     u64 = np.asarray(u64, dtype=np.float64)
     r64 = np.asarray(r64, dtype=np.float64)
@@ -385,3 +394,71 @@ def greedy_token_admissible(token: np.ndarray, r64: np.ndarray, s64: np.ndarray,
     best = r64.max(axis=-1)
     chosen = r64[rows, token]
     return chosen >= best - bound[rows, token] - bound.max(axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# Prologues on A
+# ---------------------------------------------------------------------------
+def sigmoid_f64(x: np.ndarray) -> np.ndarray:
+    """1 / (1 + e^-x) in float64."""
+    x = np.asarray(x, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return 1.0 / (1.0 + np.exp(-x))
+
+
+def gate_view(gate_rows: np.ndarray, k: int, group: int, group_stride: int) -> np.ndarray:
+    """The [m, k] gate read through q_proj's head-strided view
+    (nanovllm/models/qwen3_5.py:81-86): element (i, k) is
+    gate_rows[i, (k // group) * group_stride + k % group], where row i of
+    gate_rows starts at the gate's first element (for the chunk of q_proj's
+    output, head_dim elements into the row)."""
+    j = np.arange(k)
+    return np.asarray(gate_rows)[:, (j // group) * group_stride + j % group]
+
+
+def sigmoid_gate(a: np.ndarray, g: np.ndarray, dtype: str) -> np.ndarray:
+    """The output gate of gated attention, `output * torch.sigmoid(gate)`
+    (qwen3_5.py:95), as two element-type tensor ops: sigmoid(g) rounded to
+    `dtype`, then the product (exact in float64 for bf16 and fp16 factors)
+    rounded to `dtype`.  a and g are storage arrays of `dtype`."""
+    s = to_f64(round_f64(sigmoid_f64(to_f64(g, dtype)), dtype), dtype)
+    return round_f64(to_f64(a, dtype) * s, dtype)
+
+
+def add_norm_operand(h: np.ndarray, r: np.ndarray, w_norm: np.ndarray, dtype: str):
+    """Residual add + zero-centred RMSNorm operand as the kernels form it
+    (Qwen3_5RMSNorm with a residual, nanovllm/layers/layernorm.py:131-142,
+    with the row scale moved behind the GEMM): s = h + r in fp32, the new
+    residual round(s) (as the reference), the GEMM operand
+    round(fp32(s * fp32(1 + w))).  Each fp32 operation is its float64 value
+    (exact for these factors) rounded once.  Returns (s as float64, operand
+    storage, residual storage)."""
+    s32 = (to_f64(h, dtype) + to_f64(r, dtype)).astype(np.float32)
+    one_w = (1.0 + to_f64(w_norm, dtype)).astype(np.float32)
+    y32 = (s32.astype(np.float64) * one_w.astype(np.float64)).astype(np.float32)
+    return s32.astype(np.float64), encode(y32, dtype), encode(s32, dtype)
+
+
+def norm_scale_f64(s64: np.ndarray, eps: float) -> np.ndarray:
+    """rsqrt(mean_k s^2 + eps) per row, in float64 (layernorm.py:126-128)."""
+    s64 = np.asarray(s64, dtype=np.float64)
+    return 1.0 / np.sqrt((s64 * s64).mean(axis=-1) + eps)
+
+
+def norm_scale_error(k: int) -> float:
+    """Relative error bound of the fp32 row scale: the sum of k positive
+    squares (k 2^-24), the divide by k and the add of eps, the square root
+    (which halves the error of its input) and the reciprocal, plus the
+    multiply that applies it: (k / 2 + 4) 2^-24, taken as k 2^-24 + 2^-21."""
+    return k * 2.0 ** -24 + 2.0 ** -21
+
+
+def add_norm_gemm_tolerance(r64, sy64, scale64, k: int, dtype: str, ulps: float = 2.0) -> np.ndarray:
+    """Bound for scale~ * (fp32 sum of the operand times w) rounded once to
+    `dtype`, against r64 = scale * sum in float64: the fp32 accumulation
+    (scaled), the fp32 row scale's relative error on the value, `ulps` of
+    the output type.  sy64 = sum_k |y w|."""
+    r64 = np.asarray(r64, dtype=np.float64)
+    scale = np.asarray(scale64, dtype=np.float64)[:, None]
+    return (ulps * ulp_at(r64, dtype) + scale * fp32_accumulation_bound(sy64, k)
+            + norm_scale_error(k) * np.abs(r64))

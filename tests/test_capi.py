@@ -252,3 +252,76 @@ def test_argmax_validates_before_launch(lib):
     rc = lib.nanovllm_gemm_argmax_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, None, 33, 64, 16, 16, 16,
                                               BF16, dummy, 10 ** 6, None)
     assert rc == L.EUNSUPPORTED
+
+
+# ---------------------------------------------------------------------------
+# GEMMs with a prologue (output gate, residual add + RMSNorm)
+# ---------------------------------------------------------------------------
+def test_prologue_workspace_bytes():
+    # enough for any kernel: the gated operand (M x K elements), plus for the
+    # norm the fp32 row scales, each rounded up to 256 bytes
+    assert L.gated_workspace_bytes(32, 2048, 256, BF16) == 32 * 2048 * 2
+    assert L.gated_workspace_bytes(4, 160, 40, BF16) == 1280
+    assert L.gated_workspace_bytes(4, 100, 40, BF16) == L.EINVAL      # group does not divide K
+    assert L.gated_workspace_bytes(4, 128, 64, F32) == L.EUNSUPPORTED
+    assert L.add_rmsnorm_workspace_bytes(32, 1024, BF16) == 32 * 2048 + 256
+    assert L.add_rmsnorm_workspace_bytes(33, 1000, F16) == (33 * 2000 + 255) // 256 * 256 + 256
+    assert L.add_rmsnorm_workspace_bytes(-1, 1024, BF16) == L.EINVAL
+
+
+def test_gated_validates_before_launch(lib):
+    d = 1 << 20
+    call = lambda *a: lib.nanovllm_gemm_gated(*a)  # noqa: E731
+    # m = 0 is a no-op even with null pointers
+    assert call(None, None, None, None, 0, 64, 512, 512, 1024, 256, 512, 512, 64, BF16, BF16, None, 0, None) == L.OK
+    rc = call(None, None, None, None, 4, 64, 512, 512, 1024, 256, 512, 512, 64, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "non-null" in L.last_error()
+    rc = call(d, d, d, d, 4, 64, 512, 512, 1024, 200, 512, 512, 64, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "divide" in L.last_error()
+    rc = call(d, d, d, d, 4, 64, 512, 512, 1024, 256, 128, 512, 64, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "group_stride" in L.last_error()
+    rc = call(d, d, d, d, 4, 64, 512, 512, 700, 256, 512, 512, 64, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "ldg" in L.last_error()
+    rc = call(d, d + 2, d, d, 4, 64, 512, 512, 1024, 256, 512, 512, 64, BF16, BF16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "aligned" in L.last_error()
+    rc = call(d, d, d, d, 4, 64, 512, 512, 1024, 256, 512, 512, 64, F32, F32, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "float16 or bfloat16" in L.last_error()
+    # the fused path (M <= 32, head size a multiple of 64) takes no workspace
+    assert L.gated_workspace_bytes(4, 512, 256, BF16) > 0
+    # M > 32 needs the workspace
+    rc = call(d, d, d, d, 40, 64, 512, 512, 1024, 256, 512, 512, 64, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "workspace" in L.last_error()
+    # the fused gate cannot take a head size that is not a multiple of 64
+    rc = lib.nanovllm_gemm_gated_with_kernel(L.KERNEL_SPLITK_DECODE, d, d, d, d, 4, 64, 480, 480, 960, 40, 80, 480,
+                                             64, BF16, BF16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "multiple of 64" in L.last_error()
+    rc = lib.nanovllm_sigmoid_gate(d, d, d, 4, 512, 512, 1024, 256, 512, 100, BF16, None)
+    assert rc == L.EINVAL and "ldo" in L.last_error()
+
+
+def test_add_rmsnorm_validates_before_launch(lib):
+    d = 1 << 20
+    call = lambda *a: lib.nanovllm_gemm_add_rmsnorm(*a)  # noqa: E731
+    assert call(None, None, None, 1e-6, None, None, None, 0, 64, 512, 512, 512, 512, 64, 512, 0, BF16, BF16,
+                None, 0, None) == L.OK
+    rc = call(None, None, None, 1e-6, None, None, None, 4, 64, 512, 512, 512, 512, 64, 512, 0, BF16, BF16, None, 0,
+              None)
+    assert rc == L.EINVAL and "non-null" in L.last_error()
+    rc = call(d, d, d, -1.0, d, d, d, 4, 64, 512, 512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "eps" in L.last_error()
+    rc = call(d, d, d, 1e-6, d, d, d, 4, 0, 512, 512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "n must be positive" in L.last_error()
+    rc = call(d, d, d, 1e-6, d, d, d, 4, 64, 512, 500, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "ldh" in L.last_error()
+    rc = call(d, d, d, 1e-6, d, d, d + 8, 4, 64, 512, 512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "aligned" in L.last_error()
+    rc = call(d, d, d, 1e-6, d, d, d, 4, 64, 512, 512, 512, 512, 64, 512, 0, BF16, F16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "dtype" in L.last_error()
+    rc = call(d, d, d, 1e-6, d, d, d, 40, 64, 512, 512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EINVAL and "workspace" in L.last_error()
+    rc = lib.nanovllm_gemm_add_rmsnorm_with_kernel(L.KERNEL_SPLITK_DECODE, d, d, d, 1e-6, d, d, d, 40, 64, 512,
+                                                   512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "m <= 32" in L.last_error()
+    rc = lib.nanovllm_gemm_add_rmsnorm_with_kernel(L.KERNEL_GEMV_DECODE, d, d, d, 1e-6, d, d, d, 40, 64, 512,
+                                                   512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "gemv_decode" in L.last_error()

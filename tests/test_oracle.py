@@ -375,3 +375,135 @@ def test_greedy_tokens_first_index_on_ties_and_admissible():
     k = 1024   # bound = 1024 * 2^-24 = 6.1e-5
     assert orc.greedy_token_admissible(np.array([2, 3]), r, s, k).all()        # ties are admissible
     assert not orc.greedy_token_admissible(np.array([0, 1]), r, s, k).any()    # clearly smaller logits are not
+
+
+# ---------------------------------------------------------------------------
+# Prologues: output gate and residual add + RMSNorm
+# ---------------------------------------------------------------------------
+def _bf16(x) -> np.ndarray:
+    return orc.encode(np.asarray(x, dtype=np.float32), "bf16")
+
+
+def test_sigmoid_closed_forms_and_torch():
+    x = np.concatenate([np.linspace(-40, 40, 8001), [-800.0, 0.0, 800.0]])
+    got = orc.sigmoid_f64(x)
+    np.testing.assert_allclose(got, torch.sigmoid(torch.from_numpy(x)).numpy(), rtol=1e-15, atol=1e-300)
+    assert orc.sigmoid_f64(np.array([0.0]))[0] == 0.5
+    np.testing.assert_allclose(got + orc.sigmoid_f64(-x), 1.0, rtol=0, atol=1e-15)   # sigma(-x) = 1 - sigma(x)
+
+
+def test_gate_view_is_the_chunk_of_q_proj():
+    """gate_view reads q_proj(x).view(-1, H, 2D).chunk(2, -1)[1]
+    (qwen3_5.py:81-86) out of the un-chunked rows."""
+    m, heads, d = 3, 4, 8
+    q = torch.arange(m * heads * 2 * d, dtype=torch.float64).view(m, heads, 2 * d)
+    want = q.chunk(2, dim=-1)[1].reshape(m, heads * d).numpy()
+    got = orc.gate_view(q.view(m, -1).numpy()[:, d:], heads * d, d, 2 * d)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_sigmoid_gate_closed_forms():
+    a = _bf16([[3.0, -5.5, 0.375, 1e-3]])
+    half = orc.to_f64(orc.sigmoid_gate(a, _bf16([[0.0] * 4]), "bf16"), "bf16")
+    np.testing.assert_array_equal(half, orc.to_f64(a, "bf16") / 2)      # sigmoid(0) = 1/2 exactly
+    one = orc.to_f64(orc.sigmoid_gate(a, _bf16([[60.0] * 4]), "bf16"), "bf16")
+    np.testing.assert_array_equal(one, orc.to_f64(a, "bf16"))           # sigmoid(60) rounds to 1
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_sigmoid_gate_matches_torch_two_ops(dtype):
+    """`output * torch.sigmoid(gate)` (qwen3_5.py:95) run by torch on the CPU
+    in the element type: equal to the oracle except where fp32 and float64
+    sigmoids round differently next to a tie (<= 1 ulp, rare); a single
+    rounding of a * sigmoid(g) (a planted mistake) differs far more often."""
+    rng = np.random.default_rng(17)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    a = torch.from_numpy(rng.standard_normal((64, 512))).to(tdt)
+    g = torch.from_numpy(rng.standard_normal((64, 512)) * 4).to(tdt)
+    ref = a * torch.sigmoid(g)
+    store = (lambda t: t.view(torch.int16).numpy().view(np.uint16)) if dtype == "bf16" else (lambda t: t.numpy())
+    want = orc.sigmoid_gate(store(a), store(g), dtype)
+    ulps = orc.ulp_distance(store(ref), want, dtype)
+    assert ulps.max() <= 1 and float((ulps == 0).mean()) >= 0.999
+    single = orc.round_f64(a.double().numpy() * orc.sigmoid_f64(g.double().numpy()), dtype)
+    assert float((orc.ulp_distance(single, want, dtype) != 0).mean()) > 0.01
+
+
+def test_add_norm_operand_and_scale_by_hand():
+    h = _bf16([[1.5, 2.0, -3.0, 0.25]])
+    r = _bf16([[0.5, -1.0, 1.0, 0.25]])
+    w = _bf16([0.0, 1.0, -0.5, 0.0])
+    s, y, res = orc.add_norm_operand(h, r, w, "bf16")
+    np.testing.assert_array_equal(s, [[2.0, 1.0, -2.0, 0.5]])
+    np.testing.assert_array_equal(orc.to_f64(y, "bf16"), [[2.0, 2.0, -1.0, 0.5]])        # s (1 + w)
+    np.testing.assert_array_equal(orc.to_f64(res, "bf16"), s)
+    assert orc.norm_scale_f64(s, 0.0)[0] == 1.0 / math.sqrt((4 + 1 + 4 + 0.25) / 4)
+    # constant rows and an all-zero row (only eps is left)
+    np.testing.assert_allclose(orc.norm_scale_f64(np.full((1, 64), 3.0), 1e-6), 1 / math.sqrt(9 + 1e-6), rtol=1e-15)
+    assert orc.norm_scale_f64(np.zeros((1, 8)), 1e-6)[0] == 1.0 / math.sqrt(1e-6)
+
+
+def test_add_norm_residual_matches_reference_and_gemm_close():
+    """Qwen3_5RMSNorm.forward(h, residual) in torch (layernorm.py:131-142):
+    the new residual is the oracle's bit for bit; normalized @ W^T of the
+    reference (rounded after scaling) and scale * (operand @ W^T) of the
+    kernels (rounded before) differ by the two roundings only."""
+    rng = np.random.default_rng(3)
+    k = 256
+    h = torch.from_numpy(rng.standard_normal((8, k))).bfloat16()
+    r = torch.from_numpy(rng.standard_normal((8, k))).bfloat16()
+    w_norm = torch.from_numpy(rng.standard_normal(k) * 0.1).bfloat16()
+    summed = h.float() + r.float()
+    ref_res = summed.to(torch.bfloat16)
+    normalized = (summed * torch.rsqrt(summed.pow(2).mean(-1, keepdim=True) + 1e-6)
+                  * (1.0 + w_norm.float())).to(torch.bfloat16)
+    st = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    s64, y, res = orc.add_norm_operand(st(h), st(r), st(w_norm), "bf16")
+    np.testing.assert_array_equal(res, st(ref_res))
+    scale = orc.norm_scale_f64(s64, 1e-6)
+    W = rng.standard_normal((64, k)) * 0.05
+    ours = scale[:, None] * (orc.to_f64(y, "bf16") @ W.T)
+    theirs = normalized.double().numpy() @ W.T
+    bound = 2.0 ** -7 * scale[:, None] * (np.abs(orc.to_f64(y, "bf16")) @ np.abs(W).T)
+    assert (np.abs(ours - theirs) <= bound).all()
+
+
+def test_add_norm_tolerance_accepts_fp32_kernel_and_rejects_planted():
+    """An fp32 evaluation of the kernels' formula (fp32 sums, fp32 row scale,
+    one rounding) meets add_norm_gemm_tolerance; the plausible mistakes do
+    not: residual dropped, w used instead of 1 + w, eps ignored, mean over
+    a padded K, the scale applied twice."""
+    rng = np.random.default_rng(23)
+    k, n, eps = 512, 96, 1e-6
+    h = _bf16(rng.standard_normal((24, k)))
+    r = _bf16(rng.standard_normal((24, k)))
+    tiny = _bf16(rng.standard_normal((2, k)) * 1e-3)
+    h[:2], r[:2] = tiny, tiny                            # rows where eps matters
+    w_norm = _bf16(rng.standard_normal(k) * 0.1)
+    W = orc.to_f64(_bf16(rng.standard_normal((n, k)) * 0.05), "bf16")
+    s64, y, _ = orc.add_norm_operand(h, r, w_norm, "bf16")
+    y64 = orc.to_f64(y, "bf16")
+    scale = orc.norm_scale_f64(s64, eps)
+    want = scale[:, None] * (y64 @ W.T)
+    tol = orc.add_norm_gemm_tolerance(want, np.abs(y64) @ np.abs(W).T, scale, k, "f32")
+    s32 = s64.astype(np.float32)
+    ss = (s32 * s32).sum(axis=1, dtype=np.float32)
+    scale32 = (np.float32(1.0) / np.sqrt(ss / np.float32(k) + np.float32(eps))).astype(np.float32)
+    fp32 = (y64.astype(np.float32) @ W.astype(np.float32).T) * scale32[:, None]
+    assert (np.abs(fp32.astype(np.float64) - want) <= tol).all()
+
+    def gemm_with(s_rows, one_w, eps_, k_mean):
+        y_ = orc.to_f64(_bf16((s_rows * one_w).astype(np.float32)), "bf16")
+        sc = 1.0 / np.sqrt((s_rows ** 2).sum(axis=1) / k_mean + eps_)
+        return sc[:, None] * (y_ @ W.T)
+    one_w = 1.0 + orc.to_f64(w_norm, "bf16")
+    h64 = orc.to_f64(h, "bf16")
+    planted = {
+        "residual dropped": gemm_with(h64, one_w, eps, k),
+        "w instead of 1 + w": gemm_with(s64, one_w - 1.0, eps, k),
+        "eps ignored": gemm_with(s64, one_w, 0.0, k),
+        "mean over K + 8": gemm_with(s64, one_w, eps, k + 8),
+        "scale applied twice": want * scale[:, None],
+    }
+    for name, bad in planted.items():
+        assert (np.abs(bad - want) > tol).any(), name
