@@ -12,9 +12,11 @@ Alongside (extra keys of the same JSON line): the decode GEMMs M in
 {1,4,8,16,32} x N=6144 x K=1024 with W rotated over more than twice the
 256 MB Infinity Cache, the FP32 1024^3 GEMM, the FP16 down projection, the
 BF16 LM head, the merged gated-delta-net input projection (one N = 8224 GEMM
-against four launches), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the
-same inputs for comparison only, and the CPU baseline (host F.linear,
-multi-threaded).
+against four launches), the fused epilogues and prologues against the
+reference's compositions (gate_up + SiLU-and-mul, the greedy LM head, the
+gated-attention output gate before o_proj, the residual add + RMSNorm before
+a projection), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
+for comparison only, and the CPU baseline (host F.linear, multi-threaded).
 
 Prints ONE JSON line on stdout; a readable table goes to stderr.
 """
@@ -397,6 +399,103 @@ def main() -> int:
             log(f"lm head greedy M={lm}: fused {t_g * 1e3:.1f} us, fp32 logits + torch argmax {t_l * 1e3:.1f} us")
         extras["lm_head_greedy_bf16_n151936_k1024"] = l_rows
         del l_ws, l_w0
+
+        # ------------------- gated-attention output gate fused before o_proj
+        # Against the reference's path: `output * torch.sigmoid(gate)` on the
+        # GPU (two element-type ops, qwen3_5.py:95), then the o_proj GEMM.
+        PK = pkg.kernels
+        heads, hd, o_n = 8, 256, 1024
+        o_k = heads * hd
+        o_gen = torch.Generator().manual_seed(1011)
+        o_w = (torch.randn(o_n, o_k, generator=o_gen) * 0.02).bfloat16().to(dev)
+        o_rows = []
+        for om in (1, 8, 32, 2048):
+            o_copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (o_w.numel() * 2)) + 1) if om <= 32 else 1
+            o_ws = [o_w] + [o_w.clone() for _ in range(o_copies - 1)]
+            o_a = torch.randn(om, heads, hd, generator=o_gen).bfloat16().to(dev)
+            o_q = (torch.randn(om, heads, 2 * hd, generator=o_gen) * 2).bfloat16().to(dev)
+            o_gate = o_q.chunk(2, -1)[1]
+            o_out = torch.empty(om, o_n, dtype=torch.bfloat16, device=dev)
+            o_need = L.gated_workspace_bytes(om, o_k, hd, L.BF16)
+            o_buf = torch.empty(o_need, dtype=torch.uint8, device=dev)
+            o_gated = torch.empty(om, o_k, dtype=torch.bfloat16, device=dev)
+
+            def gated(wt, o_a=o_a, o_gate=o_gate, o_out=o_out, o_buf=o_buf, om=om, o_need=o_need):
+                args_ = (o_a.data_ptr(), o_gate.data_ptr(), wt.data_ptr(), o_out.data_ptr(), om, o_n, o_k, o_k,
+                         o_gate.stride(0), hd, o_gate.stride(1), o_k, o_n, L.BF16, L.BF16, o_buf.data_ptr(), o_need)
+
+                def f():
+                    L.gated_raw(*args_, torch.cuda.current_stream().cuda_stream)
+                return f
+
+            def gate_then_gemm(wt, o_a=o_a, o_gate=o_gate, o_gated=o_gated, o_out=o_out, om=om):
+                gemm = launcher(o_gated, wt, o_out, om, o_n, o_k, L.B_NK, torch.bfloat16, torch.bfloat16)
+
+                def f():
+                    torch.mul(o_a, torch.sigmoid(o_gate), out=o_gated.view(om, heads, hd))
+                    gemm()
+                return f
+            reps = min(o_copies * 2, 400) if om <= 32 else 40
+            t_f = median_graph_ms(torch, [gated(o_ws[i % o_copies]) for i in range(reps)])
+            t_u = median_graph_ms(torch, [gate_then_gemm(o_ws[i % o_copies]) for i in range(reps)])
+            o_rows.append({"m": om, "fused_us": round(t_f * 1e3, 3), "torch_gate_then_gemm_us": round(t_u * 1e3, 3),
+                           "speedup": round(t_u / t_f, 3), "fused_in_gemm": om <= 8})
+            log(f"o_proj with output gate M={om}: fused {t_f * 1e3:.2f} us, "
+                f"torch sigmoid gate + GEMM {t_u * 1e3:.2f} us")
+            del o_ws
+        extras["attn_o_proj_gated_bf16_n1024_k2048"] = o_rows
+        del o_w
+
+        # ----------- residual add + RMSNorm fused before the next projection
+        # Against the reference's path: Qwen3_5RMSNorm(h, residual) in eager
+        # torch (layernorm.py:131-142), then the GEMM (for the MLP block, the
+        # fused gate_up + SiLU GEMM).
+        n_rows = []
+        n_gen = torch.Generator().manual_seed(1013)
+        for label, n_out, silu in (("gdn_in_proj_n8224", 8224, False), ("mlp_gate_up_silu_n3584", 3584, True)):
+            n_w = (torch.randn((2 if silu else 1) * n_out, 1024, generator=n_gen) * 0.02).bfloat16().to(dev)
+            n_nw = (torch.randn(1024, generator=n_gen) * 0.1).bfloat16().to(dev)
+            for nm in (1, 32, 2048):
+                n_copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (n_w.numel() * 2)) + 1) if nm <= 32 else 1
+                n_ws = [n_w] + [n_w.clone() for _ in range(n_copies - 1)]
+                n_h = torch.randn(nm, 1024, generator=n_gen).bfloat16().to(dev)
+                n_r = torch.randn(nm, 1024, generator=n_gen).bfloat16().to(dev)
+                n_out_t = torch.empty(nm, n_out, dtype=torch.bfloat16, device=dev)
+                n_res = torch.empty(nm, 1024, dtype=torch.bfloat16, device=dev)
+                n_need = L.add_rmsnorm_workspace_bytes(nm, 1024, L.BF16)
+                n_buf = torch.empty(n_need, dtype=torch.uint8, device=dev)
+
+                def fused_norm(wt, n_h=n_h, n_r=n_r, n_out_t=n_out_t, n_res=n_res, n_buf=n_buf, nm=nm,
+                               n_need=n_need, n_nw=n_nw, n_out=n_out, silu=silu):
+                    args_ = (n_h.data_ptr(), n_r.data_ptr(), n_nw.data_ptr(), 1e-6, wt.data_ptr(), n_out_t.data_ptr(),
+                             n_res.data_ptr(), nm, n_out, 1024, 1024, 1024, 1024, n_out, 1024, silu, L.BF16, L.BF16,
+                             n_buf.data_ptr(), n_need)
+
+                    def f():
+                        L.add_rmsnorm_raw(*args_, torch.cuda.current_stream().cuda_stream)
+                    return f
+
+                def norm_then_gemm(wt, n_h=n_h, n_r=n_r, n_out_t=n_out_t, nm=nm, n_nw=n_nw, n_out=n_out, silu=silu):
+                    def f():
+                        normed, _ = PK.torch_add_rmsnorm(n_h, n_r, n_nw, 1e-6)
+                        if silu:
+                            L.silu_mul_raw(normed.data_ptr(), wt.data_ptr(), n_out_t.data_ptr(), nm, n_out, 1024,
+                                           1024, 1024, n_out, L.BF16, L.BF16, torch.cuda.current_stream().cuda_stream)
+                        else:
+                            L.gemm_raw(normed.data_ptr(), wt.data_ptr(), n_out_t.data_ptr(), nm, n_out, 1024, 1024,
+                                       1024, n_out, L.B_NK, L.BF16, L.BF16, torch.cuda.current_stream().cuda_stream)
+                    return f
+                reps = min(n_copies * 2, 200) if nm <= 32 else 20
+                t_f = median_graph_ms(torch, [fused_norm(n_ws[i % n_copies]) for i in range(reps)])
+                t_u = median_graph_ms(torch, [norm_then_gemm(n_ws[i % n_copies]) for i in range(reps)])
+                n_rows.append({"block": label, "m": nm, "fused_us": round(t_f * 1e3, 3),
+                               "torch_norm_then_gemm_us": round(t_u * 1e3, 3), "speedup": round(t_u / t_f, 3),
+                               "fused_in_gemm": nm <= 32})
+                log(f"add+RMSNorm before {label} M={nm}: fused {t_f * 1e3:.2f} us, "
+                    f"torch Qwen3_5RMSNorm + GEMM {t_u * 1e3:.2f} us")
+                del n_ws
+            del n_w
+        extras["add_rmsnorm_before_projection_bf16_k1024"] = n_rows
 
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:

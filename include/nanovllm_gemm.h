@@ -230,11 +230,12 @@ int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k,
  * (qwen3_5.py:81-86): element (i, k) at
  *     gate[i * ldg + (k / group) * group_stride + k % group]
  * (group = head_dim, group_stride = 2 head_dim for q_gate; a contiguous
- * [m, k] gate is group = group_stride = k).  For m <= 32 and group a
+ * [m, k] gate is group = group_stride = k).  For m <= 8 and group a
  * multiple of 64 the gate is applied inside the split-K decode kernel (one
- * launch, no workspace); otherwise a gate kernel writes the gated operand to
- * the workspace (nanovllm_gemm_gated_workspace_bytes() bytes) and the GEMM
- * the selection table picks reads it.  Inputs f16 or bf16, output the input
+ * launch, no workspace; every workgroup gates all of A, which stops paying
+ * above m = 8); otherwise a gate kernel writes the gated operand to the
+ * workspace (nanovllm_gemm_gated_workspace_bytes() bytes) and the GEMM the
+ * selection table picks reads it.  Inputs f16 or bf16, output the input
  * type or f32, on the vector path (16-byte aligned a, gate and w; k, lda,
  * ldg, group, group_stride and ldw multiples of 8).  Asynchronous, no
  * allocation, capturable. */

@@ -332,9 +332,15 @@ bool gated_vector_ok(int64_t k, int64_t lda, int64_t ldg, int64_t group, int64_t
            group_stride % 8 == 0;
 }
 
+// The fused gate runs inside splitk_decode up to this M.  Every workgroup
+// gates all of A, so the sigmoids grow with M times the workgroup count; on
+// the Qwen3.5 o_proj (N = 1024, K = 2048) fused / gate kernel + GEMM measured
+// 4.7 / 5.4 us at M = 1, 6.1 / 6.6 us at M = 8, 9.9 / 7.0 us at M = 16.
+constexpr int64_t kGateFusedMaxM = 8;
+
 // The fused path copies whole 64-element lines of the gate, so a line must
 // not straddle two gate groups.
-bool gated_fused(int64_t m, int64_t group) { return m <= kDecodeMaxM && group % 64 == 0; }
+bool gated_fused(int64_t m, int64_t group) { return m <= kGateFusedMaxM && group % 64 == 0; }
 
 // Enough for any kernel that can run the problem (the fused gate uses none).
 int64_t gated_workspace_bytes(int64_t m, int64_t k) { return round_up_256(m * k * 2); }
@@ -356,7 +362,7 @@ int gated_entry(int forced_kernel, const void* a, const void* gate, const void* 
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool fused = forced_kernel < 0 ? gated_fused(m, group) : forced_kernel == NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
     if (fused) {
-        if (!gated_fused(m, group))
+        if (!(m <= kDecodeMaxM && group % 64 == 0))
             return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
                              "the fused gate runs in splitk_decode for m <= 32 and group a multiple of 64 "
                              "(m=%lld group=%lld)", (long long)m, (long long)group);

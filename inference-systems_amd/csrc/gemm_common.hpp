@@ -191,9 +191,31 @@ __device__ __forceinline__ float silu_f32(float x) {
     return x / (1.0f + expf(-x));
 }
 
-// sigmoid(x) = 1 / (1 + e^-x) in fp32 (library exp, IEEE divide).
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) with the hardware base-2 exponential
+// and reciprocal (v_exp_f32, v_rcp_f32, each within 1 ulp in fp32): six
+// instructions against ~50 for the library exp and IEEE divide, which
+// matters because every workgroup of a decode GEMM gates all of A.  Its
+// result is rounded to bf16 / fp16 next, where the difference from a
+// correctly rounded sigmoid decides the rounding only next to a tie.  Large
+// negative x: 2^(+large) = inf, 1 / inf = 0; large positive x: 1 / 1 = 1.
 __device__ __forceinline__ float sigmoid_f32(float x) {
-    return 1.0f / (1.0f + expf(-x));
+    constexpr float kLog2e = 1.44269504088896340736f;
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
+// fp32 -> one bf16 / fp16 element (round to nearest even; the same
+// conversion pack2 applies to pairs).
+template <int DT>
+__device__ __forceinline__ uint16_t round_half(float x) {
+    if constexpr (DT == NANOVLLM_GEMM_BF16) return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+    else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// PRO_GATE on one element: round(a * round(sigmoid(g))).
+template <int DT>
+__device__ __forceinline__ uint16_t gate1(uint16_t a, uint16_t g) {
+    const uint16_t sg = round_half<DT>(sigmoid_f32(half_to_f32<DT>(g)));
+    return round_half<DT>(half_to_f32<DT>(a) * half_to_f32<DT>(sg));
 }
 
 // PRO_GATE on 8 packed elements: round(a * round(sigmoid(g))), each product

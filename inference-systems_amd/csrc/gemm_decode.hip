@@ -117,6 +117,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const int64_t lines = (k + kLine - 1) / kLine;
     const uint32_t base = lds_address(&buf[wave][0]);
     f32x4_t acc[PW][RG][MG];
+    // PRO_ADD_NORM: this lane's sum of s^2 for its fragment rows.
     float ss[MG];
 #pragma unroll
     for (int g = 0; g < MG; ++g) ss[g] = 0.0f;
@@ -170,6 +171,28 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                 }
             }
             wait_vmcnt<0>();
+            if constexpr (PRO == PRO_GATE) {
+                // The gate, in place on this batch's copies of A: lane j takes
+                // column j of each line for the M real rows only (the copy's
+                // rows past M repeat row M - 1 and their outputs are not
+                // stored), so the work per lane is M sigmoids a line (against
+                // 16 per lane on fragments at M <= 8).  Row r sits in copy
+                // r / 8 at 16-bit position 8 (8 (r % 8) + ((j / 8) ^ (r % 8))) + j % 8.
+#pragma unroll
+                for (int t = 0; t < LPB; ++t) {
+                    const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
+                    if (line >= lines) break;
+                    uint16_t* lh = reinterpret_cast<uint16_t*>(&buf[wave][t * IL * 64]);
+#pragma unroll
+                    for (int r = 0; r < AROWS; ++r) {
+                        if (r >= m) break;
+                        const int r8v = r & 7;
+                        const int pos = 8 * (8 * r8v + ((lane >> 3) ^ r8v)) + (lane & 7);
+                        uint16_t* ap = lh + (IW + (r >> 3)) * 512 + pos;
+                        *ap = gate1<DT>(*ap, lh[(IW + IA + (r >> 3)) * 512 + pos]);
+                    }
+                }
+            }
 #pragma unroll
             for (int t = 0; t < LPB; ++t) {
                 const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
@@ -184,25 +207,23 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                     for (int r = 0; r < RG; ++r) wf[r] = lb[(2 * r + hi) * 64 + slot];
 #pragma unroll
                     for (int g = 0; g < MG; ++g) af[g] = lb[(IW + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot];
-                    if constexpr (PRO == PRO_GATE) {
-#pragma unroll
-                        for (int g = 0; g < MG; ++g)
-                            af[g] = gate8<DT>(af[g], lb[(IW + IA + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot]);
-                    }
                     if constexpr (PRO == PRO_ADD_NORM) {
                         // Element k of this fragment chunk; chunks past K are zero in h and r.
                         const int64_t kc = line * kLine + (4 * st + grp) * 8;
                         const bool in_k = kc < k;
                         const u32x4_t wv = in_k ? nwv[t][st] : u32x4_t{0u, 0u, 0u, 0u};
+                        // Every workgroup forms s for all of A; line L's new residual is
+                        // written by workgroup L mod gridDim.x.
+                        const bool writes =
+                            __builtin_amdgcn_readfirstlane(int(uint32_t(line) % gridDim.x)) == int(blockIdx.x);
 #pragma unroll
                         for (int g = 0; g < MG; ++g) {
                             u32x4_t res;
                             af[g] = add_norm8<DT>(af[g], lb[(IW + IA + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot],
                                                   wv, ss[g], res);
-                            // Workgroup 0 writes the new residual (each element once: rows
-                            // 8..15 of an 8-row copy repeat rows 0..7).
+                            // each element once: rows 8..15 of an 8-row copy repeat rows 0..7
                             const int64_t row = 16 * g + i16;
-                            if (blockIdx.x == 0 && in_k && row < m && (AROWS != 8 || i16 < 8))
+                            if (writes && in_k && row < m && (AROWS != 8 || i16 < 8))
                                 *reinterpret_cast<u32x4_t*>(pro.res_out + row * pro.ldres + kc) = res;
                         }
                     }

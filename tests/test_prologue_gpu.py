@@ -89,8 +89,9 @@ def test_sigmoid_gate_kernel_vs_oracle(dtype, view):
                          ids=["bf16", "f16-f32"])
 def test_gemm_gated_fused_equals_gate_then_gemm(m, dtype, dout):
     """Qwen3.5 o_proj (N = 1024, K = 8 heads x 256): the gate inside
-    splitk_decode gives the same bits as the gate kernel followed by
-    splitk_decode, and that meets the GEMM bound on the gated operand."""
+    splitk_decode (forced here at every M; the default fuses it up to M = 8)
+    gives the same bits as the gate kernel followed by splitk_decode, and so
+    does the default path; that meets the GEMM bound on the gated operand."""
     gen = torch.Generator().manual_seed(100 + m)
     heads, hd, n = 8, 256, 1024
     a = torch.randn((m, heads, hd), generator=gen).to(dtype).to(DEV)
@@ -98,11 +99,13 @@ def test_gemm_gated_fused_equals_gate_then_gemm(m, dtype, dout):
     gate = q_gate.to(DEV).chunk(2, -1)[1]
     w = (torch.randn((n, heads * hd), generator=gen) * 0.02).to(dtype).to(DEV)
     _say(f"gemm_gated fused M={m} {NAME[dtype]}->{NAME[dout]}")
-    fused = K.gemm_gated(a, gate, w, dout)
+    fused = K.gemm_gated_with_kernel(a, gate, w, L.KERNEL_SPLITK_DECODE, dout)
+    default = K.gemm_gated(a, gate, w, dout)
     operand = K.sigmoid_gate(a, gate)
     composed = PKG.kernels.gemm_with_kernel(operand, w, L.KERNEL_SPLITK_DECODE, dout)
     torch.cuda.synchronize()
     assert torch.equal(fused, composed)
+    assert torch.equal(default, composed)
     a64, w64 = _value(operand), _value(w)
     r = orc.gemm_f64(a64, w64)
     tol = orc.gemm_tolerance(r, orc.abs_products_f64(a64, w64), heads * hd, NAME[dout])
