@@ -1,5 +1,5 @@
 """nano-vLLM layer mirrors whose matmul is the MI355X GEMM (see linear.py,
-gdn_projection.py and mlp.py)."""
+gdn_projection.py and mlp.py) and the Qwen3.5 RMSNorm (norm.py)."""
 from .gdn_projection import GdnInputProjection
 from .linear import (
     ColumnParallelLinear,
@@ -12,6 +12,7 @@ from .linear import (
     RowParallelLinear,
 )
 from .mlp import Qwen35MLP
+from .norm import Qwen35RMSNorm
 
 __all__ = [
     "ColumnParallelLinear",
@@ -22,6 +23,7 @@ __all__ = [
     "ParallelLMHead",
     "QKVParallelLinear",
     "Qwen35MLP",
+    "Qwen35RMSNorm",
     "ReplicatedLinear",
     "RowParallelLinear",
 ]

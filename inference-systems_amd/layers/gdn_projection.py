@@ -24,6 +24,7 @@ from typing import Optional
 import torch
 from torch import nn
 
+from ..kernels import add_rmsnorm_linear
 from ..kernels import linear as gemm_linear
 from .linear import _tp_rank_size, divide
 
@@ -80,3 +81,13 @@ class GdnInputProjection(nn.Module):
         y = gemm_linear(x, self.weight, None, backend=self.gemm_backend)
         qkv, z, b, a = y.split(self.output_sizes, dim=-1)
         return qkv, z, b, a
+
+    def forward_add_norm(self, hidden: torch.Tensor, residual: torch.Tensor, norm):
+        """``(self(norm(hidden, residual)), new residual)``: the input norm of
+        a linear-attention decoder layer and the merged projection
+        (nanovllm/models/qwen3_5.py:157-163).  On the HIP path the residual
+        add and the norm run inside the GEMM."""
+        y, new_residual = add_rmsnorm_linear(hidden, residual, norm.weight, norm.eps, self.weight,
+                                             backend=self.gemm_backend)
+        qkv, z, b, a = y.split(self.output_sizes, dim=-1)
+        return (qkv, z, b, a), new_residual

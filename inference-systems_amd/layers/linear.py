@@ -20,7 +20,7 @@ import torch
 import torch.distributed as dist
 from torch import nn
 
-from ..kernels import greedy_linear
+from ..kernels import gated_linear, greedy_linear
 from ..kernels import linear as gemm_linear
 
 
@@ -148,6 +148,19 @@ class RowParallelLinear(LinearBase):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         y = self.matmul(x, self.bias if self.tp_rank == 0 else None)
+        if self.tp_size > 1:
+            dist.all_reduce(y)
+        return y
+
+    def forward_gated(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        """``self(x * sigmoid(gate))``: the output gate of Qwen3.5 gated
+        attention before o_proj (nanovllm/models/qwen3_5.py:95-96).  ``x`` is
+        this rank's heads [M, heads, head_dim] (or [M, K]) and ``gate`` the
+        matching view of q_proj's output; on the HIP path the gate is applied
+        in front of the GEMM."""
+        y = gated_linear(x, gate, self.weight, backend=self.gemm_backend)
+        if self.bias is not None and self.tp_rank == 0:
+            y = y + self.bias.to(y.dtype)
         if self.tp_size > 1:
             dist.all_reduce(y)
         return y

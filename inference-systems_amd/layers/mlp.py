@@ -17,8 +17,9 @@ from typing import Optional
 import torch
 from torch import nn
 
-from ..kernels import silu_mul_linear
+from ..kernels import add_rmsnorm_linear, silu_mul_linear
 from .linear import MergedColumnParallelLinear, RowParallelLinear
+from .norm import Qwen35RMSNorm
 
 
 class Qwen35MLP(nn.Module):
@@ -46,3 +47,13 @@ class Qwen35MLP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         h = silu_mul_linear(x, self.gate_up_proj.weight, backend=self._gemm_backend)
         return self.down_proj(h)
+
+    def forward_add_norm(self, hidden: torch.Tensor, residual: torch.Tensor,
+                         norm: Qwen35RMSNorm) -> tuple[torch.Tensor, torch.Tensor]:
+        """``self(norm(hidden, residual))`` with the new residual: the
+        post-attention norm and MLP of a decoder layer
+        (nanovllm/models/qwen3_5.py:200-204).  On the HIP path the residual
+        add, the norm, gate_up_proj and SiluAndMul are one launch."""
+        h, new_residual = add_rmsnorm_linear(hidden, residual, norm.weight, norm.eps, self.gate_up_proj.weight,
+                                             silu_mul=True, backend=self._gemm_backend)
+        return self.down_proj(h), new_residual

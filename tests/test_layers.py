@@ -148,6 +148,63 @@ def test_qwen35_mlp_matches_reference_composition():
         mlp(x)
 
 
+def test_qwen35_rmsnorm_mirror():
+    """Qwen3_5RMSNorm (layernorm.py:110-142): zero-centred scale, 1 + w in
+    fp32; with a residual, (round(norm(x + r)), round(x + r))."""
+    g = torch.Generator().manual_seed(4)
+    norm = Lyr.Qwen35RMSNorm(16, eps=1e-6)
+    x = torch.randn(3, 16, generator=g).bfloat16()
+    r = torch.randn(3, 16, generator=g).bfloat16()
+    # w = 0: plain RMSNorm
+    x32 = x.float()
+    want = (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + 1e-6)).bfloat16()
+    assert torch.equal(norm(x), want)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(16, generator=g) * 0.1)
+    y, new_r = norm(x, r)
+    s = x.float() + r.float()
+    assert torch.equal(new_r, s.bfloat16())
+    want = (s * torch.rsqrt(s.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + norm.weight.float())).bfloat16()
+    assert torch.equal(y, want)
+
+
+def test_forward_add_norm_and_gated_torch_paths():
+    """The fused entry points of the layers on the torch backend are the
+    reference compositions: norm then MLP / merged projection
+    (qwen3_5.py:157-163, 200-204), o_proj of x * sigmoid(gate) (:95-96)."""
+    g = torch.Generator().manual_seed(6)
+    norm = Lyr.Qwen35RMSNorm(32)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(32, generator=g) * 0.1)
+    mlp = Lyr.Qwen35MLP(32, 48)
+    for p_ in mlp.parameters():
+        with torch.no_grad():
+            p_.copy_(torch.randn(p_.shape, generator=g) * 0.1)
+    h, r = torch.randn(5, 32, generator=g), torch.randn(5, 32, generator=g)
+    for backend in ("torch", "auto"):
+        mlp.gemm_backend = backend
+        out, new_r = mlp.forward_add_norm(h, r, norm)
+        normed, want_r = norm(h, r)
+        torch.testing.assert_close(out, mlp(normed))
+        assert torch.equal(new_r, want_r)
+    proj = Lyr.GdnInputProjection(32, 2, 2, 4, 4)
+    with torch.no_grad():
+        proj.weight.copy_(torch.randn(proj.weight.shape, generator=g) * 0.1)
+    proj.gemm_backend = "auto"
+    parts, new_r = proj.forward_add_norm(h, r, norm)
+    for got, want in zip(parts, proj(norm(h, r)[0])):
+        torch.testing.assert_close(got, want)
+    o = Lyr.RowParallelLinear(16, 24)
+    with torch.no_grad():
+        o.weight.copy_(torch.randn(24, 16, generator=g))
+    o.gemm_backend = "auto"
+    attn = torch.randn(5, 2, 8, generator=g)
+    q_gate = torch.randn(5, 2, 16, generator=g)
+    gate = q_gate.chunk(2, -1)[1]
+    torch.testing.assert_close(o.forward_gated(attn, gate),
+                               F.linear((attn * torch.sigmoid(gate)).flatten(1), o.weight))
+
+
 def _tp_worker(rank, world, init_file, result_file):
     dist.init_process_group("gloo", init_method=f"file://{init_file}", rank=rank, world_size=world)
     try:
@@ -211,6 +268,19 @@ def _tp_worker(rank, world, init_file, result_file):
             ok = ok and torch.allclose(gv, full.max(-1).values, rtol=1e-6, atol=1e-6)
         else:
             ok = ok and gt is None and gv is None
+        # o_proj with the output gate: each rank holds its heads' columns of
+        # W and its heads of the attention output and the gate (the head split
+        # of the reference's tensor parallelism); the all-reduce adds them.
+        og = torch.Generator().manual_seed(14)
+        w_o = torch.randn(k, 4 * 8, generator=og)
+        attn = torch.randn(m, 4, 8, generator=og)
+        gate = torch.randn(m, 4, 16, generator=og).chunk(2, -1)[1]
+        o = Lyr.RowParallelLinear(4 * 8, k)
+        o.weight.weight_loader(o.weight, w_o)
+        o.gemm_backend = "auto"
+        mine = slice(rank * 2, rank * 2 + 2)
+        yo = o.forward_gated(attn[:, mine].contiguous(), gate[:, mine])
+        ok = ok and torch.allclose(yo, F.linear((attn * torch.sigmoid(gate)).flatten(1), w_o), rtol=1e-4, atol=1e-4)
         with open(f"{result_file}.{rank}", "w") as fh:
             fh.write("ok" if ok else "mismatch")
     finally:

@@ -200,3 +200,95 @@ def test_lm_head_greedy_hip(m):
     torch.cuda.synchronize()
     assert torch.equal(tokens, logits.argmax(-1))
     assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
+
+
+def _norm(gen, hidden=1024):
+    norm = Lyr.Qwen35RMSNorm(hidden)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(hidden, generator=gen) * 0.1)
+    return norm.to(DEV, torch.bfloat16)
+
+
+@pytest.mark.parametrize("m", [1, 8, 32, 100])
+@torch.inference_mode()
+def test_mlp_forward_add_norm_hip_graph(m):
+    """The post-attention norm + MLP of a Qwen3.5 decoder layer
+    (qwen3_5.py:200-204) on the HIP path: add + RMSNorm + gate_up + SiLU in
+    one launch (the prologue kernel + row-scaled GEMM at M = 100), then
+    down_proj; captured in a HIP graph, every replay equals eager execution;
+    the new residual equals the reference norm's, the output stays close to
+    the torch path."""
+    gen = torch.Generator().manual_seed(90 + m)
+    norm = _norm(gen)
+    mlp = Lyr.Qwen35MLP(1024, 3584)
+    _init(mlp.gate_up_proj, gen)
+    _init(mlp.down_proj, gen)
+    mlp = mlp.to(DEV, torch.bfloat16)
+    mlp.gemm_backend = "hip"
+    h_static = torch.zeros(m, 1024, dtype=torch.bfloat16, device=DEV)
+    r_static = torch.zeros(m, 1024, dtype=torch.bfloat16, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mlp.forward_add_norm(h_static, r_static, norm)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_static, res_static = mlp.forward_add_norm(h_static, r_static, norm)
+    for step in range(3):
+        h = torch.randn(m, 1024, generator=gen).bfloat16().to(DEV)
+        r = torch.randn(m, 1024, generator=gen).bfloat16().to(DEV)
+        h_static.copy_(h)
+        r_static.copy_(r)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager, eager_res = mlp.forward_add_norm(h, r, norm)
+        torch.cuda.synchronize()
+        assert torch.equal(y_static, eager) and torch.equal(res_static, eager_res), f"replay {step}"
+    mlp.gemm_backend = "torch"
+    ref, ref_res = mlp.forward_add_norm(h, r, norm)
+    assert torch.equal(eager_res, ref_res)
+    assert orc.rel_frobenius(eager.double().cpu().numpy(), ref.double().cpu().numpy()) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [1, 32, 300])
+@torch.inference_mode()
+def test_gdn_forward_add_norm_hip(m):
+    """The input norm of a linear-attention layer and the merged GDN
+    projection (qwen3_5.py:157-163) with the norm inside the GEMM."""
+    gen = torch.Generator().manual_seed(95 + m)
+    norm = _norm(gen)
+    proj = _init(Lyr.GdnInputProjection(1024, 16, 16, 128, 128), gen).to(DEV, torch.bfloat16)
+    h = torch.randn(m, 1024, generator=gen).bfloat16().to(DEV)
+    r = torch.randn(m, 1024, generator=gen).bfloat16().to(DEV)
+    proj.gemm_backend = "hip"
+    parts, res = proj.forward_add_norm(h, r, norm)
+    proj.gemm_backend = "torch"
+    ref_parts, ref_res = proj.forward_add_norm(h, r, norm)
+    torch.cuda.synchronize()
+    assert torch.equal(res, ref_res)
+    got = torch.cat(parts, -1).double().cpu().numpy()
+    ref = torch.cat(ref_parts, -1).double().cpu().numpy()
+    assert got.shape == (m, 8224) and orc.rel_frobenius(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [1, 8, 32, 300])
+@torch.inference_mode()
+def test_o_proj_forward_gated_hip(m):
+    """Qwen3.5 o_proj with the output gate (qwen3_5.py:81-96: 8 heads of 256,
+    gate = the second half of each head of q_proj's output): the layer on
+    the HIP path equals nanovllm::gemm_gated bit for bit and stays close to
+    `output * torch.sigmoid(gate)` + F.linear."""
+    gen = torch.Generator().manual_seed(99 + m)
+    o = _init(Lyr.RowParallelLinear(2048, 1024), gen).to(DEV, torch.bfloat16)
+    attn = torch.randn(m, 8, 256, generator=gen).bfloat16().to(DEV)
+    q_gate = torch.randn(m, 8, 512, generator=gen).bfloat16().to(DEV)
+    gate = q_gate.chunk(2, -1)[1]
+    o.gemm_backend = "hip"
+    y = o.forward_gated(attn, gate)
+    want = PKG.kernels.gemm_gated(attn, gate, o.weight)
+    o.gemm_backend = "torch"
+    ref = o.forward_gated(attn, gate)
+    torch.cuda.synchronize()
+    assert torch.equal(y, want)
+    assert orc.rel_frobenius(y.double().cpu().numpy(), ref.double().cpu().numpy()) <= 1e-2
