@@ -5,7 +5,8 @@
 // (cuda_kernels/gemm/src/gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
 // designed for CDNA4 instead of translated:
 //   * 128 x 128 macro tile per 256-thread workgroup (4 waves in a 2x2
-//     grid, 64 x 64 each), K-tiles of 64 elements;
+//     grid, 64 x 64 each), K-tiles of 64 elements; grids of at most 128
+//     such tiles (half the CUs) take 64 x 64 tiles (waves of 32 x 32);
 //   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging) into a ring of STAGES tile buffers; tiles t+1 .. t+STAGES-1
 //     are in flight while tile t is multiplied, and each wave waits on its
@@ -355,10 +356,33 @@ int launch_tile(const Problem& p, hipStream_t s) {
     return check_launch("mfma_staged");
 }
 
+// Grids of at most this many 128 x 128 tiles (half the CUs) take smaller
+// tiles: four times the workgroups fill the chip.  Measured on MI355X (bf16,
+// 128 x 128 against 64 x 64 tiles): 1024^3 11.7 -> 6.8 us, 512 x 4096 x 1024
+// 12.3 -> 8.1 us, 2048 x 1024 x 2048 20.6 -> 13.8 us, 512 x 1024 x 3584
+// 33.0 -> 17.0 us; from 512 tiles up 128 x 128 stays ahead (4096 x 2048 x
+// 1024: 20.2 against 27.7 us).  Every tile shape sums K in the same order,
+// so the choice does not change any result bit.
+constexpr int64_t kSmallGridTiles = kCus / 2;
+
 template <int DT, int DT_OUT, int EPI, int RS = 0>
 int launch_epi(const Problem& p, hipStream_t s) {
-    // A fused gate/up tile covers 64 output columns from 128 W rows.
+    // A fused gate/up tile covers half its W rows in output columns.
     const int64_t n_tiles = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
+    const int64_t tiles = ((p.m + 127) / 128) * ((n_tiles + 127) / 128);
+    if (tiles <= kSmallGridTiles) {
+        // A deeper ring pays off over longer K (2048 x 1024 x 2048: 13.8 us
+        // with 3 stages, 14.1 with 2; 512 x 1024 x 3584: 17.0 against 27.3).
+        const bool deep = p.k >= 2048;
+        if constexpr (EPI == EPI_NONE) {
+            if (deep) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI, RS>(p, s);
+            return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 2, EPI, RS>(p, s);
+        } else if constexpr (EPI == EPI_SILU_MUL) {
+            // gate/up pairs need two 32-row W blocks per wave
+            if (deep) return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS>(p, s);
+            return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 2, EPI, RS>(p, s);
+        }
+    }
     if (choose_stages(p.m, n_tiles) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI, RS>(p, s);
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS>(p, s);
 }
