@@ -5,13 +5,21 @@
 // (cuda_kernels/gemm/src/gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
 // designed for CDNA4 instead of translated:
 //   * 128 x 128 macro tile per 256-thread workgroup (4 waves in a 2x2
-//     grid, 64 x 64 each), K-tiles of 64 elements; grids of at most 128
-//     such tiles (half the CUs) take 64 x 64 tiles (waves of 32 x 32);
+//     grid, 64 x 64 each), K-tiles of 64 elements; grids with enough
+//     128 x 256 tiles for every CU take those (8 waves in a 2x4 grid, 64 x
+//     64 each), grids of at most 128 tiles of 128 x 128 (half the CUs) take
+//     64 x 64 tiles (waves of 32 x 32);
 //   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging) into a ring of STAGES tile buffers; tiles t+1 .. t+STAGES-1
 //     are in flight while tile t is multiplied, and each wave waits on its
 //     own vmcnt for exactly the tile it needs before the one barrier per
 //     K-tile;
+//   * with a 3-deep ring and one workgroup per CU (SP = 1) the copies of
+//     tile t+2 are spread between the MFMAs of tile t instead of issued as
+//     one burst after the barrier: a copy instruction that finds the CU's
+//     load queue full holds up every later instruction of its wave, MFMAs
+//     included, so a burst leaves the matrix units idle while the queue
+//     drains;
 //   * LDS rows of 64 elements are 8 chunks of 16 bytes; chunk c of row r
 //     sits at position c ^ ((r >> 1) & 7).  gfx950's LDS serves 16 lanes of
 //     a ds_read_b128 per clock from 64 banks (256 bytes), and with this key
@@ -25,6 +33,8 @@
 // Rows past M or N are clamped for loading and masked at the store; K-tail
 // chunks (K must be a multiple of 8) are copied from a zero chunk in device
 // memory, so the LDS tile is zero past K.
+#include <type_traits>
+
 #include "gemm_common.hpp"
 
 namespace nvg {
@@ -41,7 +51,8 @@ __device__ __forceinline__ int lds_swizzle(int row) { return (row >> 1) & 7; }
 
 // RS: output row i is multiplied by row_scale[i] before rounding (with
 // EPI_NONE or EPI_SILU_MUL, where it scales both sums of a pair).
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS>
+// SP: spread copy schedule (3-deep ring only).
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP>
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
@@ -57,6 +68,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int AHEAD = STAGES - 1;    // tiles in flight ahead of the one multiplied
     static_assert(IPW * 8 * NW == ROWS && WM % 32 == 0 && WN % 32 == 0, "tile shape");
     static_assert(AHEAD >= 1 && AHEAD <= 3 && AHEAD * IPW < 64, "vmcnt range");
+    static_assert(!SP || STAGES == 3, "the spread schedule refills the stage of tile t - 1 with tile t + 2");
     // EPI_SILU_MUL: the W rows of a tile alternate 32 gate rows and the 32 up
     // rows of the same output columns, so block pair (2i, 2i + 1) of a wave
     // holds gate and up values of one 32-column group in the same lanes.
@@ -135,6 +147,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         }
     };
 
+    // Copy instruction j of tile t into `stage` alone (the spread schedule).
+    auto issue_one = [&](int t, int stage, int j) {
+        const int64_t k0 = int64_t(t) * kBK;
+        const uint32_t dst = ring_lds + uint32_t(stage * STAGE_CHUNKS + 64 * wave * IPW) * 16u + 1024u * j;
+        dma16(k0 + koff[j] < k ? static_cast<const void*>(src[j] + k0) : zero, dst);
+    };
+
     f32x16_t acc[NI][MJ];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
@@ -187,28 +206,99 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         if (u + AHEAD < ktiles) issue(u + AHEAD, free_stage);
     };
 
+    if constexpr (SP) {
+        // Tile t's K-steps 0, 1 and 2 each carry D0, D1, D2 of the wave's IPW
+        // copy instructions for tile t + 2, which go to the stage tile t - 1
+        // used (free since the barrier that opened tile t).  All IPW are out
+        // before the wait for tile t + 1, so that wait is vmcnt <= IPW, and
+        // tile t + 2 has the rest of tile t and all of tile t + 1 to land.
+        constexpr int D0 = (IPW + 2) / 3, D1 = (IPW - D0 + 1) / 2, D2 = IPW - D0 - D1;
+        constexpr int STEP = NI * MJ;   // MFMAs per K-step
+        // The MFMAs of one K-step with copies J0 .. J0 + CNT - 1 of tile tt
+        // evenly between them; the scheduling barriers pin each copy to its
+        // slot in the MFMA sequence.
+        auto mfmas_copy = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI], int tt, int stage, auto j0_c,
+                              auto cnt_c) {
+            constexpr int J0 = decltype(j0_c)::value, CNT = decltype(cnt_c)::value;
 #pragma unroll
-    for (int t = 0; t < AHEAD; ++t)
-        if (t < ktiles) issue(t, t);
-    tile_ready(0, STAGES - 1);
-    read_frags(ring, 0, af0, wf0);
+            for (int x = 0; x < STEP; ++x) {
+                acc[x / MJ][x % MJ] = mfma_32x32x16<DT>(wf[x / MJ], af[x % MJ], acc[x / MJ][x % MJ]);
+                const int from = x * CNT / STEP, to = (x + 1) * CNT / STEP;
+                if (to > from) {
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int j = from; j < to; ++j) issue_one(tt, stage, J0 + j);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+        using C0 = std::integral_constant<int, 0>;
+        using CD0 = std::integral_constant<int, D0>;
+        using CD1 = std::integral_constant<int, D1>;
+        using CD2 = std::integral_constant<int, D2>;
+        using CD01 = std::integral_constant<int, D0 + D1>;
+        if (ktiles > 0) issue(0, 0);
+        if (ktiles > 1) issue(1, 1);
+        if (ktiles > 1) wait_vmcnt<IPW>();
+        else wait_vmcnt<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        read_frags(ring, 0, af0, wf0);
+        int cur = 0;   // ring stage of tile t
+        // COPY: whether tile t + 2 exists (false for the last two tiles).
+        auto k_tile = [&](int t, auto copy_c) {
+            constexpr bool COPY = decltype(copy_c)::value;
+            const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
+            const int refill = cur == 0 ? STAGES - 1 : cur - 1;
+            read_frags(tile, 1, af1, wf1);
+            if constexpr (COPY) mfmas_copy(af0, wf0, t + 2, refill, C0{}, CD0{});
+            else mfmas(af0, wf0);
+            read_frags(tile, 2, af0, wf0);
+            if constexpr (COPY) mfmas_copy(af1, wf1, t + 2, refill, CD0{}, CD1{});
+            else mfmas(af1, wf1);
+            read_frags(tile, 3, af1, wf1);
+            if constexpr (COPY) mfmas_copy(af0, wf0, t + 2, refill, CD01{}, CD2{});
+            else mfmas(af0, wf0);
+            const int next = cur + 1 == STAGES ? 0 : cur + 1;
+            if (t + 1 < ktiles) {
+                if constexpr (COPY) wait_vmcnt<IPW>();
+                else wait_vmcnt<0>();
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                read_frags(ring + next * STAGE_CHUNKS, 0, af0, wf0);
+            }
+            cur = next;
+            mfmas(af1, wf1);
+        };
+        int t = 0;
+        for (; t + 2 < ktiles; ++t) k_tile(t, std::true_type{});
+        for (; t < ktiles; ++t) k_tile(t, std::false_type{});
+    } else {
+#pragma unroll
+        for (int t = 0; t < AHEAD; ++t)
+            if (t < ktiles) issue(t, t);
+        tile_ready(0, STAGES - 1);
+        read_frags(ring, 0, af0, wf0);
 
-    int cur = 0;   // ring stage of tile t
-    for (int t = 0; t < ktiles; ++t) {
-        const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
-        read_frags(tile, 1, af1, wf1);
-        mfmas(af0, wf0);
-        read_frags(tile, 2, af0, wf0);
-        mfmas(af1, wf1);
-        read_frags(tile, 3, af1, wf1);
-        mfmas(af0, wf0);
-        const int next = cur + 1 == STAGES ? 0 : cur + 1;
-        if (t + 1 < ktiles) {
-            tile_ready(t + 1, cur);
-            read_frags(ring + next * STAGE_CHUNKS, 0, af0, wf0);
+        int cur = 0;   // ring stage of tile t
+        for (int t = 0; t < ktiles; ++t) {
+            const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
+            read_frags(tile, 1, af1, wf1);
+            mfmas(af0, wf0);
+            read_frags(tile, 2, af0, wf0);
+            mfmas(af1, wf1);
+            read_frags(tile, 3, af1, wf1);
+            mfmas(af0, wf0);
+            const int next = cur + 1 == STAGES ? 0 : cur + 1;
+            if (t + 1 < ktiles) {
+                tile_ready(t + 1, cur);
+                read_frags(ring + next * STAGE_CHUNKS, 0, af0, wf0);
+            }
+            cur = next;
+            mfmas(af1, wf1);
         }
-        cur = next;
-        mfmas(af1, wf1);
     }
 
     // Epilogue through LDS.  acc[i][j][v] is D[n][m] with n = 8 (v/4) +
@@ -323,22 +413,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     }
 }
 
-// Ring depth for a problem.  Measured on MI355X with 128 x 128 tiles and
-// 4 waves: when the grid has more tiles than CUs, a 2-deep ring (64 KiB)
-// lets two workgroups share a CU and run out of phase, so one's MFMAs
-// overlap the other's loads (bf16 2048 x 4096 x 1024, 512 tiles: 19-20 us,
-// against 24 us with a 3-deep ring at one workgroup per CU).  With at most
-// one tile per CU there is nothing to pair with, and a 3-deep ring (96 KiB)
-// keeps two K-tiles in flight instead (4096 x 1024 x 3584, 256 tiles:
-// 34 us, against 39 us with the 2-deep ring).
 constexpr int64_t kCus = 256;
 
-int choose_stages(int64_t m, int64_t n) {
-    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    return tiles <= kCus ? 3 : 2;
-}
-
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS>
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP>
 int launch_tile(const Problem& p, hipStream_t s) {
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;
     const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BNO - 1) / BNO;
@@ -349,20 +426,31 @@ int launch_tile(const Problem& p, hipStream_t s) {
     // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
     const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && ((p.ldc * out_bytes) % 16 == 0);
     if (EPI == EPI_ARGMAX) *p.key_blocks = tiles_n;
-    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI, RS>), grid, block, 0, s,
+    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI, RS, SP>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c,
                        p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec, p.keys,
                        p.row_scale);
     return check_launch("mfma_staged");
 }
 
-// Grids of at most this many 128 x 128 tiles (half the CUs) take smaller
-// tiles: four times the workgroups fill the chip.  Measured on MI355X (bf16,
-// 128 x 128 against 64 x 64 tiles): 1024^3 11.7 -> 6.8 us, 512 x 4096 x 1024
-// 12.3 -> 8.1 us, 2048 x 1024 x 2048 20.6 -> 13.8 us, 512 x 1024 x 3584
-// 33.0 -> 17.0 us; from 512 tiles up 128 x 128 stays ahead (4096 x 2048 x
-// 1024: 20.2 against 27.7 us).  Every tile shape sums K in the same order,
-// so the choice does not change any result bit.
+// Tile and schedule by grid size, in 128 x 128 tiles (bf16, MI355X, one
+// launch; every choice sums K in the same order, so none changes a result
+// bit):
+//   * at most 128 (half the CUs): 64 x 64 tiles, four times the workgroups
+//     (1024^3 11.7 -> 6.8 us, 512 x 4096 x 1024 12.3 -> 8.1 us,
+//     2048 x 1024 x 2048 20.6 -> 13.8 us, 512 x 1024 x 3584 33.0 -> 17.0 us),
+//     with a 3-deep ring from K = 2048 (2048 x 1024 x 2048: 13.8 us against
+//     14.1; 512 x 1024 x 3584: 17.0 against 27.3);
+//   * enough 128 x 256 tiles for every CU: one 8-wave workgroup per CU on
+//     128 x 256 (half the A reads of two 128 x 128 tiles), 3-deep ring,
+//     spread copies (2048 x 4096 x 1024: 20.3 -> 18.9 us; 2048 x 37984 x
+//     1024: 172 -> 162 us);
+//   * otherwise at most one tile per CU: 128 x 128, 3-deep ring, spread
+//     copies (4096 x 1024 x 3584, 256 tiles: 40.0 -> 31.1 us against the
+//     burst schedule, which measured 34-39 us with 3 or 2 stages);
+//   * otherwise (257 .. 511 tiles, and the greedy LM head, whose epilogue
+//     is written for 4 waves): 128 x 128 with a 2-deep ring (64 KiB), so two
+//     workgroups share a CU and one's MFMAs overlap the other's copies.
 constexpr int64_t kSmallGridTiles = kCus / 2;
 
 template <int DT, int DT_OUT, int EPI, int RS = 0>
@@ -371,20 +459,22 @@ int launch_epi(const Problem& p, hipStream_t s) {
     const int64_t n_tiles = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
     const int64_t tiles = ((p.m + 127) / 128) * ((n_tiles + 127) / 128);
     if (tiles <= kSmallGridTiles) {
-        // A deeper ring pays off over longer K (2048 x 1024 x 2048: 13.8 us
-        // with 3 stages, 14.1 with 2; 512 x 1024 x 3584: 17.0 against 27.3).
         const bool deep = p.k >= 2048;
         if constexpr (EPI == EPI_NONE) {
-            if (deep) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI, RS>(p, s);
-            return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 2, EPI, RS>(p, s);
+            if (deep) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI, RS, 0>(p, s);
+            return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 2, EPI, RS, 0>(p, s);
         } else if constexpr (EPI == EPI_SILU_MUL) {
             // gate/up pairs need two 32-row W blocks per wave
-            if (deep) return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS>(p, s);
-            return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 2, EPI, RS>(p, s);
+            if (deep) return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS, 0>(p, s);
+            return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 2, EPI, RS, 0>(p, s);
         }
     }
-    if (choose_stages(p.m, n_tiles) == 3) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI, RS>(p, s);
-    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS>(p, s);
+    if constexpr (EPI != EPI_ARGMAX) {
+        const int64_t wide_tiles = ((p.m + 127) / 128) * ((n_tiles + 255) / 256);
+        if (wide_tiles >= kCus) return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI, RS, 1>(p, s);
+    }
+    if (tiles <= kCus) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI, RS, 1>(p, s);
+    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS, 0>(p, s);
 }
 
 template <int DT, int DT_OUT>

@@ -250,6 +250,24 @@ def test_add_rmsnorm_prologue_kernel_path(m, silu):
         _check_add_norm(out, res_out, h, r, nw, w, 1e-5, torch.bfloat16, torch.bfloat16)
 
 
+@pytest.mark.parametrize("m,n,silu", [(1500, 2000, False), (2100, 4100, False), (2100, 2050, True)],
+                         ids=["128x128-spread", "128x256", "128x256-silu"])
+def test_add_rmsnorm_row_scale_large_grids(m, n, silu):
+    """The row-scaled epilogue on mfma_staged's large-grid tiles: 192 tiles
+    of 128 x 128 (3-deep ring, spread copies) and at least 256 tiles of
+    128 x 256 (8 waves), plain and with SiLU-and-mul; ragged M, N and K."""
+    gen = torch.Generator().manual_seed(m + n)
+    k = 1000
+    h, r, nw, w = _norm_inputs(m, 2 * n if silu else n, k, torch.bfloat16, gen)
+    _say(f"add_rmsnorm large grid M={m} N={n} silu={silu}")
+    out, res_out = K.gemm_add_rmsnorm(h.to(DEV), r.to(DEV), nw.to(DEV), w.to(DEV), 1e-5, silu_mul=silu)
+    torch.cuda.synchronize()
+    if silu:
+        _check_add_norm_silu(out, res_out, h, r, nw, w, 1e-5, torch.bfloat16, torch.bfloat16)
+    else:
+        _check_add_norm(out, res_out, h, r, nw, w, 1e-5, torch.bfloat16, torch.bfloat16)
+
+
 def test_add_rmsnorm_close_to_reference_composition():
     """The reassociated row scale stays close to Qwen3_5RMSNorm + F.linear
     computed by torch on the GPU, which rounds the normalized activations
