@@ -13,9 +13,9 @@ Alongside (extra keys of the same JSON line): the decode GEMMs M in
 256 MB Infinity Cache, the FP32 1024^3 GEMM, the FP16 down projection, the
 BF16 LM head, the merged gated-delta-net input projection (one N = 8224 GEMM
 against four launches), the fused epilogues and prologues against the
-reference's compositions (gate_up + SiLU-and-mul, the greedy LM head, the
-gated-attention output gate before o_proj, the residual add + RMSNorm before
-a projection), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
+reference's compositions (gate_up + SiLU-and-mul, the greedy and the sampled
+LM head, the gated-attention output gate before o_proj, the residual add +
+RMSNorm before a projection), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
 for comparison only, and the CPU baseline (host F.linear, multi-threaded).
 
 Prints ONE JSON line on stdout; a readable table goes to stderr.
@@ -146,6 +146,7 @@ def main() -> int:
     L = pkg._lib
     L.load()                      # raises if the HIP library is not built
     W = pkg.workloads
+    K_ops = pkg.kernels
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     code = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16}
@@ -364,7 +365,7 @@ def main() -> int:
 
         # ----------------------------- greedy LM head (argmax, no logits)
         # Against the reference's path: fp32 logits [M, 151936] from the GEMM,
-        # then float_logits.argmax(dim=-1) (sampler.py:19-32) on the GPU.
+        # then float_logits.argmax(dim=-1) (sampler.py:8-21) on the GPU.
         lw = W.WORKLOADS["bf16_lm_head_n151936_k1024"]
         _, l_w0 = W.make_inputs("bf16_lm_head_n151936_k1024", 1, device=dev)
         l_ws = [l_w0, l_w0.clone()]
@@ -398,6 +399,44 @@ def main() -> int:
                            "speedup": round(t_l / t_g, 3)})
             log(f"lm head greedy M={lm}: fused {t_g * 1e3:.1f} us, fp32 logits + torch argmax {t_l * 1e3:.1f} us")
         extras["lm_head_greedy_bf16_n151936_k1024"] = l_rows
+
+        # ----------------------------- sampled LM head (Sampler, no logits)
+        # Every row sampled at temperature 0.8, against the reference's path:
+        # fp32 logits from the GEMM, then Sampler.forward (sampler.py:8-21:
+        # softmax, exponential draws, divide, argmax; eager here, the
+        # reference wraps it in torch.compile).
+        p_rows = []
+        for lm in (1, 32):
+            l_a, _ = W.make_inputs("bf16_lm_head_n151936_k1024", lm, device=dev)
+            p_tok = torch.empty(lm, dtype=torch.int64, device=dev)
+            p_val = torch.empty(lm, dtype=torch.float32, device=dev)
+            p_temp = torch.full((lm,), 0.8, dtype=torch.float32, device=dev)
+            p_need = L.argmax_workspace_bytes(lm, lw.n, lw.k, lw.k, lw.k, L.BF16)
+            p_ws_buf = torch.empty(p_need, dtype=torch.uint8, device=dev)
+            p_logits = torch.empty(lm, lw.n, dtype=torch.float32, device=dev)
+
+            def sampled(wt, step, l_a=l_a, p_tok=p_tok, p_val=p_val, p_temp=p_temp, p_ws_buf=p_ws_buf, lm=lm,
+                        p_need=p_need):
+                def f():
+                    L.sample_raw(l_a.data_ptr(), wt.data_ptr(), p_temp.data_ptr(), 1234, step, p_tok.data_ptr(),
+                                 p_val.data_ptr(), lm, lw.n, lw.k, lw.k, lw.k, L.BF16, p_ws_buf.data_ptr(), p_need,
+                                 torch.cuda.current_stream().cuda_stream)
+                return f
+
+            def logits_then_sampler(wt, l_a=l_a, p_logits=p_logits, p_temp=p_temp, lm=lm):
+                gemm = launcher(l_a, wt, p_logits, lm, lw.n, lw.k, L.B_NK, torch.bfloat16, torch.float32)
+
+                def f():
+                    gemm()
+                    K_ops.torch_sampler(p_logits, p_temp)
+                return f
+            t_s = median_graph_ms(torch, [sampled(l_ws[i % 2], i) for i in range(20)], trials=3)
+            t_r = median_graph_ms(torch, [logits_then_sampler(l_ws[i % 2]) for i in range(20)], trials=3)
+            p_rows.append({"m": lm, "sampled_us": round(t_s * 1e3, 3),
+                           "logits_then_sampler_us": round(t_r * 1e3, 3), "speedup": round(t_r / t_s, 3)})
+            log(f"lm head sampled (T=0.8) M={lm}: fused {t_s * 1e3:.1f} us, "
+                f"fp32 logits + eager torch Sampler {t_r * 1e3:.1f} us")
+        extras["lm_head_sampled_bf16_n151936_k1024"] = p_rows
         del l_ws, l_w0
 
         # ------------------- gated-attention output gate fused before o_proj

@@ -186,7 +186,7 @@ int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k,
  * be NULL) receives the fp32 logit of the token.  Replaces the [m, n] fp32
  * logits of ParallelLMHead (nanovllm/layers/embed_head.py:61) followed by
  * the greedy branch of Sampler, float_logits.argmax(dim=-1)
- * (nanovllm/layers/sampler.py:19-32).  `workspace` (8-byte aligned, device
+ * (nanovllm/layers/sampler.py:8-21).  `workspace` (8-byte aligned, device
  * memory, contents scratch) must hold
  * nanovllm_gemm_argmax_workspace_bytes() bytes; one call launches the GEMM
  * pass and a small reduction pass on `stream`.  Inputs f16 or bf16 on the
@@ -219,6 +219,44 @@ int nanovllm_gemm_argmax_with_kernel(int kernel_id,
 int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k,
                                 int64_t lda, int64_t ldw, int dtype_in,
                                 int aligned16);
+
+/*
+ * Sampled LM head: Sampler.forward (nanovllm/layers/sampler.py:8-21) on the
+ * logits a w^T without writing them.  Row i with temperatures[i] <= 1e-10
+ * takes the greedy token, exactly as nanovllm_gemm_argmax; every other row
+ * takes
+ *
+ *     tokens[i] = argmax_j (l[i,j] / temperatures[i] - ln E[i,j]),
+ *
+ * l the fp32 logits, which is the reference's argmax_j of
+ * softmax(l / T)_j / E_j (the Gumbel-max form of a draw from softmax(l / T)).
+ * E[i,j] = max(-ln u, 1e-10) with u = ((x >> 8) + 1) / 2^24 and x word
+ * j % 4 of Philox4x32-10(counter = {j / 4, i, offset, offset >> 32},
+ * key = {seed, seed >> 32}), so a (seed, offset) pair fixes every draw;
+ * callers advance `offset` between steps (the reference draws fresh
+ * exponentials from torch's generator on every call).  A call captured in a
+ * HIP graph replays its own seed and offset.  scores[i] (optional) receives
+ * the winning score (the logit on greedy rows).  temperatures: m floats in
+ * device memory.  Workspace as nanovllm_gemm_argmax (same size function).
+ */
+int nanovllm_gemm_sample(const void* a, const void* w,
+                         const float* temperatures, uint64_t seed, uint64_t offset,
+                         int64_t* tokens, float* scores,
+                         int64_t m, int64_t n, int64_t k,
+                         int64_t lda, int64_t ldw, int dtype_in,
+                         void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/* The sampled head forced onto one kernel (splitk_decode for m <= 32 or
+ * mfma_staged), for parity tests of both (gemm_bench.cu:396-416 pattern). */
+int nanovllm_gemm_sample_with_kernel(int kernel_id,
+                                     const void* a, const void* w,
+                                     const float* temperatures, uint64_t seed, uint64_t offset,
+                                     int64_t* tokens, float* scores,
+                                     int64_t m, int64_t n, int64_t k,
+                                     int64_t lda, int64_t ldw, int dtype_in,
+                                     void* workspace, int64_t workspace_bytes,
+                                     void* stream);
 
 /* Gated-attention output projection: the output gate of Qwen3.5 gated
  * attention applied to A in front of o_proj,

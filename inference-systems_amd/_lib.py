@@ -35,6 +35,7 @@ _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _VP = ctypes.c_void_p
 _F32 = ctypes.c_float
+_U64 = ctypes.c_uint64
 SIGNATURES = {
     "nanovllm_gemm": (_INT, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _VP]),
     "nanovllm_gemm_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT,
@@ -50,6 +51,10 @@ SIGNATURES = {
     "nanovllm_gemm_argmax_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP,
                                                 _I64, _VP]),
     "nanovllm_gemm_argmax_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _INT, _INT]),
+    "nanovllm_gemm_sample": (_INT, [_VP, _VP, _VP, _U64, _U64, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP,
+                                    _I64, _VP]),
+    "nanovllm_gemm_sample_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _U64, _U64, _VP, _VP, _I64, _I64, _I64, _I64,
+                                                _I64, _INT, _VP, _I64, _VP]),
     "nanovllm_gemm_gated": (_INT, [_VP, _VP, _VP, _VP] + [_I64] * 9 + [_INT, _INT, _VP, _I64, _VP]),
     "nanovllm_gemm_gated_workspace_bytes": (_I64, [_I64, _I64, _I64, _INT]),
     "nanovllm_gemm_gated_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP] + [_I64] * 9 + [_INT, _INT, _VP, _I64, _VP]),
@@ -172,6 +177,21 @@ def argmax_raw(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in
         rc = lib.nanovllm_gemm_argmax_with_kernel(kernel, a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw,
                                                   dtype_in, ws_ptr, ws_bytes, stream)
     check(rc, "nanovllm_gemm_argmax")
+
+
+def sample_raw(a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr, m, n, k, lda, ldw, dtype_in, ws_ptr,
+               ws_bytes, stream, kernel: int | None = None) -> None:
+    """Enqueue the sampled LM head (GEMM pass + reduction) on `stream`; raise on error."""
+    lib = load()
+    seed &= (1 << 64) - 1
+    offset &= (1 << 64) - 1
+    if kernel is None:
+        rc = lib.nanovllm_gemm_sample(a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr, m, n, k, lda, ldw,
+                                      dtype_in, ws_ptr, ws_bytes, stream)
+    else:
+        rc = lib.nanovllm_gemm_sample_with_kernel(kernel, a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr,
+                                                  m, n, k, lda, ldw, dtype_in, ws_ptr, ws_bytes, stream)
+    check(rc, "nanovllm_gemm_sample")
 
 
 def gemm_raw(a_ptr, b_ptr, c_ptr, m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out, stream,

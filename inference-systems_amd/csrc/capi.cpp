@@ -244,15 +244,21 @@ int64_t argmax_workspace_bytes(int64_t m, int64_t n) {
     return ((n + cols_per_block - 1) / cols_per_block) * m * int64_t(sizeof(uint64_t));
 }
 
+// `sample`: nullptr for the greedy head; the sampled head passes its
+// per-row temperatures (device memory, required) and noise seed / offset.
 int argmax_entry(int forced_kernel, const void* a, const void* w, int64_t* tokens, float* logits, int64_t m,
                  int64_t n, int64_t k, int64_t lda, int64_t ldw, int din, void* workspace, int64_t workspace_bytes,
-                 void* stream) {
+                 void* stream, const SampleArgs* sample = nullptr) {
     g_last_error.clear();
     int rc = validate_argmax(m, n, k, lda, ldw, din);
     if (rc != NANOVLLM_GEMM_OK) return rc;
     if (m == 0) return NANOVLLM_GEMM_OK;
     if (a == nullptr || w == nullptr || tokens == nullptr || workspace == nullptr)
         return set_error(NANOVLLM_GEMM_EINVAL, "a, w, tokens and workspace must be non-null device pointers");
+    if (sample != nullptr && sample->temperature == nullptr)
+        return set_error(NANOVLLM_GEMM_EINVAL, "temperatures must be a non-null device pointer to m floats");
+    if (sample != nullptr && reinterpret_cast<uintptr_t>(sample->temperature) % 4 != 0)
+        return set_error(NANOVLLM_GEMM_EINVAL, "temperatures must be 4-byte aligned");
     if (reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
         return set_error(NANOVLLM_GEMM_EINVAL, "workspace must be 8-byte aligned");
     const int64_t need = argmax_workspace_bytes(m, n);
@@ -273,6 +279,7 @@ int argmax_entry(int forced_kernel, const void* a, const void* w, int64_t* token
     p.epi = EPI_ARGMAX;
     p.keys = static_cast<uint64_t*>(workspace);
     p.key_blocks = &blocks;
+    if (sample != nullptr) p.sample = *sample;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     rc = run(kernel, p, s);
     if (rc != NANOVLLM_GEMM_OK) return rc;
@@ -576,6 +583,27 @@ int nanovllm_gemm_argmax_with_kernel(int kernel_id, const void* a, const void* w
                              workspace_bytes, stream);
 }
 
+int nanovllm_gemm_sample(const void* a, const void* w, const float* temperatures, uint64_t seed, uint64_t offset,
+                         int64_t* tokens, float* scores, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
+                         int dtype_in, void* workspace, int64_t workspace_bytes, void* stream) {
+    const nvg::SampleArgs sa{temperatures, seed, offset};
+    return nvg::argmax_entry(-1, a, w, tokens, scores, m, n, k, lda, ldw, dtype_in, workspace, workspace_bytes,
+                             stream, &sa);
+}
+
+int nanovllm_gemm_sample_with_kernel(int kernel_id, const void* a, const void* w, const float* temperatures,
+                                     uint64_t seed, uint64_t offset, int64_t* tokens, float* scores, int64_t m,
+                                     int64_t n, int64_t k, int64_t lda, int64_t ldw, int dtype_in, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
+        nvg::g_last_error.clear();
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
+    }
+    const nvg::SampleArgs sa{temperatures, seed, offset};
+    return nvg::argmax_entry(kernel_id, a, w, tokens, scores, m, n, k, lda, ldw, dtype_in, workspace,
+                             workspace_bytes, stream, &sa);
+}
+
 int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int dtype_in,
                                 int aligned16) {
     nvg::g_last_error.clear();
@@ -666,6 +694,6 @@ int nanovllm_gemm_add_rmsnorm_with_kernel(int kernel_id, const void* h, const vo
 
 const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
 
-int nanovllm_gemm_version(void) { return (1 << 16) | 3; }
+int nanovllm_gemm_version(void) { return (1 << 16) | 4; }
 
 }  // extern "C"

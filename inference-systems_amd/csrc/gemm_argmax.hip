@@ -2,7 +2,7 @@
 // left one key per row of A (argmax_key of its best column); this kernel
 // takes the maximum key of each row over all workgroups and decodes it into
 // the token id and its logit.  It stands in for Sampler's greedy branch,
-// float_logits.argmax(dim=-1) (nanovllm/layers/sampler.py:19-32), which
+// float_logits.argmax(dim=-1) (nanovllm/layers/sampler.py:8-21), which
 // reads back the [M, vocab] fp32 logits the GEMM wrote.
 #include "gemm_common.hpp"
 

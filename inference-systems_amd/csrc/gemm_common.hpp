@@ -40,6 +40,13 @@ constexpr int PRO_NONE = 0;
 constexpr int PRO_GATE = 1;
 constexpr int PRO_ADD_NORM = 2;
 
+// Per-row temperatures and noise of the sampled LM head (see sample_score).
+struct SampleArgs {
+    const float* temperature = nullptr;   // [M]; nullptr: every row greedy
+    uint64_t seed = 0;
+    uint64_t offset = 0;
+};
+
 // One GEMM problem as it crosses the C ABI (see include/nanovllm_gemm.h).
 struct Problem {
     const void* a;
@@ -53,6 +60,7 @@ struct Problem {
     int epi = EPI_NONE;   // EPI_SILU_MUL: n output columns from 2n rows of b
     uint64_t* keys = nullptr;         // EPI_ARGMAX: [m, workgroups along N] partial keys
     int64_t* key_blocks = nullptr;    // EPI_ARGMAX: set by the launcher to its workgroups along N
+    SampleArgs sample;                // EPI_ARGMAX: per-row temperatures and noise (sampled LM head)
     const float* row_scale = nullptr; // mfma_staged, EPI_NONE / EPI_SILU_MUL: output row i (both
                                       // sums of a SiLU pair) times row_scale[i] before rounding
     int pro = PRO_NONE;
@@ -268,6 +276,69 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int64_t col) {
     const uint32_t b = v != v ? 0x7FC00000u : (v == 0.0f ? 0u : __builtin_bit_cast(uint32_t, v));
     const uint32_t ordered = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return (uint64_t(ordered) << 32) | uint64_t(0xFFFFFFFFu - uint32_t(col));
+}
+
+// Sampled LM head (EPI_ARGMAX with a temperature per row).  Sampler
+// (nanovllm/layers/sampler.py:8-21) keeps row i greedy when its temperature
+// is <= 1e-10 and otherwise takes argmax_j softmax(v / T)_j / E_j with E_j
+// ~ Exp(1) clamped to >= 1e-10.  That is argmax_j (v_j / T - ln E_j), the
+// Gumbel-max form, which needs no row-wide softmax: each workgroup ranks its
+// own columns by this score and the greedy finalize picks the best key.
+// E comes from a counter-based generator so any workgroup can draw the
+// noise of any (row, column): u = (24 high bits of word col % 4 of
+// Philox4x32-10(counter = (col / 4, row, offset, offset >> 32), key = seed))
+// + 1) / 2^24, in (0, 1]; E = max(-ln u, 1e-10).
+//
+// Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers:
+// as easy as 1, 2, 3", SC 2011): ten rounds, each two 32 x 32 -> 64-bit
+// products of counter words with the round multipliers, the high halves
+// mixed with the other two words and the round key, and the key advanced
+// by the Weyl constants between rounds.
+__device__ __forceinline__ u32x4_t philox4x32_10(u32x4_t c, uint32_t k0, uint32_t k1) {
+    constexpr uint32_t kMul0 = 0xD2511F53u, kMul1 = 0xCD9E8D57u;
+    constexpr uint32_t kWeyl0 = 0x9E3779B9u, kWeyl1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = uint64_t(kMul0) * c[0];
+        const uint64_t p1 = uint64_t(kMul1) * c[2];
+        c = u32x4_t{uint32_t(p1 >> 32) ^ c[1] ^ k0, uint32_t(p1), uint32_t(p0 >> 32) ^ c[3] ^ k1, uint32_t(p0)};
+        k0 += kWeyl0;
+        k1 += kWeyl1;
+    }
+    return c;
+}
+
+// Temperature of a sampled row, 0 for a greedy one (temperature <= 1e-10)
+// or when the head is greedy altogether.
+__device__ __forceinline__ float sample_temperature(int64_t row, const SampleArgs& sa) {
+    if (sa.temperature == nullptr) return 0.0f;
+    const float t = sa.temperature[row];
+    return t <= 1e-10f ? 0.0f : t;
+}
+
+// The four noise words of columns 4 q .. 4 q + 3 of a row.
+__device__ __forceinline__ u32x4_t sample_words(int64_t row, int64_t q, const SampleArgs& sa) {
+    return philox4x32_10(u32x4_t{uint32_t(q), uint32_t(row), uint32_t(sa.offset), uint32_t(sa.offset >> 32)},
+                         uint32_t(sa.seed), uint32_t(sa.seed >> 32));
+}
+
+// Score of a sampled column from its logit, the row's temperature and its
+// noise word: v / T - ln E (ln from the hardware log2).
+__device__ __forceinline__ float gumbel_score(float v, float t, uint32_t word) {
+    constexpr float kLn2 = 0.693147180559945309f;
+    const float u = float((word >> 8) + 1u) * 0x1p-24f;
+    const float e = fmaxf(-__builtin_amdgcn_logf(u) * kLn2, 1e-10f);
+    return v / t - __builtin_amdgcn_logf(e) * kLn2;
+}
+
+// The score that ranks column col of row row: the logit itself on a greedy
+// row, v / T - ln E on a sampled one.
+__device__ __forceinline__ float sample_score(float v, int64_t row, int64_t col, const SampleArgs& sa) {
+    const float t = sample_temperature(row, sa);
+    if (t == 0.0f) return v;
+    const u32x4_t x = sample_words(row, col >> 2, sa);
+    const int j = int(col & 3);
+    return gumbel_score(v, t, j == 0 ? x[0] : j == 1 ? x[1] : j == 2 ? x[2] : x[3]);
 }
 
 // Integer minimum.  The device `min` overload set has no exact match for

@@ -55,7 +55,7 @@ template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, 
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
-    ProArgs pro) {
+    ProArgs pro, SampleArgs sa) {
     static_assert(AROWS == 8 || AROWS == 16 || AROWS == 32, "rows of A per line");
     constexpr int MG = AROWS == 32 ? 2 : 1;   // 16-row groups of A in the MFMA
     constexpr int IW = 2 * RG;                 // W copies per line (8 rows each)
@@ -287,10 +287,28 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
         static_assert(TPR >= 1 && TPR <= 64 && (TPR & (TPR - 1)) == 0, "a row's threads share a wave");
         const int row = threadIdx.x / TPR, sub = threadIdx.x % TPR;
         uint64_t best = 0;
-        for (int cc = sub; cc < 16 * RG; cc += TPR) {
-            if (n0 + cc >= n) break;
-            const uint64_t key = argmax_key(total(cc >> 4, row >> 4, cc & 15, row & 15), n0 + cc);
-            best = key > best ? key : best;
+        const float t = row < m ? sample_temperature(row, sa) : 0.0f;
+        if (row < m && t == 0.0f) {
+            for (int cc = sub; cc < 16 * RG; cc += TPR) {
+                if (n0 + cc >= n) break;
+                const uint64_t key = argmax_key(total(cc >> 4, row >> 4, cc & 15, row & 15), n0 + cc);
+                best = key > best ? key : best;
+            }
+        } else if (row < m) {
+            // A sampled row: groups of 4 adjacent columns, so one noise draw
+            // serves 4 scores (n0 is a multiple of 16).
+            for (int c4 = 4 * sub; c4 < 16 * RG; c4 += 4 * TPR) {
+                if (n0 + c4 >= n) break;
+                const u32x4_t x = sample_words(row, (n0 + c4) >> 2, sa);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int cc = c4 + j;
+                    if (n0 + cc >= n) break;
+                    const float v = gumbel_score(total(cc >> 4, row >> 4, cc & 15, row & 15), t, x[j]);
+                    const uint64_t key = argmax_key(v, n0 + cc);
+                    best = key > best ? key : best;
+                }
+            }
         }
 #pragma unroll
         for (int off = TPR / 2; off >= 1; off >>= 1) {
@@ -344,7 +362,8 @@ constexpr int kRegWaves = 4, kRegUnroll = 8, kRegStep = 32;
 template <int DT, int DT_OUT, int EPI>
 __global__ __launch_bounds__(kRegWaves * 64) void splitk_regs_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
-    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys) {
+    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
+    SampleArgs sa) {
     static_assert(EPI != EPI_SILU_MUL, "gate/up pairs need the LDS-staged kernel");
     __shared__ float red[kRegWaves][16][16];
     const int lane = threadIdx.x & 63;
@@ -381,7 +400,7 @@ __global__ __launch_bounds__(kRegWaves * 64) void splitk_regs_kernel(
     if constexpr (EPI == EPI_ARGMAX) {
         // Per row of A, the best of the workgroup's 16 columns: a 16-lane
         // max over the keys of one row (lanes 16 mm .. 16 mm + 15).
-        uint64_t best = n0 + nn < n ? argmax_key(sum, n0 + nn) : 0;
+        uint64_t best = n0 + nn < n && mm < m ? argmax_key(sample_score(sum, mm, n0 + nn, sa), n0 + nn) : 0;
 #pragma unroll
         for (int off = 8; off >= 1; off >>= 1) {
             const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), off))) << 32) |
@@ -402,7 +421,7 @@ int launch_regs(const Problem& p, hipStream_t s) {
     if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
     hipLaunchKernelGGL((splitk_regs_kernel<DT, DT_OUT, EPI>), dim3(static_cast<uint32_t>(blocks)),
                        dim3(kRegWaves * 64), 0, s, static_cast<const uint16_t*>(p.a),
-                       static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k, p.lda, p.ldb, p.ldc, p.keys);
+                       static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k, p.lda, p.ldb, p.ldc, p.keys, p.sample);
     return check_launch("splitk_decode");
 }
 
@@ -418,7 +437,7 @@ int launch_cfg(const Problem& p, hipStream_t s) {
                       static_cast<const uint16_t*>(p.norm_w), p.eps, static_cast<uint16_t*>(p.res_out), p.ldres};
     hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI, PRO>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
-                       p.lda, p.ldb, p.ldc, p.keys, pro);
+                       p.lda, p.ldb, p.ldc, p.keys, pro, p.sample);
     return check_launch("splitk_decode");
 }
 

@@ -56,7 +56,8 @@ template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int 
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n, int c_vec, uint64_t* __restrict__ keys, const float* __restrict__ row_scale) {
+    int tiles_m, int tiles_n, int c_vec, uint64_t* __restrict__ keys, const float* __restrict__ row_scale,
+    SampleArgs sa) {
     constexpr int NW = WGM * WGN;        // waves, in a WGM x WGN grid
     constexpr int NT = NW * 64;          // threads
     constexpr int WM = BM / WGM;         // wave tile rows (M)
@@ -366,11 +367,22 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         const int r = tid >> 1, h = tid & 1;
         const float* rowp = reinterpret_cast<const float*>(ctile + r * PITCH);
         uint64_t best = 0;
-        for (int cc = 0; cc < BN / 2; ++cc) {
-            const int col = h * (BN / 2) + cc;
-            if (n0 + col >= n) break;
-            const uint64_t key = argmax_key(rowp[col], n0 + col);
-            best = key > best ? key : best;
+        if (m0 + r < m) {
+            // Groups of 4 adjacent columns: one noise draw serves 4 scores on
+            // a sampled row (n0 is a multiple of BN).
+            const float t = sample_temperature(m0 + r, sa);
+            for (int c4 = 0; c4 < BN / 2; c4 += 4) {
+                const int col0 = h * (BN / 2) + c4;
+                if (n0 + col0 >= n) break;
+                const u32x4_t x = t != 0.0f ? sample_words(m0 + r, (n0 + col0) >> 2, sa) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = col0 + j;
+                    if (n0 + col >= n) break;
+                    const uint64_t key = argmax_key(t != 0.0f ? gumbel_score(rowp[col], t, x[j]) : rowp[col], n0 + col);
+                    best = key > best ? key : best;
+                }
+            }
         }
         const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), 1))) << 32) |
                                uint64_t(uint32_t(__shfl_xor(int(best & 0xFFFFFFFFu), 1)));
@@ -429,7 +441,7 @@ int launch_tile(const Problem& p, hipStream_t s) {
     hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI, RS, SP>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c,
                        p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), c_vec, p.keys,
-                       p.row_scale);
+                       p.row_scale, p.sample);
     return check_launch("mfma_staged");
 }
 

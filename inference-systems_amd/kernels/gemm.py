@@ -303,6 +303,83 @@ def gemm_argmax_with_kernel(a: torch.Tensor, w: torch.Tensor, kernel: int) -> tu
     return _launch_argmax(a, w, kernel)
 
 
+# ---------------------------------------------------------------------------
+# Sampled LM head: Sampler.forward on a @ w.T without the logits
+# ---------------------------------------------------------------------------
+def sample_contract_reason(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor) -> Optional[str]:
+    """Why the sampled head cannot take these inputs, or None if it can."""
+    reason = argmax_contract_reason(a, w)
+    if reason is not None:
+        return reason
+    if temperatures.dtype != torch.float32:
+        return f"temperatures must be float32, got {temperatures.dtype}"
+    if temperatures.device != a.device:
+        return "temperatures must be on the device of a"
+    if temperatures.shape != a.shape[:-1]:
+        return f"temperatures must have shape {tuple(a.shape[:-1])}, got {tuple(temperatures.shape)}"
+    if not temperatures.is_contiguous():
+        return "temperatures must be contiguous"
+    return None
+
+
+def _launch_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
+                   kernel: Optional[int] = None):
+    reason = sample_contract_reason(a, w, temperatures)
+    if reason is not None:
+        raise RuntimeError(f"nanovllm::gemm_sample: {reason}")
+    k = a.shape[-1]
+    n = w.shape[0]
+    m = a.numel() // k
+    tokens = torch.empty(a.shape[:-1], dtype=torch.int64, device=a.device)
+    scores = torch.empty(a.shape[:-1], dtype=torch.float32, device=a.device)
+    if m == 0:
+        return tokens, scores
+    need = _lib.argmax_workspace_bytes(m, n, k, k, k, _CODE[a.dtype])
+    _lib.check(need if need < 0 else _lib.OK, "nanovllm_gemm_argmax_workspace_bytes")
+    workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+    with torch.cuda.device(a.device):
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+        _lib.sample_raw(a.data_ptr(), w.data_ptr(), temperatures.data_ptr(), int(seed), int(offset),
+                        tokens.data_ptr(), scores.data_ptr(), m, n, k, k, k, _CODE[a.dtype], workspace.data_ptr(),
+                        need, stream, kernel)
+    return tokens, scores
+
+
+@torch.library.custom_op("nanovllm::gemm_sample", mutates_args=())
+def _gemm_sample_op(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
+                    offset: int) -> tuple[torch.Tensor, torch.Tensor]:
+    return _launch_sample(a, w, temperatures, seed, offset)
+
+
+@_gemm_sample_op.register_fake
+def _gemm_sample_fake(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
+                      offset: int) -> tuple[torch.Tensor, torch.Tensor]:
+    torch._check(w.dim() == 2)
+    torch._check(a.shape[-1] == w.shape[1])
+    torch._check(a.dtype == w.dtype)
+    torch._check(a.device == w.device)
+    torch._check(temperatures.shape == a.shape[:-1])
+    return (a.new_empty(a.shape[:-1], dtype=torch.int64), a.new_empty(a.shape[:-1], dtype=torch.float32))
+
+
+def gemm_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
+                offset: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Sampler.forward (nanovllm/layers/sampler.py:8-21) on the fp32 logits
+    a @ w.T without writing them: (token ids, winning scores).  Rows with
+    temperature <= 1e-10 take the greedy token (score = its logit); the
+    others a draw from softmax(logits / T) by the Gumbel-max rule
+    argmax_j (l_j / T - ln E_j), the reference's argmax of
+    softmax(l / T) / E, with E from the library's Philox4x32-10 stream at
+    (seed, offset); advance `offset` between calls for fresh draws."""
+    return torch.ops.nanovllm.gemm_sample(a, w, temperatures, int(seed), int(offset))
+
+
+def gemm_sample_with_kernel(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
+                            kernel: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The sampled head with its GEMM pass on one named kernel."""
+    return _launch_sample(a, w, temperatures, seed, offset, kernel)
+
+
 def validate_gemm_backend(backend: str) -> str:
     """Normalise a backend name (pattern of validate_gdn_decode_backend, gdn.py:13)."""
     value = str(backend).strip().lower()
@@ -369,7 +446,7 @@ def greedy_linear(x: torch.Tensor, weight: torch.Tensor, *,
                   backend: Optional[str] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """(argmax, max) of F.linear(x, weight) in fp32 along the last dim, with
     the backend switch of ``linear``: ``torch`` computes the fp32 logits and
-    takes torch.argmax (Sampler's greedy branch, sampler.py:19-32), ``hip``
+    takes torch.argmax (Sampler's greedy branch, sampler.py:8-21), ``hip``
     runs the fused greedy head, ``auto`` the fused head when its contract
     holds."""
     backend = validate_gemm_backend(backend) if backend is not None else default_backend()
@@ -382,3 +459,32 @@ def greedy_linear(x: torch.Tensor, weight: torch.Tensor, *,
     logits = F.linear(x, weight).float()
     tokens = logits.argmax(dim=-1)
     return tokens, logits.gather(-1, tokens.unsqueeze(-1)).squeeze(-1)
+
+
+def torch_sampler(logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Tensor:
+    """Sampler.forward (nanovllm/layers/sampler.py:8-21) as the reference
+    writes it, with torch's exponential draws: the ``torch`` backend of
+    sample_linear and the unfused baseline of the bench."""
+    greedy = temperatures <= 1e-10
+    safe_temperatures = torch.where(greedy, torch.ones_like(temperatures), temperatures)
+    float_logits = logits.float()
+    probs = torch.softmax(float_logits / safe_temperatures.unsqueeze(dim=1), dim=-1)
+    sample_tokens = probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
+    return torch.where(greedy, float_logits.argmax(dim=-1), sample_tokens)
+
+
+def sample_linear(x: torch.Tensor, weight: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int, *,
+                  backend: Optional[str] = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Sampled tokens of F.linear(x, weight) with the backend switch of
+    ``linear``: ``torch`` writes the fp32 logits and runs the reference
+    Sampler (its own exponential draws; no scores, None), ``hip`` the fused
+    sampled head, ``auto`` the fused head when its contract holds.  Returns
+    (tokens, scores)."""
+    backend = validate_gemm_backend(backend) if backend is not None else default_backend()
+    if backend != "torch":
+        reason = sample_contract_reason(x, weight, temperatures)
+        if reason is None:
+            return gemm_sample(x, weight, temperatures, seed, offset)
+        if backend == "hip":
+            raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
+    return torch_sampler(F.linear(x, weight), temperatures), None

@@ -20,8 +20,10 @@ import torch
 import torch.distributed as dist
 from torch import nn
 
-from ..kernels import gated_linear, greedy_linear
+from ..kernels import gated_linear, gemm_sample, greedy_linear, sample_contract_reason, sample_linear, torch_sampler
 from ..kernels import linear as gemm_linear
+from ..kernels import validate_gemm_backend
+from ..kernels.gemm import default_backend
 
 
 def divide(numerator: int, denominator: int) -> int:
@@ -173,7 +175,7 @@ class ParallelLMHead(nn.Module):
     context in prefill (embed_head.py:57-60); here the caller passes
     ``last_indices`` (or None in decode).  On the HIP path the GEMM writes
     fp32 logits directly (out_dtype=float32), which is the dtype the sampler
-    casts to (nanovllm/layers/sampler.py:26)."""
+    casts to (nanovllm/layers/sampler.py:15)."""
 
     def __init__(self, num_embeddings: int, embedding_dim: int, bias: bool = False):
         super().__init__()
@@ -205,7 +207,7 @@ class ParallelLMHead(nn.Module):
 
     def greedy(self, x: torch.Tensor, last_indices: Optional[torch.Tensor] = None):
         """Greedy tokens without the logits: the temperature-0 branch of
-        Sampler (nanovllm/layers/sampler.py:19-32, argmax of the fp32 logits,
+        Sampler (nanovllm/layers/sampler.py:8-21, argmax of the fp32 logits,
         first index on ties) applied to this head's output.  Returns (token
         ids int64, their fp32 logits); on the HIP path one fused launch
         replaces the [M, vocab] logits write and the argmax read-back.  With
@@ -229,6 +231,45 @@ class ParallelLMHead(nn.Module):
             tokens = torch.stack(all_tokens, 0).gather(0, best).squeeze(0)
             values = stacked_values.gather(0, best).squeeze(0)
         return tokens, values
+
+    def sample(self, x: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
+               last_indices: Optional[torch.Tensor] = None):
+        """Sampler.forward (nanovllm/layers/sampler.py:8-21) on this head's
+        logits: greedy tokens where temperature <= 1e-10, draws from
+        softmax(logits / T) elsewhere.  On the HIP path the sampled head ranks
+        each column by l / T - ln E (Gumbel-max, Philox noise at (seed,
+        offset)) inside the GEMM, so no logits are written; the caller
+        advances `offset` per step.  Returns token ids (and, on the HIP path,
+        the winning scores; None on the torch path, which runs the
+        reference Sampler on the gathered logits).  With tensor parallelism
+        every rank draws for its vocabulary shard with its own key (the seed
+        mixed with the rank, so shards draw independent noise), and rank 0
+        keeps the best score, the lower rank on ties; other ranks return
+        (None, None)."""
+        if last_indices is not None:
+            x = x[last_indices].contiguous()
+        if self.tp_size == 1:
+            return sample_linear(x, self.weight, temperatures, seed, offset, backend=self.gemm_backend)
+        backend = validate_gemm_backend(self.gemm_backend) if self.gemm_backend is not None else default_backend()
+        if backend == "torch" or sample_contract_reason(x, self.weight, temperatures) is not None:
+            if backend == "hip":
+                raise RuntimeError("HIP GEMM backend is unavailable: "
+                                   f"{sample_contract_reason(x, self.weight, temperatures)}")
+            logits = self.forward(x)
+            return (torch_sampler(logits, temperatures), None) if self.tp_rank == 0 else (None, None)
+        rank_seed = (int(seed) ^ (self.tp_rank * 0x9E3779B97F4A7C15)) & ((1 << 64) - 1)
+        tokens, scores = gemm_sample(x, self.weight, temperatures, rank_seed, offset)
+        tokens = tokens + self.vocab_start_idx
+        rank0 = self.tp_rank == 0
+        all_tokens = [torch.empty_like(tokens) for _ in range(self.tp_size)] if rank0 else None
+        all_scores = [torch.empty_like(scores) for _ in range(self.tp_size)] if rank0 else None
+        dist.gather(tokens, all_tokens, 0)
+        dist.gather(scores, all_scores, 0)
+        if not rank0:
+            return None, None
+        stacked = torch.stack(all_scores, 0)
+        best = stacked.argmax(0, keepdim=True)
+        return torch.stack(all_tokens, 0).gather(0, best).squeeze(0), stacked.gather(0, best).squeeze(0)
 
 
 class GemmLinear(nn.Linear):

@@ -23,7 +23,9 @@ path (paths relative to the reference repo):
     the shape table kDefaultShapes (gemm_bench.cu:45-57) and the repeat
     rule (gemm_bench.cu:371-379);
   * next to the GEMM (nanovllm/): SiluAndMul (layers/activation.py:8-11),
-    the greedy sampler's argmax (layers/sampler.py:19-32), the output gate
+    the sampler (layers/sampler.py:8-21: greedy argmax, and the sampled
+    rows' argmax of softmax(l / T) / E with E ~ Exp(1), here with the noise
+    of the library's counter-based generator, Philox4x32-10), the output gate
     of gated attention (models/qwen3_5.py:95) and the residual add +
     zero-centred RMSNorm (layers/layernorm.py:131-142).
 
@@ -33,7 +35,10 @@ reference's recorded zero error on every KAT row
 (results/rtx3060_gemm_matrix.csv:4-23); the float64 GEMM against
 torch.matmul in float64; the bf16/fp16 rounding against torch's and numpy's
 conversions and against hand-picked ties; the ULP metric against
-np.nextafter.  See tests/test_oracle.py.
+np.nextafter; Philox4x32-10 against the published known-answer vectors of
+its authors' Random123 distribution, and the sampled-row score
+l / T - ln E against the reference's softmax(l / T) / E (same argmax) and
+against the distribution it must draw from.  See tests/test_oracle.py.
 """
 from __future__ import annotations
 
@@ -378,7 +383,7 @@ def silu_mul_bound(r64, g64, u64, dg, du, dtype: str, ulps: float = 2.0) -> np.n
 # Greedy token of the LM head
 # ---------------------------------------------------------------------------
 def greedy_tokens(logits: np.ndarray) -> np.ndarray:
-    """Greedy rows of Sampler.forward (layers/sampler.py:19-32): argmax of
+    """Greedy rows of Sampler.forward (layers/sampler.py:8-21): argmax of
     the fp32 logits along the vocabulary, first index on ties (torch.argmax)."""
     return np.argmax(np.asarray(logits), axis=-1)
 
@@ -393,6 +398,98 @@ def greedy_token_admissible(token: np.ndarray, r64: np.ndarray, s64: np.ndarray,
     rows = np.arange(r64.shape[0])
     best = r64.max(axis=-1)
     chosen = r64[rows, token]
+    return chosen >= best - bound[rows, token] - bound.max(axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# Sampled rows of the LM head (Sampler.forward, layers/sampler.py:8-21)
+# ---------------------------------------------------------------------------
+_PHILOX_MUL = (0xD2511F53, 0xCD9E8D57)
+_PHILOX_WEYL = (0x9E3779B9, 0xBB67AE85)
+_MASK32 = np.uint64(0xFFFFFFFF)
+
+
+def philox4x32_10(counters: np.ndarray, key: tuple[int, int]) -> np.ndarray:
+    """Philox4x32-10 (Salmon, Moraes, Dror and Shaw, SC 2011) of uint32
+    counters [..., 4] under a 2-word key: ten rounds of
+    (c0, c1, c2, c3) -> (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0)),
+    the key advanced by the Weyl constants between rounds."""
+    c = np.asarray(counters, dtype=np.uint64) & _MASK32
+    c0, c1, c2, c3 = (c[..., i].copy() for i in range(4))
+    k0, k1 = int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF
+    for _ in range(10):
+        p0 = np.uint64(_PHILOX_MUL[0]) * c0
+        p1 = np.uint64(_PHILOX_MUL[1]) * c2
+        c0, c1, c2, c3 = ((p1 >> np.uint64(32)) ^ c1 ^ np.uint64(k0), p1 & _MASK32,
+                          (p0 >> np.uint64(32)) ^ c3 ^ np.uint64(k1), p0 & _MASK32)
+        k0 = (k0 + _PHILOX_WEYL[0]) & 0xFFFFFFFF
+        k1 = (k1 + _PHILOX_WEYL[1]) & 0xFFFFFFFF
+    return np.stack([c0, c1, c2, c3], axis=-1).astype(np.uint32)
+
+
+def sample_uniform(m: int, n: int, seed: int, offset: int) -> np.ndarray:
+    """u[i, j] in (0, 1] of the library's sampled head: the 24 high bits of
+    word j % 4 of Philox4x32-10(counter = (j // 4, i, offset, offset >> 32),
+    key = (seed, seed >> 32)), plus one, over 2^24 (exact in float64)."""
+    rows = np.arange(m, dtype=np.uint64)[:, None]
+    cols = np.arange(n, dtype=np.uint64)[None, :]
+    ctr = np.empty((m, n, 4), dtype=np.uint64)
+    ctr[..., 0] = cols >> np.uint64(2)
+    ctr[..., 1] = rows
+    ctr[..., 2] = np.uint64(offset & 0xFFFFFFFF)
+    ctr[..., 3] = np.uint64((offset >> 32) & 0xFFFFFFFF)
+    words = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))
+    word = np.broadcast_to((cols & np.uint64(3)).astype(np.int64)[..., None], (m, n, 1))
+    x = np.take_along_axis(words, word, axis=-1)[..., 0]
+    return ((x.astype(np.float64) // 256.0) + 1.0) / 2.0 ** 24
+
+
+def sample_exponential(u: np.ndarray) -> np.ndarray:
+    """E = -ln u clamped to >= 1e-10, as the reference clamps its Exp(1)
+    draws (sampler.py:20)."""
+    return np.maximum(-np.log(np.asarray(u, dtype=np.float64)), 1e-10)
+
+
+def sample_scores_f64(logits: np.ndarray, temperatures: np.ndarray, e: np.ndarray) -> np.ndarray:
+    """Rank of every column: the logit on a greedy row (temperature <= 1e-10
+    in float32, sampler.py:9), l / T - ln E on a sampled one (the Gumbel-max
+    form of the reference's softmax(l / T) / E)."""
+    logits = np.asarray(logits, dtype=np.float64)
+    t = np.asarray(temperatures, dtype=np.float32)
+    greedy = (t <= np.float32(1e-10))[:, None]
+    safe_t = np.where(greedy[:, 0], 1.0, t.astype(np.float64))[:, None]
+    return np.where(greedy, logits, logits / safe_t - np.log(e))
+
+
+def sampler_reference_f64(logits: np.ndarray, temperatures: np.ndarray, e: np.ndarray) -> np.ndarray:
+    """Sampler.forward (sampler.py:9-21) restated in float64 for given noise
+    E: greedy rows take argmax l; the others argmax softmax(l / T) / E."""
+    logits = np.asarray(logits, dtype=np.float64)
+    t = np.asarray(temperatures, dtype=np.float32)
+    greedy = t <= np.float32(1e-10)
+    safe_t = np.where(greedy, 1.0, t.astype(np.float64))[:, None]
+    z = logits / safe_t
+    p = np.exp(z - z.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    sample = (p / e).argmax(axis=-1)
+    return np.where(greedy, logits.argmax(axis=-1), sample)
+
+
+def sample_token_admissible(token: np.ndarray, r64: np.ndarray, s64: np.ndarray, k: int,
+                            temperatures: np.ndarray, e: np.ndarray) -> np.ndarray:
+    """True where `token` is a correct choice of the sampled head for fp32
+    logits: its exact score is within the error budget of the best exact
+    score.  The budget is the fp32 accumulation bound of each logit over T
+    (twice, as two logits may swap), plus 4e-6 (1 + |score|) for the fp32
+    division, the hardware logarithms and the draw's fp32 E."""
+    t = np.asarray(temperatures, dtype=np.float32)
+    greedy = t <= np.float32(1e-10)
+    scale = np.where(greedy, 1.0, 1.0 / np.where(greedy, 1.0, t.astype(np.float64)))[:, None]
+    sc = sample_scores_f64(r64, temperatures, e)
+    bound = fp32_accumulation_bound(s64, k) * scale + np.where(greedy[:, None], 0.0, 4e-6 * (1.0 + np.abs(sc)))
+    rows = np.arange(sc.shape[0])
+    best = sc.max(axis=-1)
+    chosen = sc[rows, token]
     return chosen >= best - bound[rows, token] - bound.max(axis=-1)
 
 

@@ -254,6 +254,29 @@ def test_argmax_validates_before_launch(lib):
     assert rc == L.EUNSUPPORTED
 
 
+def test_sample_validates_before_launch(lib):
+    """The sampled head shares the greedy head's checks and adds its own:
+    temperatures must be a non-null, 4-byte aligned device pointer."""
+    assert lib.nanovllm_gemm_sample(None, None, None, 1, 2, None, None, 0, 64, 16, 16, 16, BF16, None, 0,
+                                    None) == L.OK
+    dummy = 1 << 20
+    need = L.argmax_workspace_bytes(4, 64, 16, 16, 16, BF16)
+    rc = lib.nanovllm_gemm_sample(dummy, dummy, None, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16, dummy, need, None)
+    assert rc == L.EINVAL and "temperatures" in L.last_error()
+    rc = lib.nanovllm_gemm_sample(dummy, dummy, dummy + 2, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16, dummy, need,
+                                  None)
+    assert rc == L.EINVAL and "4-byte aligned" in L.last_error()
+    rc = lib.nanovllm_gemm_sample(dummy, dummy, dummy, 1, 2, dummy, None, 4, 64, 16, 16, 16, L.F32, dummy, need,
+                                  None)
+    assert rc == L.EUNSUPPORTED
+    rc = lib.nanovllm_gemm_sample_with_kernel(L.KERNEL_FP32_TILED, dummy, dummy, dummy, 1, 2, dummy, None, 4, 64,
+                                              16, 16, 16, BF16, dummy, need, None)
+    assert rc == L.EUNSUPPORTED and "fp32_tiled" in L.last_error()
+    rc = lib.nanovllm_gemm_sample_with_kernel(99, dummy, dummy, dummy, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16,
+                                              dummy, need, None)
+    assert rc == L.EINVAL and "unknown kernel" in L.last_error()
+
+
 # ---------------------------------------------------------------------------
 # GEMMs with a prologue (output gate, residual add + RMSNorm)
 # ---------------------------------------------------------------------------

@@ -585,3 +585,131 @@ def test_argmax_lm_head_shape_and_graph(m):
         t_eager, v_eager = G.gemm_argmax(x, w)
         torch.cuda.synchronize()
         assert torch.equal(t_static, t_eager) and torch.equal(v_static, v_eager), f"replay {step}"
+
+
+# ---------------------------------------------------------------------------
+# Sampled LM head (Sampler.forward without logits: greedy rows + Gumbel-max)
+# ---------------------------------------------------------------------------
+SAMPLE_CASES = ([(L.KERNEL_SPLITK_DECODE, m, n) for m in (1, 5, 32) for n in (1000, 70001)]
+                + [(L.KERNEL_MFMA_STAGED, m, 1000) for m in (1, 33, 300)])
+
+
+def _sample_temps(m, gen):
+    t = torch.rand(m, generator=gen) * 1.8 + 0.2
+    t[::3] = 0.0                       # greedy rows
+    if m > 1:
+        t[1] = 1e-10                   # <= 1e-10 in float32: greedy
+    return t
+
+
+@pytest.mark.parametrize("kernel,m,n", SAMPLE_CASES, ids=[f"{L.kernel_name(k)}-M{m}-N{n}" for k, m, n in SAMPLE_CASES])
+@pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_sample_admissible_against_oracle(kernel, m, n, din):
+    """Every token is an admissible winner of the oracle's scores (same
+    Philox noise, float64 logits); greedy rows are exactly the greedy head's
+    token and logit on the same kernel; a sampled row's score is its
+    token's l / T - ln E within the fp32 budget."""
+    gen = torch.Generator().manual_seed(m * 13 + n)
+    k = 256
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.2).to(din)
+    temps = _sample_temps(m, gen)
+    seed, offset = 0x5EED0000 + m, (3 << 32) | n
+    ad, wd, td = a.to(DEV), w.to(DEV), temps.to(DEV)
+    _say(f"sample {L.kernel_name(kernel)} {NAME[din]} M={m} N={n}")
+    tokens, scores = G.gemm_sample_with_kernel(ad, wd, td, seed, offset, kernel)
+    g_tokens, g_values = G.gemm_argmax_with_kernel(ad, wd, kernel)
+    torch.cuda.synchronize()
+    tokens, scores = tokens.cpu().numpy(), scores.cpu().numpy()
+    greedy = (temps <= 1e-10).numpy()
+    np.testing.assert_array_equal(tokens[greedy], g_tokens.cpu().numpy()[greedy])
+    np.testing.assert_array_equal(scores[greedy], g_values.cpu().numpy()[greedy])
+    a64, w64 = a.double().numpy(), w.double().numpy()
+    r = orc.gemm_f64(a64, w64)
+    e = orc.sample_exponential(orc.sample_uniform(m, n, seed, offset))
+    ok = orc.sample_token_admissible(tokens, r, orc.abs_products_f64(a64, w64), k, temps.numpy(), e)
+    assert ok.all(), f"rows {np.flatnonzero(~ok)[:8]}"
+    sc = orc.sample_scores_f64(r, temps.numpy(), e)[np.arange(m), tokens]
+    np.testing.assert_allclose(scores[~greedy], sc[~greedy], rtol=1e-5, atol=1e-3)
+
+
+@pytest.mark.parametrize("kernel,m", [(L.KERNEL_SPLITK_DECODE, 32), (L.KERNEL_MFMA_STAGED, 64)],
+                         ids=["splitk_decode", "mfma_staged"])
+def test_sample_noise_is_the_oracles_philox(kernel, m):
+    """At a huge temperature the score is -ln E (the logits vanish), so each
+    row's token must carry the row's largest uniform u of the oracle's
+    Philox stream: pins the device generator, its counter layout and word
+    choice bit for bit (64 columns: a wrong word or counter would miss the
+    maximum on most rows)."""
+    gen = torch.Generator().manual_seed(5)
+    n, k = 64, 64
+    a = torch.randn((m, k), generator=gen).bfloat16()
+    w = (torch.randn((n, k), generator=gen) * 0.1).bfloat16()
+    temps = torch.full((m,), 1e30)
+    seed, offset = 0xDEADBEEF12345678, 99
+    _say(f"sample noise {L.kernel_name(kernel)} M={m}")
+    tokens, _ = G.gemm_sample_with_kernel(a.to(DEV), w.to(DEV), temps.to(DEV), seed, offset, kernel)
+    torch.cuda.synchronize()
+    u = orc.sample_uniform(m, n, seed, offset)
+    tokens = tokens.cpu().numpy()
+    np.testing.assert_array_equal(u[np.arange(m), tokens], u.max(axis=-1))
+
+
+def test_sample_distribution():
+    """8192 rows with the same logits (exact in bf16: a = e_0, W[j] = l_j e_0)
+    draw from softmax(l / T): a chi-square test against the exact
+    probabilities, and agreement with the oracle's own draws on >= 99.9% of
+    rows (the rest are near-ties of the fp32 score)."""
+    from scipy import stats
+    logits = torch.tensor([1.0, 0.25, -0.5, 2.0, 0.0, 1.5])
+    m, n, k, t = 8192, logits.numel(), 8, 0.75
+    a = torch.zeros((m, k))
+    a[:, 0] = 1.0
+    w = torch.zeros((n, k))
+    w[:, 0] = logits
+    temps = torch.full((m,), t)
+    seed, offset = 77, 5
+    _say("sample distribution M=8192")
+    tokens, _ = G.gemm_sample(a.bfloat16().to(DEV), w.bfloat16().to(DEV), temps.to(DEV), seed, offset)
+    torch.cuda.synchronize()
+    tokens = tokens.cpu().numpy()
+    z = logits.double().numpy() / np.float64(np.float32(t))
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    counts = np.bincount(tokens, minlength=n)
+    assert stats.chisquare(counts, p * m).pvalue > 1e-4, counts
+    e = orc.sample_exponential(orc.sample_uniform(m, n, seed, offset))
+    want = orc.sample_scores_f64(np.tile(logits.double().numpy(), (m, 1)), temps.numpy(), e).argmax(-1)
+    assert float((tokens == want).mean()) >= 0.999
+
+
+def test_sample_offsets_and_graph_replay():
+    """A new offset gives new draws; a call captured in a HIP graph replays
+    its own seed and offset (the eager call with the same pair gives the
+    same tokens on every replay)."""
+    gen = torch.Generator().manual_seed(8)
+    m, n, k = 16, 5000, 128
+    a = torch.randn((m, k), generator=gen).bfloat16().to(DEV)
+    w = (torch.randn((n, k), generator=gen) * 0.05).bfloat16().to(DEV)
+    temps = torch.full((m,), 1.0, device=DEV)
+    _say("sample offsets and graph")
+    t0, _ = G.gemm_sample(a, w, temps, 1, 0)
+    t1, _ = G.gemm_sample(a, w, temps, 1, 1)
+    t0b, _ = G.gemm_sample(a, w, temps, 1, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(t0, t0b)
+    assert not torch.equal(t0, t1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        G.gemm_sample(a, w, temps, 1, 7)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        t_static, s_static = G.gemm_sample(a, w, temps, 1, 7)
+    for step in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        t_eager, s_eager = G.gemm_sample(a, w, temps, 1, 7)
+        torch.cuda.synchronize()
+        assert torch.equal(t_static, t_eager) and torch.equal(s_static, s_eager), f"replay {step}"

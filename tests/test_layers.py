@@ -126,6 +126,28 @@ def test_lm_head_greedy_matches_argmax_of_logits():
     assert t2.shape == (2,)
 
 
+def test_lm_head_sample_torch_path():
+    """ParallelLMHead.sample off the HIP path runs the reference Sampler on
+    the fp32 logits: greedy rows (temperature <= 1e-10) are the greedy
+    tokens, sampled rows valid token ids, and no scores."""
+    head = Lyr.ParallelLMHead(50, 16)
+    head.weight.weight_loader(head.weight, torch.randn(50, 16, generator=torch.Generator().manual_seed(6)))
+    head.gemm_backend = "auto"
+    x = torch.randn(8, 16, generator=torch.Generator().manual_seed(7))
+    temps = torch.tensor([0.0, 1.0, 1e-10, 0.7, 0.0, 2.0, 0.0, 0.3])
+    tokens, scores = head.sample(x, temps, seed=1, offset=2)
+    greedy_tokens, _ = head.greedy(x)
+    greedy = temps <= 1e-10
+    assert scores is None and tokens.dtype == torch.int64 and tokens.shape == (8,)
+    assert torch.equal(tokens[greedy], greedy_tokens[greedy])
+    assert ((tokens >= 0) & (tokens < 50)).all()
+    torch.manual_seed(0)
+    many = torch.stack([head.sample(x[1:2], temps[1:2], 1, 2)[0] for _ in range(2000)]).flatten()
+    p = torch.softmax(head(x[1:2]).float(), -1).flatten()
+    top = int(p.argmax())
+    assert abs(float((many == top).float().mean()) - float(p[top])) < 0.05
+
+
 def test_qwen35_mlp_matches_reference_composition():
     """down_proj(SiluAndMul(gate_up_proj(x))) of models/qwen3_5.py:117-118; on
     CPU tensors the auto backend takes the reference composition."""
@@ -268,6 +290,14 @@ def _tp_worker(rank, world, init_file, result_file):
             ok = ok and torch.allclose(gv, full.max(-1).values, rtol=1e-6, atol=1e-6)
         else:
             ok = ok and gt is None and gv is None
+        # Sampled head across shards off the HIP path: the logits are
+        # gathered to rank 0, which runs the reference Sampler; greedy rows
+        # (temperature 0) give the greedy tokens.
+        st, ss = gh.sample(xt, torch.zeros(4), seed=3, offset=4)
+        if rank == 0:
+            ok = ok and ss is None and torch.equal(st, F.linear(xt, wt).argmax(-1))
+        else:
+            ok = ok and st is None and ss is None
         # o_proj with the output gate: each rank holds its heads' columns of
         # W and its heads of the attention output and the gate (the head split
         # of the reference's tensor parallelism); the all-reduce adds them.

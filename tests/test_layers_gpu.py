@@ -202,6 +202,44 @@ def test_lm_head_greedy_hip(m):
     assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
 
 
+@torch.inference_mode()
+@pytest.mark.parametrize("m", [1, 32, 40])
+def test_lm_head_sample_hip(m):
+    """ParallelLMHead.sample on the HIP path (Qwen3.5 vocabulary): greedy
+    rows equal ParallelLMHead.greedy, sampled rows are admissible draws for
+    the oracle's noise (checked on the oracle's float64 logits of the head's
+    own bf16 weights), and the torch backend (the reference Sampler on the
+    logits) agrees on the greedy rows."""
+    gen = torch.Generator().manual_seed(90 + m)
+    head = _init(Lyr.ParallelLMHead(151936, 1024), gen).to(DEV, torch.bfloat16)
+    head.gemm_backend = "hip"
+    x = torch.randn(m, 1024, generator=gen).bfloat16().to(DEV)
+    temps = torch.rand(m, generator=gen) + 0.5
+    temps[::2] = 0.0
+    seed, offset = 1234, 56
+    tokens, scores = head.sample(x, temps.to(DEV), seed, offset)
+    g_tokens, _ = head.greedy(x)
+    logits = head(x).cpu()
+    head.gemm_backend = "torch"
+    t_tokens, t_scores = head.sample(x, temps.to(DEV), seed, offset)
+    torch.cuda.synchronize()
+    greedy = temps <= 1e-10
+    assert t_scores is None
+    assert torch.equal(tokens.cpu()[greedy], g_tokens.cpu()[greedy])
+    assert ((t_tokens >= 0) & (t_tokens < 151936)).all()
+    # The torch path's logits come out of a bf16 GEMM: its greedy tokens are
+    # the best up to one bf16 rounding of the logit.
+    best = logits[greedy].max(-1).values
+    picked = logits[greedy].gather(-1, t_tokens.cpu()[greedy][:, None]).squeeze(-1)
+    assert (picked >= best - best.abs() * 2.0 ** -7).all()
+    a64 = x.double().cpu().numpy()
+    w64 = head.weight.double().cpu().numpy()
+    r = orc.gemm_f64(a64, w64)
+    e = orc.sample_exponential(orc.sample_uniform(m, 151936, seed, offset))
+    ok = orc.sample_token_admissible(tokens.cpu().numpy(), r, orc.abs_products_f64(a64, w64), 1024, temps.numpy(), e)
+    assert ok.all()
+
+
 def _norm(gen, hidden=1024):
     norm = Lyr.Qwen35RMSNorm(hidden)
     with torch.no_grad():

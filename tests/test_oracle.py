@@ -378,6 +378,108 @@ def test_greedy_tokens_first_index_on_ties_and_admissible():
 
 
 # ---------------------------------------------------------------------------
+# Sampled LM head: Philox noise and the Gumbel-max form of Sampler.forward
+# ---------------------------------------------------------------------------
+# Known-answer vectors of Philox4x32-10 published with its authors' Random123
+# library (kat_vectors: counter, key, expected output).
+PHILOX_KATS = [
+    ((0x00000000, 0x00000000, 0x00000000, 0x00000000), (0x00000000, 0x00000000),
+     (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF), (0xFFFFFFFF, 0xFFFFFFFF),
+     (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", PHILOX_KATS)
+def test_philox_known_answers(ctr, key, want):
+    got = orc.philox4x32_10(np.array([ctr], dtype=np.uint64), key)[0]
+    assert tuple(int(x) for x in got) == want
+
+
+def test_sample_uniform_layout():
+    """u[i, j] comes from word j % 4 of the draw at counter (j // 4, i,
+    offset, offset >> 32) under key (seed, seed >> 32), lies in (0, 1] and is
+    a multiple of 2^-24."""
+    seed, offset = 0x0123456789ABCDEF, (7 << 32) | 5
+    u = orc.sample_uniform(3, 9, seed, offset)
+    assert ((u > 0) & (u <= 1)).all()
+    assert np.array_equal(u * 2.0 ** 24, np.round(u * 2.0 ** 24))
+    for i in range(3):
+        for j in range(9):
+            w = orc.philox4x32_10(np.array([[j // 4, i, 5, 7]], dtype=np.uint64), (0x89ABCDEF, 0x01234567))[0]
+            assert u[i, j] == ((int(w[j % 4]) >> 8) + 1) / 2.0 ** 24
+    # different offsets and seeds give different draws
+    assert not np.array_equal(u, orc.sample_uniform(3, 9, seed, offset + 1))
+    assert not np.array_equal(u, orc.sample_uniform(3, 9, seed + 1, offset))
+
+
+def test_gumbel_scores_pick_the_reference_sample():
+    """argmax_j (l / T - ln E) is the reference's argmax_j softmax(l / T) / E
+    for the same noise E, on sampled and greedy rows alike."""
+    rng = np.random.default_rng(11)
+    logits = rng.normal(0.0, 3.0, size=(64, 50))
+    temps = rng.uniform(0.05, 2.0, size=64).astype(np.float32)
+    temps[::7] = 0.0                      # greedy rows
+    temps[3] = np.float32(1e-10)          # <= 1e-10 in float32: greedy
+    temps[4] = np.float32(1.2e-10)        # just above: sampled
+    e = orc.sample_exponential(orc.sample_uniform(64, 50, 3, 0))
+    want = orc.sampler_reference_f64(logits, temps, e)
+    got = orc.sample_scores_f64(logits, temps, e).argmax(axis=-1)
+    np.testing.assert_array_equal(got, want)
+    greedy_rows = temps <= np.float32(1e-10)
+    np.testing.assert_array_equal(got[greedy_rows], logits[greedy_rows].argmax(-1))
+
+
+def _chi2_pvalue(counts: np.ndarray, probs: np.ndarray) -> float:
+    from scipy import stats
+    expected = probs * counts.sum()
+    return float(stats.chisquare(counts, expected).pvalue)
+
+
+def test_sampled_rows_follow_softmax():
+    """20000 rows with the same logits, each with its own noise (the row
+    enters the counter), draw from softmax(l / T): a chi-square test against
+    the exact probabilities passes, and planted mistakes in the score (+ln E,
+    T applied twice, the noise of column j + 1) fail it."""
+    logits = np.array([1.0, 0.2, -0.5, 2.0, 0.0, 1.5])
+    t = 0.8
+    m = 20000
+    r = np.tile(logits, (m, 1))
+    temps = np.full(m, t, dtype=np.float32)
+    e = orc.sample_exponential(orc.sample_uniform(m, logits.size, 2024, 17))
+    z = logits / np.float64(np.float32(t))
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    tokens = orc.sample_scores_f64(r, temps, e).argmax(-1)
+    assert _chi2_pvalue(np.bincount(tokens, minlength=logits.size), p) > 1e-3
+    zz = r / np.float64(np.float32(t))
+    planted = {
+        "+ln E": (zz + np.log(e)).argmax(-1),
+        "T twice": (zz / t - np.log(e)).argmax(-1),
+        "no noise": zz.argmax(-1),
+    }
+    for name, bad in planted.items():
+        assert _chi2_pvalue(np.bincount(bad, minlength=logits.size), p) < 1e-6, name
+
+
+def test_sample_admissibility():
+    """The exact winner is admissible; a clearly worse column is not; a
+    column whose score is within the fp32 budget of the best is."""
+    r = np.array([[0.0, 1.0, 3.0, 2.0]])
+    s = np.ones_like(r)
+    temps = np.array([0.5], dtype=np.float32)
+    e = np.array([[1.0, 1.0, 1.0, 1.0]])
+    assert orc.sample_token_admissible(np.array([2]), r, s, 1024, temps, e).all()
+    assert not orc.sample_token_admissible(np.array([3]), r, s, 1024, temps, e).any()
+    e2 = np.array([[1.0, 1.0, 1.0, np.exp(-1.0 + 1e-7)]])   # column 3 scores 4 + 1 - 1e-7 against 6
+    assert not orc.sample_token_admissible(np.array([3]), r, s, 1024, temps, e2).any()
+    e3 = np.array([[1.0, 1.0, 1.0, np.exp(-2.0 + 1e-6)]])   # column 3 within 1e-6 of column 2
+    assert orc.sample_token_admissible(np.array([3]), r, s, 1024, temps, e3).all()
+
+
+# ---------------------------------------------------------------------------
 # Prologues: output gate and residual add + RMSNorm
 # ---------------------------------------------------------------------------
 def _bf16(x) -> np.ndarray:
