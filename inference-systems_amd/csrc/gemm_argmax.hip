@@ -10,10 +10,11 @@ namespace nvg {
 namespace {
 
 // One workgroup per row; a row's keys are contiguous ([m, blocks]).  Each
-// thread issues kFinalizeUnroll independent loads per round, so the ~9500
-// keys of a 151936-entry vocabulary take three rounds of memory latency.
+// thread issues kFinalizeUnroll independent loads per round, so up to 10240
+// keys (the ~9500 of a 151936-entry vocabulary at 16 columns per
+// workgroup) take one round of memory latency.
 constexpr int kFinalizeThreads = 1024;
-constexpr int kFinalizeUnroll = 4;
+constexpr int kFinalizeUnroll = 10;
 
 __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(
     const uint64_t* __restrict__ keys, int64_t blocks, int64_t m, int64_t* __restrict__ tokens,

@@ -362,6 +362,13 @@ def _gemm_sample_fake(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tens
     return (a.new_empty(a.shape[:-1], dtype=torch.int64), a.new_empty(a.shape[:-1], dtype=torch.float32))
 
 
+def _as_i64(x: int) -> int:
+    """x modulo 2^64 as a signed 64-bit value (the op schema's int), the
+    same 64 bits the C ABI reads as uint64_t."""
+    x = int(x) & ((1 << 64) - 1)
+    return x - (1 << 64) if x >= 1 << 63 else x
+
+
 def gemm_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
                 offset: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Sampler.forward (nanovllm/layers/sampler.py:8-21) on the fp32 logits
@@ -370,8 +377,9 @@ def gemm_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, se
     others a draw from softmax(logits / T) by the Gumbel-max rule
     argmax_j (l_j / T - ln E_j), the reference's argmax of
     softmax(l / T) / E, with E from the library's Philox4x32-10 stream at
-    (seed, offset); advance `offset` between calls for fresh draws."""
-    return torch.ops.nanovllm.gemm_sample(a, w, temperatures, int(seed), int(offset))
+    (seed, offset), both taken modulo 2^64; advance `offset` between calls
+    for fresh draws."""
+    return torch.ops.nanovllm.gemm_sample(a, w, temperatures, _as_i64(seed), _as_i64(offset))
 
 
 def gemm_sample_with_kernel(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,

@@ -7,6 +7,7 @@ unsharded F.linear.  The 2-rank case follows the reference's gloo pattern
 (tests/test_qwen35_tp.py:26-31, 125-158)."""
 from __future__ import annotations
 
+import importlib
 import os
 import tempfile
 
@@ -326,3 +327,14 @@ def test_tensor_parallel_two_ranks_gloo():
         mp.start_processes(_tp_worker, args=(2, init_file, result), nprocs=2, start_method="spawn")
         for r in range(2):
             assert open(f"{result}.{r}").read() == "ok", f"rank {r}"
+
+
+def test_sample_seed_and_offset_wrap_to_64_bits():
+    """Seeds and offsets reach the C ABI as their low 64 bits, through the
+    op schema's signed int."""
+    G = importlib.import_module(PKG.__name__ + ".kernels.gemm")
+    assert G._as_i64(5) == 5
+    assert G._as_i64(-1) == -1
+    assert G._as_i64((1 << 64) - 1) == -1
+    assert G._as_i64(1 << 63) == -(1 << 63)
+    assert G._as_i64((1 << 64) + 7) == 7
