@@ -445,24 +445,31 @@ int launch_tile(const Problem& p, hipStream_t s) {
     return check_launch("mfma_staged");
 }
 
-// Tile and schedule by grid size, in 128 x 128 tiles (bf16, MI355X, one
-// launch; every choice sums K in the same order, so none changes a result
-// bit):
-//   * at most 128 (half the CUs): 64 x 64 tiles, four times the workgroups
+// Tile and schedule by grid size (bf16, MI355X, one launch; every choice
+// sums K in the same order, so none changes a result bit).  "tiles" counts
+// 128 x 128 tiles, "wide" 128 x 256 ones:
+//   * tiles <= 128 (half the CUs): 64 x 64 tiles, four times the workgroups
 //     (1024^3 11.7 -> 6.8 us, 512 x 4096 x 1024 12.3 -> 8.1 us,
 //     2048 x 1024 x 2048 20.6 -> 13.8 us, 512 x 1024 x 3584 33.0 -> 17.0 us),
 //     with a 3-deep ring from K = 2048 (2048 x 1024 x 2048: 13.8 us against
 //     14.1; 512 x 1024 x 3584: 17.0 against 27.3);
-//   * enough 128 x 256 tiles for every CU: one 8-wave workgroup per CU on
+//   * 128 < wide <= 256 or wide > 384: one 8-wave workgroup per CU on
 //     128 x 256 (half the A reads of two 128 x 128 tiles), 3-deep ring,
-//     spread copies (2048 x 4096 x 1024: 20.3 -> 18.9 us; 2048 x 37984 x
-//     1024: 172 -> 162 us);
-//   * otherwise at most one tile per CU: 128 x 128, 3-deep ring, spread
-//     copies (4096 x 1024 x 3584, 256 tiles: 40.0 -> 31.1 us against the
-//     burst schedule, which measured 34-39 us with 3 or 2 stages);
-//   * otherwise (257 .. 511 tiles, and the greedy LM head, whose epilogue
-//     is written for 4 waves): 128 x 128 with a 2-deep ring (64 KiB), so two
-//     workgroups share a CU and one's MFMAs overlap the other's copies.
+//     copies spread between the MFMAs.  Against the 2-deep 128 x 128 burst
+//     schedule below: wide 144 (2304 x 2048 x 1024) 17.5 -> 14.7 us, 160
+//     (2048 x 2560) 17.8 -> 15.5, 192 (2048 x 3072 x 2048) 32.8 -> 28.4,
+//     224 (2048 x 3584) 19.8 -> 18.0, 256 (2048 x 4096) 20.3 -> 18.9, 416
+//     (2048 x 6656) 35.9 -> 33.2, 512 (2048 x 8192) 38.5 -> 36.6, 2384
+//     (2048 x 37984) 172 -> 162;
+//   * 256 < wide <= 384 (one full round of 128 x 256 tiles and a partial
+//     second): the 128 x 128 burst schedule with two workgroups per CU, whose
+//     smaller tiles fill the second round better (wide 288 / 320 / 352 /
+//     384: 29.1 / 30.1 / 29.4 / 30.4 us against 30.8 / 32.0 / 32.2 / 32.6);
+//   * otherwise (128 < tiles <= 256): 128 x 128, 4 waves, 3-deep ring,
+//     spread copies, one workgroup per CU (4096 x 1024 x 3584, 256 tiles:
+//     40.0 -> 31.1 us against the burst schedule);
+//   * the greedy head, whose epilogue is written for 4 waves, takes the
+//     128 x 128 choices only.
 constexpr int64_t kSmallGridTiles = kCus / 2;
 
 template <int DT, int DT_OUT, int EPI, int RS = 0>
@@ -482,8 +489,9 @@ int launch_epi(const Problem& p, hipStream_t s) {
         }
     }
     if constexpr (EPI != EPI_ARGMAX) {
-        const int64_t wide_tiles = ((p.m + 127) / 128) * ((n_tiles + 255) / 256);
-        if (wide_tiles >= kCus) return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI, RS, 1>(p, s);
+        const int64_t wide = ((p.m + 127) / 128) * ((n_tiles + 255) / 256);
+        if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2))
+            return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI, RS, 1>(p, s);
     }
     if (tiles <= kCus) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI, RS, 1>(p, s);
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS, 0>(p, s);

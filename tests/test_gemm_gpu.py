@@ -172,21 +172,22 @@ def test_workload_parity(name, m):
     _check_tolerance(got, a, b, wl.b_layout, wl.dtype_out, rows=rows)
 
 
-STAGED_GRIDS = [(600, 1000, 1000), (600, 1000, 2056), (1100, 2000, 1000), (2100, 2000, 1000), (2100, 4100, 1000)]
+STAGED_GRIDS = [(600, 1000, 1000), (600, 1000, 2056), (1100, 2000, 1000), (2100, 2000, 1000), (2100, 4100, 1000),
+                (2100, 7000, 1000)]
 
 
 @pytest.mark.parametrize("m,n,k", STAGED_GRIDS, ids=["40tiles-64x64", "40tiles-64x64-deep", "144tiles-spread",
-                                                     "272tiles-2deep", "561tiles-128x256"])
+                                                     "wide136-128x256", "wide289-2deep", "wide476-128x256"])
 @pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
                          ids=["bf16", "f16-f32"])
 def test_staged_ring_depths_ragged(m, n, k, din, dout):
     """mfma_staged's tile choices: a grid of at most 128 tiles of 128 x 128
-    takes 64 x 64 tiles (3-deep ring from K = 2048); one with at least 256
-    tiles of 128 x 256 takes those (8 waves, 3-deep ring, copies spread
-    between the MFMAs); otherwise up to 256 tiles 128 x 128 with the spread
-    3-deep ring, above that a 2-deep one; each on ragged M and N and a K
-    that is not a multiple of the 64-wide K-tile (the last tile is padded
-    with zeros)."""
+    takes 64 x 64 tiles (3-deep ring from K = 2048); up to 256 tiles 128 x
+    128 with the spread 3-deep ring; above that 128 x 256 tiles (8 waves,
+    3-deep ring, copies spread between the MFMAs) unless there are 257-384
+    of those, where 128 x 128 with a 2-deep ring takes over; each on ragged
+    M and N and a K that is not a multiple of the 64-wide K-tile (the last
+    tile is padded with zeros)."""
     _say(f"staged ring M={m} N={n} K={k} {NAME[din]}->{NAME[dout]}")
     gen = torch.Generator().manual_seed(m + n)
     a = torch.randn((m, k), generator=gen).to(din)

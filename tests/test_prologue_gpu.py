@@ -250,12 +250,14 @@ def test_add_rmsnorm_prologue_kernel_path(m, silu):
         _check_add_norm(out, res_out, h, r, nw, w, 1e-5, torch.bfloat16, torch.bfloat16)
 
 
-@pytest.mark.parametrize("m,n,silu", [(1500, 2000, False), (2100, 4100, False), (2100, 2050, True)],
-                         ids=["128x128-spread", "128x256", "128x256-silu"])
+@pytest.mark.parametrize("m,n,silu", [(1500, 2000, False), (2100, 2000, False), (2100, 1000, True),
+                                      (2100, 4100, False)],
+                         ids=["128x128-spread", "128x256", "128x256-silu", "128x128-2deep"])
 def test_add_rmsnorm_row_scale_large_grids(m, n, silu):
     """The row-scaled epilogue on mfma_staged's large-grid tiles: 192 tiles
-    of 128 x 128 (3-deep ring, spread copies) and at least 256 tiles of
-    128 x 256 (8 waves), plain and with SiLU-and-mul; ragged M, N and K."""
+    of 128 x 128 (3-deep ring, spread copies), 136 tiles of 128 x 256 (8
+    waves, spread copies; plain and with SiLU-and-mul) and 289 (where 128 x
+    128 with a 2-deep ring takes over); ragged M, N and K."""
     gen = torch.Generator().manual_seed(m + n)
     k = 1000
     h, r, nw, w = _norm_inputs(m, 2 * n if silu else n, k, torch.bfloat16, gen)
