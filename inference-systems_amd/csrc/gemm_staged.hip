@@ -451,8 +451,11 @@ int launch_tile(const Problem& p, hipStream_t s) {
 //   * tiles <= 128 (half the CUs): 64 x 64 tiles, four times the workgroups
 //     (1024^3 11.7 -> 6.8 us, 512 x 4096 x 1024 12.3 -> 8.1 us,
 //     2048 x 1024 x 2048 20.6 -> 13.8 us, 512 x 1024 x 3584 33.0 -> 17.0 us),
-//     with a 3-deep ring from K = 2048 (2048 x 1024 x 2048: 13.8 us against
-//     14.1; 512 x 1024 x 3584: 17.0 against 27.3);
+//     on a 3-deep ring with spread copies (against a 2-deep burst ring:
+//     1024^3 6.85 -> 6.57 us, 512 x 4096 x 1024 8.49 -> 8.04, 256 x 6144 x
+//     1024 8.03 -> 7.46, 2048 x 1024 x 2048 14.2 -> 14.0, 512 x 1024 x 3584
+//     27.3 -> 17.2); SiLU pairs take 64 x 128 with a 3-deep ring from
+//     K = 2048;
 //   * 128 < wide <= 256 or wide > 384: one 8-wave workgroup per CU on
 //     128 x 256 (half the A reads of two 128 x 128 tiles), 3-deep ring,
 //     copies spread between the MFMAs.  Against the 2-deep 128 x 128 burst
@@ -480,8 +483,7 @@ int launch_epi(const Problem& p, hipStream_t s) {
     if (tiles <= kSmallGridTiles) {
         const bool deep = p.k >= 2048;
         if constexpr (EPI == EPI_NONE) {
-            if (deep) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI, RS, 0>(p, s);
-            return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 2, EPI, RS, 0>(p, s);
+            return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI, RS, 1>(p, s);
         } else if constexpr (EPI == EPI_SILU_MUL) {
             // gate/up pairs need two 32-row W blocks per wave
             if (deep) return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS, 0>(p, s);

@@ -182,7 +182,7 @@ STAGED_GRIDS = [(600, 1000, 1000), (600, 1000, 2056), (1100, 2000, 1000), (2100,
                          ids=["bf16", "f16-f32"])
 def test_staged_ring_depths_ragged(m, n, k, din, dout):
     """mfma_staged's tile choices: a grid of at most 128 tiles of 128 x 128
-    takes 64 x 64 tiles (3-deep ring from K = 2048); up to 256 tiles 128 x
+    takes 64 x 64 tiles (3-deep ring, spread copies); up to 256 tiles 128 x
     128 with the spread 3-deep ring; above that 128 x 256 tiles (8 waves,
     3-deep ring, copies spread between the MFMAs) unless there are 257-384
     of those, where 128 x 128 with a 2-deep ring takes over; each on ragged
