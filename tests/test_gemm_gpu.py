@@ -714,3 +714,19 @@ def test_sample_offsets_and_graph_replay():
         t_eager, s_eager = G.gemm_sample(a, w, temps, 1, 7)
         torch.cuda.synchronize()
         assert torch.equal(t_static, t_eager) and torch.equal(s_static, s_eager), f"replay {step}"
+
+
+@pytest.mark.parametrize("k", [8, 520, 1024, 1032, 2056, 3584])
+def test_gemv_load_unrolls(k):
+    """gemv_decode issues 1, 2 or 4 loads per lane together depending on K
+    (one per 512-element slice of a row, up to 4); every choice sums in the
+    same order and meets the bar, including K that leaves the last trip
+    partly empty."""
+    n = 777
+    gen = torch.Generator().manual_seed(k)
+    a = torch.randn((1, k), generator=gen).bfloat16()
+    w = (torch.randn((n, k), generator=gen) * 0.1).bfloat16()
+    _say(f"gemv unroll K={k}")
+    out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_GEMV_DECODE, torch.bfloat16)
+    torch.cuda.synchronize()
+    _check_tolerance(out.cpu(), a, w, L.B_NK, torch.bfloat16)
