@@ -3,10 +3,13 @@
 
 Headline: the BF16 prefill projection C[2048,4096] = A[2048,1024] W[4096,1024]^T
 (bf16 out, fp32 accumulate) on the kernel the selection table picks.  A step
-is one GEMM over resident inputs; K steps are captured back to back in one
-HIP graph (launch gaps of the host excluded, as the reference's adaptive
-repeat loop of cuda_kernels/gemm/src/gemm_bench.cu:198-223 excludes them)
-and timed with HIP events on the stream they run on.
+is one GEMM over resident inputs.  The K timed steps are launched back to
+back on one stream and timed with HIP events on that stream, the pattern of
+the reference's benchmark_ms (cuda_kernels/gemm/src/gemm_bench.cu:198-223);
+the same K steps replayed as one HIP graph are reported beside them.  For the
+short bandwidth-bound workloads (``--workload`` with a decode shape, and the
+decode rows below) the graph replay is the measure, so host launch gaps are
+excluded, and plain stream launches are reported beside it.
 
 Alongside (extra keys of the same JSON line): the decode GEMMs M in
 {1,4,8,16,32} x N=6144 x K=1024 with W rotated over more than twice the
@@ -104,10 +107,35 @@ class GraphTimer:
         return start.elapsed_time(end)
 
 
+def median_plain_ms(torch, launches, trials=5) -> float:
+    """Median over trials of (time / launches) for the same launches issued
+    one by one on the stream, without a graph (host launch cost included)."""
+    for f in launches[:4]:
+        f()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(trials):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for f in launches:
+            f()
+        end.record()
+        torch.cuda.synchronize()
+        samples.append(start.elapsed_time(end) / len(launches))
+    return sorted(samples)[len(samples) // 2]
+
+
+RAMP_MS = 30.0   # GPU time replayed before the trials of an extra row
+
+
 def median_graph_ms(torch, launches, trials=5) -> float:
-    """Median over trials of (graph replay time / launches), in ms."""
+    """Median over trials of (graph replay time / launches), in ms.  The
+    graph is replayed for RAMP_MS first: capture leaves the GPU idle, and
+    the clocks of an idle MI355X drop."""
     timer = GraphTimer(torch, launches)
-    timer.time_ms()
+    ramp = 0.0
+    while ramp < RAMP_MS:
+        ramp += timer.time_ms()
     samples = sorted(timer.time_ms() / len(launches) for _ in range(trials))
     return samples[len(samples) // 2]
 
@@ -184,27 +212,55 @@ def main() -> int:
     launches = [launcher(a, ws_h[i % copies], out, m, n, k, wl.b_layout, wl.dtype_in, wl.dtype_out)
                 for i in range(copies)]
     log(f"headline {name} M={m}: kernel {kernel}, W buffers {copies}, warmup {args.warmup}, steps {args.steps}")
+    # Graphs are captured first: capture is host work that leaves the GPU
+    # idle, and an idle MI355X drops its clocks.
+    steps = [launches[i % copies] for i in range(args.steps)]
+    timer = GraphTimer(torch, steps)
+    warm_graph = GraphTimer(torch, steps[:args.warmup]) if args.warmup > 0 and wl.bound != "mfma" else None
     # Device warm-up: MI355X clocks ramp over the first ~0.1-0.2 s of load
     # (the same kernel measured 10% slower in its first 100 launches), so run
-    # the kernel for DEVICE_WARMUP_S before the warm-up steps.  Untimed.
+    # the kernel for DEVICE_WARMUP_S right before the warm-up steps.  Untimed.
     ramp = GraphTimer(torch, [launches[i % copies] for i in range(200)])
     t_ramp = 0.0
     while t_ramp < DEVICE_WARMUP_S * 1e3:
         t_ramp += ramp.time_ms()
     del ramp
-    if args.warmup > 0:
-        GraphTimer(torch, [launches[i % copies] for i in range(args.warmup)]).time_ms()
-    timer = GraphTimer(torch, [launches[i % copies] for i in range(args.steps)])
-    torch.cuda.synchronize()
-    elapsed_ms = timer.time_ms()
-    torch.cuda.synchronize()
+    if wl.bound == "mfma":
+        # Kernels of ~10 us and more: K launches issued back to back on the
+        # stream and timed with HIP events, the pattern of the reference's
+        # benchmark_ms (gemm_bench.cu:198-223); the graph replay of the same
+        # K launches is reported beside it.
+        for f in steps[:args.warmup]:
+            f()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for f in steps:
+            f()
+        end.record()
+        torch.cuda.synchronize()
+        elapsed_ms = start.elapsed_time(end)
+        other_ms = timer.time_ms() / args.steps
+        timing = "K launches back to back on one stream, HIP events; graph_ms_per_step: the same K in one HIP graph"
+    else:
+        # Short, bandwidth-bound kernels: the K launches replayed as one HIP
+        # graph, so host launch gaps are excluded; plain stream launches
+        # reported beside.
+        if warm_graph is not None:
+            warm_graph.time_ms()
+        torch.cuda.synchronize()
+        elapsed_ms = timer.time_ms()
+        torch.cuda.synchronize()
+        other_ms = median_plain_ms(torch, steps[:200], trials=3)
+        timing = "K launches back to back in one HIP graph, HIP events; plain_launch_ms_per_step: stream launches"
     ms_per_step = elapsed_ms / args.steps
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_MFMA_TFLOPS[dname[wl.dtype_in]]
     byts = W.problem_bytes(m, n, k, wl.dtype_in, wl.dtype_out)
     gbs = byts / (ms_per_step * 1e-3) / 1e9
     log(f"  {ms_per_step * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  {100 * tflops / peak:.1f}% of {peak} TFLOP/s  "
-        f"{gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM")
+        f"{gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM  ({timing.split(';')[0]}; "
+        f"{'graph' if wl.bound == 'mfma' else 'plain'}: {other_ms * 1e3:.2f} us/step)")
     if wl.bound == "hbm":
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4)}
@@ -222,6 +278,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_per_step,
+        ("graph_ms_per_step" if wl.bound == "mfma" else "plain_launch_ms_per_step"): round(other_ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -231,7 +288,7 @@ def main() -> int:
                    "b_layout": "W[N,K]" if wl.b_layout == L.B_NK else "B[K,N]",
                    "out_dtype": dname[wl.dtype_out], "kernel": kernel,
                    "w_buffers": copies, "device_warmup_s": DEVICE_WARMUP_S,
-                   "timing": "K launches back to back in one HIP graph, HIP events"},
+                   "timing": timing},
         "roofline": roof,
     }
 
@@ -251,12 +308,15 @@ def main() -> int:
             launches = [launcher(a_d, ws[i % copies], o_d, dm, dw.n, dw.k, L.B_NK, dw.dtype_in, dw.dtype_out)
                         for i in range(copies * 10)]
             t_ms = median_graph_ms(torch, launches)
+            t_plain = median_plain_ms(torch, launches)
             byts = W.problem_bytes(dm, dw.n, dw.k, dw.dtype_in, dw.dtype_out)
             gbs = byts / (t_ms * 1e-3) / 1e9
             kd = L.kernel_name(L.select(dm, dw.n, dw.k, dw.k, dw.k, dw.n, L.B_NK, L.BF16, L.BF16, True))
             rows.append({"m": dm, "us": round(t_ms * 1e3, 3), "GB/s": round(gbs, 1),
-                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": kd, "w_buffers": copies})
-            log(f"decode M={dm:2d}: {t_ms * 1e3:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM ({kd})")
+                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": kd, "w_buffers": copies,
+                         "plain_launch_us": round(t_plain * 1e3, 3)})
+            log(f"decode M={dm:2d}: {t_ms * 1e3:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM ({kd}); "
+                f"plain stream launches {t_plain * 1e3:.2f} us")
         extras["decode_bf16_n6144_k1024"] = rows
         del ws
 
