@@ -57,6 +57,8 @@ constexpr int kT32Threads = 512;        // 8 waves: two groups of 4 (2 x 2 over 
 constexpr int kT32VecLoads = kT32BM * kT32Cpr / kT32Threads;     // 16-byte loads per operand per thread
 constexpr int kT32ScalarLoads = kT32BM * kT32BK / kT32Threads;   // 4-byte loads per operand per thread
 static_assert(kT32BM == 64 && kT32BN == 64, "B[K,N] tiles are read as rows of 64 floats");
+static_assert(kT32VecLoads == 2 && kT32Threads == 512, "B[K,N]: one 2 x 4 block of the 64 x 64 tile per thread");
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 template <int BL, int VEC>
 __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
@@ -115,7 +117,8 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
                     const int64_t gn = n0 + e / kT32Cpr, gk = k0 + 4 * (e % kT32Cpr);
                     vb[S][r] = *reinterpret_cast<const f32x4_t*>(b + min_i64(gn, n - 1) * ldb + min_i64(gk, k - 4));
                 } else {
-                    const int64_t gn = n0 + 4 * (e & 15), gk = k0 + (e >> 4);   // B[K,N]: 16 chunks of 4 n per k row
+                    // B[K,N]: thread t takes 4 columns (t % 16) of rows 2 (t / 16) and 2 (t / 16) + 1.
+                    const int64_t gn = n0 + 4 * (tid & 15), gk = k0 + 2 * (tid >> 4) + r;
                     vb[S][r] = *reinterpret_cast<const f32x4_t*>(b + min_i64(gk, k - 1) * ldb + min_i64(gn, n - 4));
                 }
             }
@@ -146,11 +149,16 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
                 if constexpr (BL == NANOVLLM_GEMM_B_NK) {
                     const bool in_b = n0 + row < n && k0 + 4 * kq < k;
                     *reinterpret_cast<f32x4_t*>(&Bs[buf][row][4 * kq]) = in_b ? vb[S][r] : z4;
-                } else {
-                    const int kk = e >> 4, nq = e & 15;
-                    const bool in_b = n0 + 4 * nq < n && k0 + kk < k;
+                } else if (r == 1) {
+                    // The thread's 2 x 4 block of B[K,N], transposed into 4
+                    // pairs of consecutive k (one 8-byte write each).
+                    const int nq = tid & 15, kp = tid >> 4;
+                    const bool in_n = n0 + 4 * nq < n;
+                    const bool in0 = in_n && k0 + 2 * kp < k, in1 = in_n && k0 + 2 * kp + 1 < k;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) Bs[buf][4 * nq + q][kk] = in_b ? vb[S][r][q] : 0.0f;
+                    for (int q = 0; q < 4; ++q)
+                        *reinterpret_cast<f32x2_t*>(&Bs[buf][4 * nq + q][2 * kp]) =
+                            f32x2_t{in0 ? vb[S][0][q] : 0.0f, in1 ? vb[S][1][q] : 0.0f};
                 }
             }
         } else {
