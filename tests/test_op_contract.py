@@ -69,3 +69,30 @@ def test_linear_backends_on_cpu_tensors():
         G.linear(x, w, b, backend="hip")
     out = G.linear(x.bfloat16(), w.bfloat16(), None, out_dtype=torch.float32, backend="torch")
     assert out.dtype == torch.float32
+
+
+def test_sample_op_registered_and_fake_shapes():
+    """nanovllm::gemm_sample: registered with (a, w, temperatures, seed,
+    offset) and a meta implementation giving (int64 tokens, fp32 scores)
+    over the leading dims of a."""
+    schema = str(torch.ops.nanovllm.gemm_sample.default._schema)
+    assert "Tensor temperatures" in schema and "seed" in schema and "offset" in schema
+    a = torch.empty((2, 3, 64), dtype=torch.bfloat16, device="meta")
+    w = torch.empty((500, 64), dtype=torch.bfloat16, device="meta")
+    t = torch.empty((2, 3), dtype=torch.float32, device="meta")
+    tokens, scores = torch.ops.nanovllm.gemm_sample(a, w, t, 1, 2)
+    assert tokens.shape == (2, 3) and tokens.dtype == torch.int64
+    assert scores.shape == (2, 3) and scores.dtype == torch.float32
+
+
+def test_sample_contract_reasons_and_backends():
+    """The sampled head's contract on CPU tensors, and sample_linear's torch
+    backend (the reference Sampler on F.linear's logits)."""
+    a = torch.randn(4, 16, dtype=torch.bfloat16)
+    w = torch.randn(10, 16, dtype=torch.bfloat16)
+    t = torch.zeros(4)
+    assert G.sample_contract_reason(a, w, t) == "a and w must be CUDA (HIP) tensors"
+    tokens, scores = G.sample_linear(a, w, t, 1, 2, backend="auto")
+    assert scores is None and torch.equal(tokens, F.linear(a, w).float().argmax(-1))
+    with pytest.raises(RuntimeError, match="HIP GEMM backend is unavailable"):
+        G.sample_linear(a, w, t, 1, 2, backend="hip")
