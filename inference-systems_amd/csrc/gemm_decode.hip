@@ -183,7 +183,6 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                     const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
                     if (line >= lines) break;
                     uint16_t* lh = reinterpret_cast<uint16_t*>(&buf[wave][t * IL * 64]);
-#pragma unroll
                     for (int r = 0; r < AROWS; ++r) {
                         if (r >= m) break;
                         const int r8v = r & 7;
