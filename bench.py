@@ -21,7 +21,10 @@ LM head, the gated-attention output gate before o_proj, the residual add +
 RMSNorm before a projection), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
 for comparison only, and the CPU baseline (host F.linear, multi-threaded).
 
-Prints ONE JSON line on stdout; a readable table goes to stderr.
+Prints ONE JSON line on stdout; a readable table goes to stderr.  With
+``--matrix`` it instead runs the reference's own shape matrix (its Qwen3.5
+shapes in fp16 and bf16, deterministic inputs, fp32 output) and prints it
+as CSV, one row per shape in the columns of the reference's results file.
 """
 from __future__ import annotations
 
@@ -61,6 +64,9 @@ def parse_args():
     p.add_argument("--m", type=int, default=None, help="M of --workload (default: its largest)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run 10 device copies of MIB MiB (reference kernel for HBM counter scaling)")
+    p.add_argument("--matrix", action="store_true",
+                   help="only run the reference's shape matrix (fp16 and bf16 over its Qwen3.5 shapes) and print "
+                        "it as CSV")
     return p.parse_args()
 
 
@@ -154,6 +160,129 @@ def read_traffic():
     return None
 
 
+def benchmark_ms(torch, launch, warmup: int, repeats: int, trials: int = 7) -> tuple:
+    """The reference's benchmark_ms (cuda_kernels/gemm/src/gemm_bench.cu:198-223):
+    `warmup` launches, then the median over `trials` of (event time of
+    `repeats` back-to-back launches) / repeats.  Returns (graph, plain):
+    the same `repeats` launches replayed as one HIP graph (after a clock
+    ramp; host launch cost excluded), and issued one by one from Python."""
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(trials):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            launch()
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end) / repeats)
+    samples.sort()
+    plain = samples[len(samples) // 2]
+    timer = GraphTimer(torch, [launch] * repeats)
+    ramp = 0.0
+    while ramp < RAMP_MS:
+        ramp += timer.time_ms()
+    graph = sorted(timer.time_ms() / repeats for _ in range(trials))[trials // 2]
+    return graph, plain
+
+
+def reference_matrix(torch, L, W) -> int:
+    """The reference's GEMM benchmark matrix on this GPU, one CSV row per
+    (dtype, shape) as run_shape writes it (gemm_bench.cu:284-450,
+    results/rtx3060_gemm_matrix.csv):
+
+    * inputs from the reference's deterministic generators
+      (gemm_bench.cu:296-305), A[M,K] and B[K,N] row-major, fp32 output;
+      every product and partial sum of these inputs is exact in fp32, so
+      the expected C is the same for any summation order;
+    * the vendor column is torch's GPU GEMM (hipBLASLt / rocBLAS) with fp32
+      output in place of cuBLAS, timed for comparison only;
+    * every output is compared to the exact product (an fp64 GEMM, exact on
+      these inputs) as compare does: max |error|, and pass if every error is
+      within 5e-2 + 1e-2 |ref| and finite (gemm_bench.cu:225-250);
+    * direct_* is mfma_direct on the reference's B[K,N] layout, staged_*
+      mfma_staged and dispatch_* the kernel the selection table picks, both
+      on the same matrix in the W[N,K] (nn.Linear) layout the library's
+      fast kernels read;
+    * timing as benchmark_ms: 10 warm-up launches, repeats =
+      clamp(2e10 / flops, 10, 200), median of 7 trials (gemm_bench.cu:371-379),
+      each group of repeats replayed as one HIP graph (these kernels run for
+      a few microseconds, less than a Python launch takes); the last column
+      gives the selected kernel's time with plain launches from Python.
+    """
+    dev = torch.device("cuda:0")
+    code = {torch.float16: L.F16, torch.bfloat16: L.BF16}
+    cols = ["dtype", "label", "M", "N", "K", "repeats", "vendor_ms", "vendor_tflops", "direct_ms", "direct_tflops",
+            "staged_ms", "staged_tflops", "vendor_max_abs", "direct_max_abs", "staged_max_abs", "dispatch",
+            "dispatch_ms", "dispatch_tflops", "dispatch_max_abs", "dispatch_vs_vendor", "status",
+            "dispatch_plain_launch_ms"]
+    print(",".join(cols), flush=True)
+    all_ok = True
+    for dt, dname in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        for label, m, n, k in W.QWEN35_SHAPES:
+            ia = torch.arange(m * k, dtype=torch.int64)
+            ib = torch.arange(k * n, dtype=torch.int64)
+            a = (((ia * 17 + 3) % 31 - 15).to(torch.float32) * 0.03125).reshape(m, k).to(dt).to(dev)
+            b = (((ib * 11 + 5) % 29 - 14).to(torch.float32) * 0.03125).reshape(k, n).to(dt).to(dev)
+            w = b.t().contiguous()
+            flops = 2.0 * m * n * k
+            repeats = min(max(int(2.0e10 / max(flops, 1.0)), 10), 200)
+            ref = torch.empty(m, n, dtype=torch.float32, device=dev)
+            out = torch.empty(m, n, dtype=torch.float32, device=dev)
+
+            expect = torch.mm(a.double(), b.double()).float()
+
+            def vendor():
+                torch.mm(a, b, out_dtype=torch.float32, out=ref)
+
+            def ours(bt, layout, kernel=None):
+                ldb = k if layout == L.B_NK else n
+                args_ = (bt.data_ptr(), m, n, k, k, ldb, n, layout, code[dt], L.F32)
+
+                def f():
+                    L.gemm_raw(a.data_ptr(), args_[0], out.data_ptr(), *args_[1:],
+                               torch.cuda.current_stream().cuda_stream, kernel=kernel)
+                return f
+
+            ok = True
+
+            def run(f, dst):
+                nonlocal ok
+                t, t_plain = benchmark_ms(torch, f, 10, repeats)
+                dst.fill_(float("nan"))
+                f()
+                torch.cuda.synchronize()
+                err = (dst.double() - expect.double()).abs()
+                good = bool(torch.isfinite(dst).all()) and bool((err <= 5e-2 + 1e-2 * expect.double().abs()).all())
+                ok = ok and good
+                return t, float(err.max()), t_plain
+
+            try:
+                vendor()
+                vendor_ms, vendor_err, _ = run(vendor, ref)
+            except RuntimeError:   # no fp32-output half GEMM in this torch build: comparison column left empty
+                vendor_ms = vendor_err = float("nan")
+            direct_ms, direct_err, _ = run(ours(b, L.B_KN, L.KERNEL_MFMA_DIRECT), out)
+            staged_ms, staged_err, _ = run(ours(w, L.B_NK, L.KERNEL_MFMA_STAGED), out)
+            sel = L.select(m, n, k, k, k, n, L.B_NK, code[dt], L.F32)
+            disp_ms, disp_err, disp_plain = run(ours(w, L.B_NK), out)
+            all_ok = all_ok and ok
+
+            def tf(ms):
+                return flops / (ms * 1e9)
+            row = [dname, label, m, n, k, repeats, f"{vendor_ms:.6f}", f"{tf(vendor_ms):.6f}", f"{direct_ms:.6f}",
+                   f"{tf(direct_ms):.6f}", f"{staged_ms:.6f}", f"{tf(staged_ms):.6f}", f"{vendor_err:.6f}",
+                   f"{direct_err:.6f}",
+                   f"{staged_err:.6f}", L.kernel_name(sel), f"{disp_ms:.6f}", f"{tf(disp_ms):.6f}",
+                   f"{disp_err:.6f}", f"{vendor_ms / disp_ms:.6f}", "PASS" if ok else "FAIL", f"{disp_plain:.6f}"]
+            print(",".join("NA" if x == "nan" else str(x) for x in row), flush=True)
+            del a, b, w, ref, out, expect
+            torch.cuda.empty_cache()
+    return 0 if all_ok else 1
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -174,6 +303,9 @@ def main() -> int:
     L = pkg._lib
     L.load()                      # raises if the HIP library is not built
     W = pkg.workloads
+    if args.matrix:
+        torch.cuda.set_device(0)
+        return reference_matrix(torch, L, W)
     K_ops = pkg.kernels
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

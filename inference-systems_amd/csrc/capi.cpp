@@ -61,7 +61,23 @@ bool vector_ok(int64_t k, int64_t lda, int64_t ldb, int b_layout, int aligned16)
 // ~312 flop/byte bf16 ridge of MI355X).
 constexpr int64_t kDecodeMaxM = 32;
 
-bool supports(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldb, int b_layout, int din,
+// The plain GEMM also runs on splitk_decode up to M = 64 when W has fewer
+// than 65536 rows.  The table picks it there for narrow problems, where
+// mfma_staged's 64 x 64 tiles leave most CUs idle (bf16, M = 64: N = 1024,
+// K = 3584 6.5 against 15.5 us; N = 4096, K = 4096 10.0 against 19.0 us;
+// N = 8224, K = 1024 5.7 against 6.2 us), and not from 16384 rows or, above
+// 4096 rows, beyond K = 1024 (N = 12288, K = 2048: 14.3 against 11.6 us).
+constexpr int64_t kSplitkPlainMaxM = 64;
+constexpr int64_t kSplitkPlainMaxRows = 65535;
+constexpr int64_t kSplitkPlainNarrowN = 4096;
+constexpr int64_t kSplitkPlainShortKMaxN = 10240;
+constexpr int64_t kSplitkPlainShortK = 1024;
+
+bool splitk_plain_ok(int64_t m, int64_t n) {
+    return m <= kDecodeMaxM || (m <= kSplitkPlainMaxM && n <= kSplitkPlainMaxRows);
+}
+
+bool supports(int kernel_id, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_layout, int din,
               int aligned16) {
     switch (kernel_id) {
         case NANOVLLM_GEMM_KERNEL_FP32_NAIVE:
@@ -69,7 +85,7 @@ bool supports(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldb, int
         case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return is_half(din);
         case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16);
         case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE:
-            return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && m <= kDecodeMaxM;
+            return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && splitk_plain_ok(m, n);
         case NANOVLLM_GEMM_KERNEL_GEMV_DECODE:
             return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && m == 1;
         default: return false;
@@ -90,6 +106,9 @@ int select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_layo
     if (vector_ok(k, lda, ldb, b_layout, aligned16)) {
         if (m == 1 && n * k * 2 <= kGemvMaxWBytes) return NANOVLLM_GEMM_KERNEL_GEMV_DECODE;
         if (m <= kDecodeMaxM) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+        if (m <= kSplitkPlainMaxM &&
+            (n <= kSplitkPlainNarrowN || (n <= kSplitkPlainShortKMaxN && k <= kSplitkPlainShortK)))
+            return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
         return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
     }
     return NANOVLLM_GEMM_KERNEL_MFMA_DIRECT;
@@ -125,7 +144,7 @@ int gemm_entry(int forced_kernel, const void* a, const void* b, void* c, int64_t
         kernel = select(m, n, k, lda, ldb, b_layout, din, al);
     } else if (kernel >= NANOVLLM_GEMM_KERNEL_COUNT) {
         return set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel);
-    } else if (!supports(kernel, m, k, lda, ldb, b_layout, din, al)) {
+    } else if (!supports(kernel, m, n, k, lda, ldb, b_layout, din, al)) {
         return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "kernel %s cannot run this problem (m=%lld n=%lld k=%lld)",
                          nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);
     }
@@ -389,7 +408,7 @@ int gated_entry(int forced_kernel, const void* a, const void* gate, const void* 
                          "this problem needs a 16-byte aligned workspace of %lld bytes (got %lld)", (long long)need,
                          (long long)workspace_bytes);
     int kernel = forced_kernel < 0 ? select(m, n, k, k, ldw, NANOVLLM_GEMM_B_NK, din, 1) : forced_kernel;
-    if (forced_kernel >= NANOVLLM_GEMM_KERNEL_COUNT || !supports(kernel, m, k, k, ldw, NANOVLLM_GEMM_B_NK, din, 1))
+    if (forced_kernel >= NANOVLLM_GEMM_KERNEL_COUNT || !supports(kernel, m, n, k, k, ldw, NANOVLLM_GEMM_B_NK, din, 1))
         return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "kernel %s cannot run the gated GEMM (m=%lld n=%lld k=%lld)",
                          nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);
     rc = launch_gate_prologue(a, lda, gate, ldg, group, group_stride, workspace, k, m, k, din, s);
@@ -519,7 +538,7 @@ int nanovllm_gemm_kernel_supports(int kernel_id, int64_t m, int64_t n, int64_t k
                                   int64_t ldc, int b_layout, int dtype_in, int dtype_out, int aligned16) {
     nvg::g_last_error.clear();
     if (nvg::validate(m, n, k, lda, ldb, ldc, b_layout, dtype_in, dtype_out) != NANOVLLM_GEMM_OK) return 0;
-    return nvg::supports(kernel_id, m, k, lda, ldb, b_layout, dtype_in, aligned16) ? 1 : 0;
+    return nvg::supports(kernel_id, m, n, k, lda, ldb, b_layout, dtype_in, aligned16) ? 1 : 0;
 }
 
 const char* nanovllm_gemm_kernel_name(int kernel_id) {
@@ -694,6 +713,6 @@ int nanovllm_gemm_add_rmsnorm_with_kernel(int kernel_id, const void* h, const vo
 
 const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
 
-int nanovllm_gemm_version(void) { return (1 << 16) | 4; }
+int nanovllm_gemm_version(void) { return (1 << 16) | 5; }
 
 }  // extern "C"

@@ -1,7 +1,7 @@
-// splitk_decode: the bandwidth-bound small-M GEMM (M <= 32), C = A * W^T
-// with W[N,K] in the nn.Linear layout.  At these shapes the work is
-// streaming W once from HBM (N*K*2 bytes) while A (M*K*2 bytes, at most
-// 64 KiB) stays in L2.  Design:
+// splitk_decode: the bandwidth-bound small-M GEMM (M <= 32, and the plain
+// GEMM up to M = 64), C = A * W^T with W[N,K] in the nn.Linear layout.  At
+// these shapes the work is streaming W once from HBM (N*K*2 bytes) while A
+// (M*K*2 bytes) stays in L2.  Design:
 //   * one workgroup per 16 * RG rows of W; its waves split K, taking
 //     64-element lines (128 bytes of a row) round robin, LPB lines at a time;
 //   * W and A reach LDS by global_load_lds_dwordx4 in whole 128-byte lines:
@@ -48,7 +48,7 @@ struct ProArgs {
 };
 
 // RG groups of 16 W rows per workgroup, AROWS rows of A copied per line
-// (8, 16 or 32: M rounded up), WAVES waves splitting K, LPB lines per wave
+// (8, 16, 32 or 64: M rounded up), WAVES waves splitting K, LPB lines per wave
 // in flight at once, PARTS K partitions (a multiple of WAVES), PRO the
 // prologue on A.
 template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO>
@@ -56,8 +56,8 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
     ProArgs pro, SampleArgs sa) {
-    static_assert(AROWS == 8 || AROWS == 16 || AROWS == 32, "rows of A per line");
-    constexpr int MG = AROWS == 32 ? 2 : 1;   // 16-row groups of A in the MFMA
+    static_assert(AROWS == 8 || AROWS == 16 || AROWS == 32 || AROWS == 64, "rows of A per line");
+    constexpr int MG = AROWS == 8 ? 1 : AROWS / 16;   // 16-row groups of A in the MFMA
     constexpr int IW = 2 * RG;                 // W copies per line (8 rows each)
     constexpr int IA = AROWS / 8;              // A copies per line
     constexpr int IP = PRO == PRO_NONE ? 0 : IA;   // gate or residual copies per line
@@ -440,8 +440,8 @@ int launch_cfg(const Problem& p, hipStream_t s) {
     return check_launch("splitk_decode");
 }
 
-// Configurations measured on MI355X.  AROWS is M rounded up to 8, 16 or 32;
-// "rows" counts the W rows read (2 N for SiLU-and-mul).
+// Configurations measured on MI355X.  AROWS is M rounded up to 8, 16, 32 or
+// 64; "rows" counts the W rows read (2 N for SiLU-and-mul).
 //   * rows < 65536: 32 W rows per 8-wave workgroup, one line per wave in
 //     flight; N = 6144, K = 1024, M = 1 / 4 / 8 / 16 / 32: 4.42 / 4.48 /
 //     4.62 / 4.96 / 5.99 us (the register-loading kernel: 4.91 / 5.15 /
@@ -453,8 +453,26 @@ int launch_cfg(const Problem& p, hipStream_t s) {
 //     register-loading kernel (48.4 us; with a prologue, the M <= 8
 //     configuration); M = 8 / 16 / 32: 53.5 / 57.5 / 63.9 us (61.2 / 65.7 /
 //     75.8 us with register loading).
+//   * 33 <= M <= 64 (the plain GEMM only, below 65536 rows): A's copies now
+//     outweigh W's, so 8 waves and 8 K partitions in every configuration,
+//     16 / 32 / 48 rows per workgroup up to 4096 / 8192 / 65535 rows.
+//     Against mfma_staged, whose 64 x 64 tiles leave most CUs idle on these
+//     grids (bf16, M = 64, K = 1024 unless given): N = 1024 3.6 against
+//     5.9 us, 1024 x K 3584 6.5 / 15.5, 2048 x K 2048 4.8 / 9.7, 3584 3.8 /
+//     6.0, 4096 x K 4096 10.0 / 19.0, 6144 4.6 / 6.0, 8224 5.7 / 6.2; from
+//     16384 rows mfma_staged's larger grid wins (7.1 against 9.9 us), and
+//     the selection table sends M > 32 there.
 // A prologue adds its own copies per line to the same configurations.
 constexpr int64_t kWideN = 65536;
+
+// 33 <= M <= 64, the plain GEMM below 65536 rows.
+template <int DT, int DT_OUT>
+int launch_rows64(const Problem& p, hipStream_t s) {
+    if (p.n >= kWideN) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M > 32 needs N < 65536");
+    if (p.n <= 4096) return launch_cfg<DT, DT_OUT, 64, 1, 8, 1, 8, EPI_NONE>(p, s);
+    if (p.n <= 8192) return launch_cfg<DT, DT_OUT, 64, 2, 8, 1, 8, EPI_NONE>(p, s);
+    return launch_cfg<DT, DT_OUT, 64, 3, 8, 1, 8, EPI_NONE>(p, s);
+}
 
 template <int DT, int DT_OUT, int EPI, int AROWS, int PRO>
 int launch_rows(const Problem& p, hipStream_t s) {
@@ -479,7 +497,10 @@ template <int DT, int DT_OUT, int EPI, int PRO = PRO_NONE>
 int launch_epi(const Problem& p, hipStream_t s) {
     if (p.m <= 8) return launch_rows<DT, DT_OUT, EPI, 8, PRO>(p, s);
     if (p.m <= 16) return launch_rows<DT, DT_OUT, EPI, 16, PRO>(p, s);
-    return launch_rows<DT, DT_OUT, EPI, 32, PRO>(p, s);
+    if (p.m <= 32) return launch_rows<DT, DT_OUT, EPI, 32, PRO>(p, s);
+    if constexpr (EPI == EPI_NONE && PRO == PRO_NONE)
+        if (p.m <= 64) return launch_rows64<DT, DT_OUT>(p, s);
+    return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above its limit");
 }
 
 template <int DT, int DT_OUT>

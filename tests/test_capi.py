@@ -81,15 +81,21 @@ def test_gemm_validates_before_launch(lib):
 
 
 def test_gemm_with_kernel_refuses_unsupported_rung(lib):
-    # fp32_tiled cannot take bf16; splitk_decode cannot take M = 64; the check
-    # happens before any launch (pointers are dummies never dereferenced).
+    # fp32_tiled cannot take bf16; splitk_decode cannot take M = 65, nor
+    # M = 33 with 65536 W rows; the check happens before any launch (pointers
+    # are dummies never dereferenced).
     dummy = 1 << 20
     rc = lib.nanovllm_gemm_with_kernel(L.KERNEL_FP32_TILED, dummy, dummy, dummy, 4, 4, 8, 8, 8, 4, NK, BF16, BF16,
                                        None)
     assert rc == L.EUNSUPPORTED and "fp32_tiled" in L.last_error()
-    rc = lib.nanovllm_gemm_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, 64, 64, 64, 64, 64, 64, NK,
+    rc = lib.nanovllm_gemm_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, 65, 64, 64, 64, 64, 64, NK,
                                        BF16, BF16, None)
     assert rc == L.EUNSUPPORTED
+    rc = lib.nanovllm_gemm_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, 33, 65536, 64, 64, 64, 65536,
+                                       NK, BF16, BF16, None)
+    assert rc == L.EUNSUPPORTED
+    assert L.kernel_supports(L.KERNEL_SPLITK_DECODE, 64, 65535, 64, 64, 64, 65535, NK, BF16, BF16, 1)
+    assert L.kernel_supports(L.KERNEL_SPLITK_DECODE, 32, 151936, 64, 64, 64, 151936, NK, BF16, BF16, 1)
 
 
 def _expected(m, n, k, lda, ldb, layout, din, aligned):
@@ -99,7 +105,12 @@ def _expected(m, n, k, lda, ldb, layout, din, aligned):
     if vec:
         if m == 1 and n * k * 2 <= 64 * 2 ** 20:
             return L.KERNEL_GEMV_DECODE
-        return L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
+        if m <= 32:
+            return L.KERNEL_SPLITK_DECODE
+        # 33 <= M <= 64: narrow problems stream W on splitk_decode as well
+        if m <= 64 and (n <= 4096 or (n <= 10240 and k <= 1024)):
+            return L.KERNEL_SPLITK_DECODE
+        return L.KERNEL_MFMA_STAGED
     return L.KERNEL_MFMA_DIRECT
 
 
@@ -110,9 +121,9 @@ PAIRS = [(F32, F32), (F16, F16), (F16, F32), (BF16, BF16), (BF16, F32)]
 def test_selection_table_total_and_self_consistent(din, dout):
     """Every valid problem maps to one of this library's kernels, that kernel
     supports it, and the table follows its stated rule."""
-    ms = [0, 1, 4, 16, 31, 32, 33, 64, 127, 2048]
-    ns = [1, 15, 193, 4096, 151936]
-    ks = [1, 7, 8, 65, 1024, 3584]
+    ms = [0, 1, 4, 16, 31, 32, 33, 48, 64, 65, 127, 2048]
+    ns = [1, 15, 193, 4096, 4097, 8224, 10240, 10241, 151936]
+    ks = [1, 7, 8, 65, 1024, 1032, 3584]
     for m, n, k, layout, aligned, pad in itertools.product(ms, ns, ks, (NK, KN), (0, 1), (0, 3)):
         lda = k + pad
         ldb = (k if layout == NK else n) + pad
@@ -141,7 +152,7 @@ def test_selection_on_workloads_and_qwen_shapes():
             assert L.kernel_name(kid) == want[name][m], (name, m)
     for label, m, n, k in W.QWEN35_SHAPES:
         kid = L.select(m, n, k, k, k, n, NK, BF16, BF16, 1)
-        want_k = "gemv_decode" if m == 1 else ("splitk_decode" if m <= 32 else "mfma_staged")
+        want_k = "gemv_decode" if m == 1 else ("splitk_decode" if m <= 64 else "mfma_staged")
         assert L.kernel_name(kid) == want_k, label
         # the reference's B[K,N] layout of the same shapes runs on the direct rung
         kid = L.select(m, n, k, k, n, n, KN, BF16, F32, 1)

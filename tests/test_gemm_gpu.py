@@ -235,6 +235,26 @@ def test_splitk_configs_ragged(n, k, m, din, dout):
     _check_tolerance(out.cpu(), a, w, L.B_NK, dout)
 
 
+SPLITK64_CASES = [(1000, 3592, 64), (4096, 1000, 33), (5000, 1000, 47), (9000, 1000, 64), (20000, 264, 40)]
+
+
+@pytest.mark.parametrize("n,k,m", SPLITK64_CASES, ids=[f"N{n}-K{k}-M{m}" for n, k, m in SPLITK64_CASES])
+@pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
+                         ids=["bf16", "f16-f32"])
+def test_splitk_m64_configs_ragged(n, k, m, din, dout):
+    """The plain GEMM's 33 <= M <= 64 configurations of splitk_decode (64 A
+    rows per line; 16 / 32 / 48 W rows per workgroup up to 4096 / 8192 /
+    65535 rows), with a ragged N, M not a multiple of 16 (rows past M repeat
+    row M - 1 and are not stored) and K ending in a partial line."""
+    _say(f"splitk M<=64 N={n} K={k} M={m} {NAME[din]}->{NAME[dout]}")
+    gen = torch.Generator().manual_seed(7 * n + k + m)
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_SPLITK_DECODE, dout, L.B_NK)
+    torch.cuda.synchronize()
+    _check_tolerance(out.cpu(), a, w, L.B_NK, dout)
+
+
 # ---------------------------------------------------------------------------
 # Edge cases and API behaviour
 # ---------------------------------------------------------------------------

@@ -119,7 +119,7 @@ def test_mlp_block_graph_capture(m):
 
 
 @torch.inference_mode()
-@pytest.mark.parametrize("m", [1, 4, 32, 300])
+@pytest.mark.parametrize("m", [1, 4, 32, 48, 300])
 def test_gdn_merged_projection_bit_exact(m):
     """Qwen3.5-0.8B gated-delta-net input projections (hidden 1024; 16 key
     and 16 value heads of 128; N = 6144 + 2048 + 16 + 16 = 8224) as one GEMM:
