@@ -36,7 +36,16 @@ __device__ __forceinline__ u32x4_t load8_strided(const uint16_t* p, int64_t stri
     return u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-template <int DT, int DT_OUT, int BL>
+// FAST: A rows (and W[N,K] rows) can be read as aligned 16-byte chunks.
+// Then the K loop runs in groups of kUnroll steps whose loads are all issued
+// (from row addresses clamped into the matrix) before the group's MFMAs, so
+// each lane keeps kUnroll steps of operands in flight instead of waiting
+// out one load latency per 16-element step; rows outside the matrix are
+// zeroed after the loads.  A K tail shorter than a group takes the general
+// loop.
+constexpr int kUnroll = 4;
+
+template <int DT, int DT_OUT, int BL, int FAST>
 __global__ __launch_bounds__(256) void mfma_direct_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
@@ -59,7 +68,25 @@ __global__ __launch_bounds__(256) void mfma_direct_kernel(
     const uint16_t* ap = a + (a_in ? arow : 0) * lda;
 
     f32x16_t acc = {};
-    for (int64_t k0 = 0; k0 < k; k0 += 16) {
+    int64_t k0 = 0;
+    if constexpr (FAST) {
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        const uint16_t* bp = BL == NANOVLLM_GEMM_B_NK ? b + (b_in ? bcol : 0) * ldb : b + (b_in ? bcol : 0);
+        for (; k0 + 16 * kUnroll <= k; k0 += 16 * kUnroll) {
+            u32x4_t af[kUnroll], bf[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t kb = k0 + 16 * u + 8 * half;
+                af[u] = load16(ap + kb);
+                if constexpr (BL == NANOVLLM_GEMM_B_NK) bf[u] = load16(bp + kb);
+                else bf[u] = load8_strided(bp + kb * ldb, ldb, 8);
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u)
+                acc = mfma_32x32x16<DT>(a_in ? af[u] : zero, b_in ? bf[u] : zero, acc);
+        }
+    }
+    for (; k0 < k; k0 += 16) {
         const int64_t kb = k0 + 8 * half;
         const int64_t kvalid = k - kb;  // may be <= 0 for the tail chunk
         u32x4_t af, bf;
@@ -97,12 +124,22 @@ int launch_typed(const Problem& p, hipStream_t s) {
     const auto* b = static_cast<const uint16_t*>(p.b);
     const int vec_a = (reinterpret_cast<uintptr_t>(p.a) % 16 == 0) && (p.lda % 8 == 0);
     const int vec_b = (reinterpret_cast<uintptr_t>(p.b) % 16 == 0) && (p.ldb % 8 == 0);
-    if (p.b_layout == NANOVLLM_GEMM_B_NK)
-        hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_NK>), grid, block, 0, s, a, b, p.c,
-                           p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), vec_a, vec_b);
-    else
-        hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_KN>), grid, block, 0, s, a, b, p.c,
-                           p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n), vec_a, vec_b);
+    const int ti = int(tiles_m), tj = int(tiles_n);
+    if (p.b_layout == NANOVLLM_GEMM_B_NK) {
+        if (vec_a && vec_b)
+            hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_NK, 1>), grid, block, 0, s, a, b, p.c,
+                               p.m, p.n, p.k, p.lda, p.ldb, p.ldc, ti, tj, vec_a, vec_b);
+        else
+            hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_NK, 0>), grid, block, 0, s, a, b, p.c,
+                               p.m, p.n, p.k, p.lda, p.ldb, p.ldc, ti, tj, vec_a, vec_b);
+    } else {
+        if (vec_a)
+            hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_KN, 1>), grid, block, 0, s, a, b, p.c,
+                               p.m, p.n, p.k, p.lda, p.ldb, p.ldc, ti, tj, vec_a, vec_b);
+        else
+            hipLaunchKernelGGL((mfma_direct_kernel<DT, DT_OUT, NANOVLLM_GEMM_B_KN, 0>), grid, block, 0, s, a, b, p.c,
+                               p.m, p.n, p.k, p.lda, p.ldb, p.ldc, ti, tj, vec_a, vec_b);
+    }
     return check_launch("mfma_direct");
 }
 
