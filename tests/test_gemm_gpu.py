@@ -750,3 +750,27 @@ def test_gemv_load_unrolls(k):
     out = G.gemm_with_kernel(a.to(DEV), w.to(DEV), L.KERNEL_GEMV_DECODE, torch.bfloat16)
     torch.cuda.synchronize()
     _check_tolerance(out.cpu(), a, w, L.B_NK, torch.bfloat16)
+
+
+def test_reference_shape_matrix(capsys):
+    """bench.py --matrix: the reference's benchmark matrix (its Qwen3.5 shape
+    table in fp16 and bf16, deterministic inputs whose products are exact in
+    fp32) on every rung it times; each row must hit the exact product."""
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parent.parent)
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    import bench
+    _say("reference shape matrix")
+    capsys.readouterr()
+    rc = bench.reference_matrix(torch, L, PKG.workloads)
+    rows = [r.split(",") for r in capsys.readouterr().out.strip().splitlines()]
+    header, body = rows[0], rows[1:]
+    assert len(body) == 2 * len(PKG.workloads.QWEN35_SHAPES)
+    col = {name: i for i, name in enumerate(header)}
+    for r in body:
+        assert r[col["status"]] == "PASS", r
+        for c in ("direct_max_abs", "staged_max_abs", "dispatch_max_abs"):
+            assert float(r[col[c]]) == 0.0, (r[col["label"]], c)
+    assert rc == 0
