@@ -63,12 +63,13 @@ enum {
  *   MFMA_STAGED    LDS multi-buffered macro-tile MFMA kernel for
  *                  prefill-shaped problems           (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
  *   SPLITK_DECODE  split-K wavefront-reduction kernel for M <= 32 (the
- *                  plain GEMM up to M = 64 below 65536 W rows) that
- *                  streams W once, copied to LDS in whole 128-byte lines;
- *                  selected for 2 <= M <= 32, for M == 1 when W is larger
- *                  than 64 MiB (LM head), for 33 <= M <= 64 when N <= 4096
- *                  (or N <= 10240 with K <= 1024), and for the fused
- *                  SiLU-and-mul at every M <= 32
+ *                  plain GEMM and the fused SiLU-and-mul up to M = 64 below
+ *                  65536 W rows) that streams W once, copied to LDS in
+ *                  whole 128-byte lines; selected for 2 <= M <= 32, for
+ *                  M == 1 when W is larger than 64 MiB (LM head), for
+ *                  33 <= M <= 64 when N <= 4096 (or N <= 10240 with
+ *                  K <= 1024), and for the fused SiLU-and-mul at every
+ *                  M <= 32 and at 33 <= M <= 64 with 2n <= 16384
  *                                                    (replaces the cuBLAS fallback of
  *                                                     gemm_bench.cu:260-273 for decode shapes)
  *   GEMV_DECODE    M == 1: one wave per W row, coalesced 16-byte streaming,

@@ -73,6 +73,8 @@ constexpr int64_t kSplitkPlainNarrowN = 4096;
 constexpr int64_t kSplitkPlainShortKMaxN = 10240;
 constexpr int64_t kSplitkPlainShortK = 1024;
 
+constexpr int64_t kSplitkSiluMaxRows = 16384;
+
 bool splitk_plain_ok(int64_t m, int64_t n) {
     return m <= kDecodeMaxM || (m <= kSplitkPlainMaxM && n <= kSplitkPlainMaxRows);
 }
@@ -174,11 +176,11 @@ int validate_silu_mul(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
     return NANOVLLM_GEMM_OK;
 }
 
-bool supports_silu_mul(int kernel_id, int64_t m, int64_t k, int64_t lda, int64_t ldw, int aligned16) {
+bool supports_silu_mul(int kernel_id, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, int aligned16) {
     if (!vector_ok(k, lda, ldw, NANOVLLM_GEMM_B_NK, aligned16)) return false;
     switch (kernel_id) {
         case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return true;
-        case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return m <= kDecodeMaxM;
+        case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE: return splitk_plain_ok(m, 2 * n);
         case NANOVLLM_GEMM_KERNEL_GEMV_DECODE: return m == 1;
         default: return false;
     }
@@ -196,6 +198,11 @@ int select_silu_mul(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw, i
     // 1024) splitk_decode's whole-line copies take 4.9 us against 5.2 us for
     // gemv_decode streaming the gate and up rows.
     if (m <= kDecodeMaxM) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+    // 33 <= M <= 64: mfma_staged's SiLU grid is one row of 64 x 128 tiles;
+    // splitk_decode spreads the gate/up pairs over 2n / 32 workgroups (bf16,
+    // K = 1024, M = 64: n = 3584 4.7 against 9.2 us, n = 8192 9.7 against
+    // 11.9 us; K = 2048, n = 3584: 8.1 against 15.1 us).
+    if (m <= kSplitkPlainMaxM && 2 * n <= kSplitkSiluMaxRows) return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
     return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
 }
 
@@ -212,7 +219,7 @@ int silu_mul_entry(int forced_kernel, const void* a, const void* w, void* c, int
     if (kernel < 0) {
         kernel = select_silu_mul(m, n, k, lda, ldw, al);
         if (kernel < 0) return kernel;
-    } else if (!supports_silu_mul(kernel, m, k, lda, ldw, al)) {
+    } else if (!supports_silu_mul(kernel, m, n, k, lda, ldw, al)) {
         return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
                          "kernel %s cannot run silu_mul for this problem (m=%lld n=%lld k=%lld)",
                          nanovllm_gemm_kernel_name(kernel), (long long)m, (long long)n, (long long)k);

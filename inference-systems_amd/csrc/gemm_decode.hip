@@ -465,13 +465,19 @@ int launch_cfg(const Problem& p, hipStream_t s) {
 // A prologue adds its own copies per line to the same configurations.
 constexpr int64_t kWideN = 65536;
 
-// 33 <= M <= 64, the plain GEMM below 65536 rows.
-template <int DT, int DT_OUT>
+// 33 <= M <= 64 below 65536 rows: the plain GEMM, and SiLU-and-mul on
+// gate/up row-group pairs (32 rows per workgroup).
+template <int DT, int DT_OUT, int EPI>
 int launch_rows64(const Problem& p, hipStream_t s) {
-    if (p.n >= kWideN) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M > 32 needs N < 65536");
-    if (p.n <= 4096) return launch_cfg<DT, DT_OUT, 64, 1, 8, 1, 8, EPI_NONE>(p, s);
-    if (p.n <= 8192) return launch_cfg<DT, DT_OUT, 64, 2, 8, 1, 8, EPI_NONE>(p, s);
-    return launch_cfg<DT, DT_OUT, 64, 3, 8, 1, 8, EPI_NONE>(p, s);
+    const int64_t rows = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
+    if (rows >= kWideN) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M > 32 needs N < 65536");
+    if constexpr (EPI == EPI_SILU_MUL) {
+        return launch_cfg<DT, DT_OUT, 64, 2, 8, 1, 8, EPI>(p, s);
+    } else {
+        if (rows <= 4096) return launch_cfg<DT, DT_OUT, 64, 1, 8, 1, 8, EPI>(p, s);
+        if (rows <= 8192) return launch_cfg<DT, DT_OUT, 64, 2, 8, 1, 8, EPI>(p, s);
+        return launch_cfg<DT, DT_OUT, 64, 3, 8, 1, 8, EPI>(p, s);
+    }
 }
 
 template <int DT, int DT_OUT, int EPI, int AROWS, int PRO>
@@ -498,8 +504,8 @@ int launch_epi(const Problem& p, hipStream_t s) {
     if (p.m <= 8) return launch_rows<DT, DT_OUT, EPI, 8, PRO>(p, s);
     if (p.m <= 16) return launch_rows<DT, DT_OUT, EPI, 16, PRO>(p, s);
     if (p.m <= 32) return launch_rows<DT, DT_OUT, EPI, 32, PRO>(p, s);
-    if constexpr (EPI == EPI_NONE && PRO == PRO_NONE)
-        if (p.m <= 64) return launch_rows64<DT, DT_OUT>(p, s);
+    if constexpr ((EPI == EPI_NONE || EPI == EPI_SILU_MUL) && PRO == PRO_NONE)
+        if (p.m <= 64) return launch_rows64<DT, DT_OUT, EPI>(p, s);
     return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above its limit");
 }
 

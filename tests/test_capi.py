@@ -172,12 +172,14 @@ def test_no_vendor_kernel_id():
 def _expected_silu(m, n, k, lda, ldw, aligned):
     if not (aligned and k % 8 == 0 and lda % 8 == 0 and ldw % 8 == 0):
         return L.EUNSUPPORTED
-    return L.KERNEL_SPLITK_DECODE if m <= 32 else L.KERNEL_MFMA_STAGED
+    if m <= 32 or (m <= 64 and 2 * n <= 16384):
+        return L.KERNEL_SPLITK_DECODE
+    return L.KERNEL_MFMA_STAGED
 
 
 @pytest.mark.parametrize("din,dout", [(F16, F16), (F16, F32), (BF16, BF16), (BF16, F32)])
 def test_silu_mul_selection(din, dout):
-    for m, n, k, aligned, pad in itertools.product([1, 2, 32, 33, 2048], [1, 100, 3584, 75968],
+    for m, n, k, aligned, pad in itertools.product([1, 2, 32, 33, 64, 65, 2048], [1, 100, 3584, 8192, 8193, 75968],
                                                    [8, 72, 1024, 1000, 7], (0, 1), (0, 2)):
         lda, ldw = k + pad, k + pad
         got = L.silu_mul_select(m, n, k, lda, ldw, n, din, dout, aligned)

@@ -482,7 +482,7 @@ def test_silu_mul_every_rung_small(kernel, din, dout):
     gen = torch.Generator().manual_seed(31)
     ran = 0
     for m, n, k in SILU_SHAPES:
-        if kernel == L.KERNEL_GEMV_DECODE and m != 1 or kernel == L.KERNEL_SPLITK_DECODE and m > 32:
+        if kernel == L.KERNEL_GEMV_DECODE and m != 1 or kernel == L.KERNEL_SPLITK_DECODE and m > 64:
             continue
         _say(f"silu_mul {L.kernel_name(kernel)} {NAME[din]}->{NAME[dout]} M={m} N={n} K={k}")
         a = torch.randn((m, k), generator=gen).to(din)
@@ -495,7 +495,7 @@ def test_silu_mul_every_rung_small(kernel, din, dout):
     assert ran > 0
 
 
-@pytest.mark.parametrize("m", [1, 4, 32, 2048])
+@pytest.mark.parametrize("m", [1, 4, 32, 48, 2048])
 def test_silu_mul_qwen_mlp_shape(m):
     """Qwen3.5-0.8B gate_up_proj (2 x 3584 rows, K = 1024) + SiluAndMul on
     the kernel the selection table picks."""
@@ -503,7 +503,8 @@ def test_silu_mul_qwen_mlp_shape(m):
     a = torch.randn((m, 1024), generator=gen).bfloat16()
     w = (torch.randn((7168, 1024), generator=gen) * 0.02).bfloat16()
     ad, wd = a.to(DEV), w.to(DEV)
-    want = {1: "splitk_decode", 4: "splitk_decode", 32: "splitk_decode", 2048: "mfma_staged"}[m]
+    want = {1: "splitk_decode", 4: "splitk_decode", 32: "splitk_decode", 48: "splitk_decode",
+            2048: "mfma_staged"}[m]
     assert G.silu_mul_selected_kernel(ad, wd) == want
     _say(f"silu_mul qwen mlp M={m} ({want})")
     out = G.gemm_silu_mul(ad, wd)
