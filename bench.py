@@ -18,7 +18,8 @@ BF16 LM head, the merged gated-delta-net input projection (one N = 8224 GEMM
 against four launches), the fused epilogues and prologues against the
 reference's compositions (gate_up + SiLU-and-mul, the greedy and the sampled
 LM head, the gated-attention output gate before o_proj, the residual add +
-RMSNorm before a projection), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
+RMSNorm before a projection), the bf16 rows of the reference's shape matrix
+(below), torch's own GPU GEMM (hipBLASLt / rocBLAS) on the same inputs
 for comparison only, and the CPU baseline (host F.linear, multi-threaded).
 
 Prints ONE JSON line on stdout; a readable table goes to stderr.  With
@@ -188,7 +189,7 @@ def benchmark_ms(torch, launch, warmup: int, repeats: int, trials: int = 7) -> t
     return graph, plain
 
 
-def reference_matrix(torch, L, W) -> int:
+def reference_matrix(torch, L, W, dtypes=None, emit=print) -> list:
     """The reference's GEMM benchmark matrix on this GPU, one CSV row per
     (dtype, shape) as run_shape writes it (gemm_bench.cu:284-450,
     results/rtx3060_gemm_matrix.csv):
@@ -218,9 +219,9 @@ def reference_matrix(torch, L, W) -> int:
             "staged_ms", "staged_tflops", "vendor_max_abs", "direct_max_abs", "staged_max_abs", "dispatch",
             "dispatch_ms", "dispatch_tflops", "dispatch_max_abs", "dispatch_vs_vendor", "status",
             "dispatch_plain_launch_ms"]
-    print(",".join(cols), flush=True)
-    all_ok = True
-    for dt, dname in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+    emit(",".join(cols))
+    rows = []
+    for dt, dname in dtypes or ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
         for label, m, n, k in W.QWEN35_SHAPES:
             ia = torch.arange(m * k, dtype=torch.int64)
             ib = torch.arange(k * n, dtype=torch.int64)
@@ -268,7 +269,6 @@ def reference_matrix(torch, L, W) -> int:
             staged_ms, staged_err, _ = run(ours(w, L.B_NK, L.KERNEL_MFMA_STAGED), out)
             sel = L.select(m, n, k, k, k, n, L.B_NK, code[dt], L.F32)
             disp_ms, disp_err, disp_plain = run(ours(w, L.B_NK), out)
-            all_ok = all_ok and ok
 
             def tf(ms):
                 return flops / (ms * 1e9)
@@ -277,10 +277,11 @@ def reference_matrix(torch, L, W) -> int:
                    f"{direct_err:.6f}",
                    f"{staged_err:.6f}", L.kernel_name(sel), f"{disp_ms:.6f}", f"{tf(disp_ms):.6f}",
                    f"{disp_err:.6f}", f"{vendor_ms / disp_ms:.6f}", "PASS" if ok else "FAIL", f"{disp_plain:.6f}"]
-            print(",".join("NA" if x == "nan" else str(x) for x in row), flush=True)
+            emit(",".join("NA" if x == "nan" else str(x) for x in row))
+            rows.append(dict(zip(cols, row)))
             del a, b, w, ref, out, expect
             torch.cuda.empty_cache()
-    return 0 if all_ok else 1
+    return rows
 
 
 def main() -> int:
@@ -305,7 +306,8 @@ def main() -> int:
     W = pkg.workloads
     if args.matrix:
         torch.cuda.set_device(0)
-        return reference_matrix(torch, L, W)
+        rows = reference_matrix(torch, L, W, emit=lambda line: print(line, flush=True))
+        return 0 if all(r["status"] == "PASS" for r in rows) else 1
     K_ops = pkg.kernels
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -727,6 +729,17 @@ def main() -> int:
                 del n_ws
             del n_w
         extras["add_rmsnorm_before_projection_bf16_k1024"] = n_rows
+
+    # --------------------------- the reference's shape matrix, bf16 rows
+    if not args.no_extras and name == W.HEADLINE:
+        mrows = reference_matrix(torch, L, W, dtypes=((torch.bfloat16, "bf16"),), emit=lambda line: None)
+        extras["reference_shape_matrix_bf16"] = [
+            {"shape": r["label"], "m": r["M"], "n": r["N"], "k": r["K"], "kernel": r["dispatch"],
+             "us": round(float(r["dispatch_ms"]) * 1e3, 3),
+             "torch_gpu_gemm_us": None if r["vendor_ms"] == "nan" else round(float(r["vendor_ms"]) * 1e3, 3),
+             "exact": r["status"] == "PASS"} for r in mrows]
+        log("reference shape matrix (bf16, fp32 out): " + ", ".join(
+            f"{r['label']} {float(r['dispatch_ms']) * 1e3:.2f} us" for r in mrows))
 
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:

@@ -753,7 +753,7 @@ def test_gemv_load_unrolls(k):
     _check_tolerance(out.cpu(), a, w, L.B_NK, torch.bfloat16)
 
 
-def test_reference_shape_matrix(capsys):
+def test_reference_shape_matrix():
     """bench.py --matrix: the reference's benchmark matrix (its Qwen3.5 shape
     table in fp16 and bf16, deterministic inputs whose products are exact in
     fp32) on every rung it times; each row must hit the exact product."""
@@ -764,14 +764,11 @@ def test_reference_shape_matrix(capsys):
         sys.path.insert(0, root)
     import bench
     _say("reference shape matrix")
-    capsys.readouterr()
-    rc = bench.reference_matrix(torch, L, PKG.workloads)
-    rows = [r.split(",") for r in capsys.readouterr().out.strip().splitlines()]
-    header, body = rows[0], rows[1:]
-    assert len(body) == 2 * len(PKG.workloads.QWEN35_SHAPES)
-    col = {name: i for i, name in enumerate(header)}
-    for r in body:
-        assert r[col["status"]] == "PASS", r
+    lines = []
+    rows = bench.reference_matrix(torch, L, PKG.workloads, emit=lines.append)
+    assert len(rows) == 2 * len(PKG.workloads.QWEN35_SHAPES) and len(lines) == len(rows) + 1
+    assert lines[0].split(",") == list(rows[0].keys())
+    for r in rows:
+        assert r["status"] == "PASS", r
         for c in ("direct_max_abs", "staged_max_abs", "dispatch_max_abs"):
-            assert float(r[col[c]]) == 0.0, (r[col["label"]], c)
-    assert rc == 0
+            assert float(r[c]) == 0.0, (r["label"], c)
