@@ -189,7 +189,7 @@ def benchmark_ms(torch, launch, warmup: int, repeats: int, trials: int = 7) -> t
     return graph, plain
 
 
-def reference_matrix(torch, L, W, dtypes=None, emit=print) -> list:
+def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
     """The reference's GEMM benchmark matrix on this GPU, one CSV row per
     (dtype, shape) as run_shape writes it (gemm_bench.cu:284-450,
     results/rtx3060_gemm_matrix.csv):
@@ -265,8 +265,10 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print) -> list:
                 vendor_ms, vendor_err, _ = run(vendor, ref)
             except RuntimeError:   # no fp32-output half GEMM in this torch build: comparison column left empty
                 vendor_ms = vendor_err = float("nan")
-            direct_ms, direct_err, _ = run(ours(b, L.B_KN, L.KERNEL_MFMA_DIRECT), out)
-            staged_ms, staged_err, _ = run(ours(w, L.B_NK, L.KERNEL_MFMA_STAGED), out)
+            direct_ms = direct_err = staged_ms = staged_err = float("nan")
+            if rungs:   # the direct and staged rungs forced, beside the selected kernel
+                direct_ms, direct_err, _ = run(ours(b, L.B_KN, L.KERNEL_MFMA_DIRECT), out)
+                staged_ms, staged_err, _ = run(ours(w, L.B_NK, L.KERNEL_MFMA_STAGED), out)
             sel = L.select(m, n, k, k, k, n, L.B_NK, code[dt], L.F32)
             disp_ms, disp_err, disp_plain = run(ours(w, L.B_NK), out)
 
@@ -732,7 +734,8 @@ def main() -> int:
 
     # --------------------------- the reference's shape matrix, bf16 rows
     if not args.no_extras and name == W.HEADLINE:
-        mrows = reference_matrix(torch, L, W, dtypes=((torch.bfloat16, "bf16"),), emit=lambda line: None)
+        mrows = reference_matrix(torch, L, W, dtypes=((torch.bfloat16, "bf16"),), emit=lambda line: None,
+                                 rungs=False)
         extras["reference_shape_matrix_bf16"] = [
             {"shape": r["label"], "m": r["M"], "n": r["N"], "k": r["K"], "kernel": r["dispatch"],
              "us": round(float(r["dispatch_ms"]) * 1e3, 3),
