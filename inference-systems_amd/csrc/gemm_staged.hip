@@ -249,16 +249,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         int cur = 0;   // ring stage of tile t
         // COPY: whether tile t + 2 exists (false for the last two tiles).
         // With two waves per SIMD (8-wave workgroups) a wave issues its
-        // K-steps at raised priority and drops it before the wait for the
-        // next tile, so a SIMD whose other wave already waits at the barrier
-        // keeps this wave's MFMAs and copies first in line (2048 x 4096 x
-        // 1024: 20.4 -> 19.9 us, 4096^3: 122.6 -> 119.8 us; no change with
-        // one wave per SIMD).
+        // K-steps at raised priority (3, the highest) and drops it before the
+        // wait for the next tile, so a SIMD whose other wave already waits at
+        // the barrier keeps this wave's MFMAs and copies first in line
+        // (2048 x 4096 x 1024: 20.7 / 20.1 -> 19.2 / 19.1 us in two runs,
+        // against 20.0 / 19.4 at priority 1; 4096^3: 120.5 -> 117.3 us; no
+        // change with one wave per SIMD).
         auto k_tile = [&](int t, auto copy_c) {
             constexpr bool COPY = decltype(copy_c)::value;
             const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
             const int refill = cur == 0 ? STAGES - 1 : cur - 1;
-            if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(1);
+            if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(3);
             read_frags(tile, 1, af1, wf1);
             if constexpr (COPY) mfmas_copy(af0, wf0, t + 2, refill, C0{}, CD0{});
             else mfmas(af0, wf0);
