@@ -248,18 +248,22 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         read_frags(ring, 0, af0, wf0);
         int cur = 0;   // ring stage of tile t
         // COPY: whether tile t + 2 exists (false for the last two tiles).
-        // With two waves per SIMD (8-wave workgroups) a wave issues its
-        // K-steps at raised priority (3, the highest) and drops it before the
-        // wait for the next tile, so a SIMD whose other wave already waits at
-        // the barrier keeps this wave's MFMAs and copies first in line
-        // (2048 x 4096 x 1024: 20.7 / 20.1 -> 19.2 / 19.1 us in two runs,
-        // against 20.0 / 19.4 at priority 1; 4096^3: 120.5 -> 117.3 us; no
-        // change with one wave per SIMD).
+        // A wave issues its K-steps at raised priority (3, the highest) and
+        // drops it before the wait for the next tile, so where waves share a
+        // SIMD (8-wave workgroups, or several 64 x 64 workgroups per CU) one
+        // whose neighbour already waits at its barrier keeps its MFMAs and
+        // copies first in line: 2048 x 4096 x 1024 20.7 / 20.1 -> 19.2 /
+        // 19.1 us in two runs (20.0 / 19.4 at priority 1), 4096^3 120.5 ->
+        // 117.3 us, 64 x 64 tiles on 512 x 4096 x 1024 9.2 / 8.5 -> 8.5 /
+        // 8.0 us and 2048 x 1024 x 2048 14.9 / 14.2 -> 14.1 / 13.6 us; no
+        // change with one wave per SIMD.  (The 2-deep burst schedule, two
+        // 128 x 128 workgroups per CU, lost 4-10% with it and keeps the
+        // default priority.)
         auto k_tile = [&](int t, auto copy_c) {
             constexpr bool COPY = decltype(copy_c)::value;
             const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
             const int refill = cur == 0 ? STAGES - 1 : cur - 1;
-            if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(3);
+            __builtin_amdgcn_s_setprio(3);
             read_frags(tile, 1, af1, wf1);
             if constexpr (COPY) mfmas_copy(af0, wf0, t + 2, refill, C0{}, CD0{});
             else mfmas(af0, wf0);
@@ -270,7 +274,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
             if constexpr (COPY) mfmas_copy(af0, wf0, t + 2, refill, CD01{}, CD2{});
             else mfmas(af0, wf0);
             const int next = cur + 1 == STAGES ? 0 : cur + 1;
-            if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_s_setprio(0);
             if (t + 1 < ktiles) {
                 if constexpr (COPY) wait_vmcnt<IPW>();
                 else wait_vmcnt<0>();
