@@ -210,10 +210,16 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     // K-tiles ago); it goes to the free LDS buffer and is refilled with
     // K-tile t + 3, so every load has two K-tiles of MFMAs to arrive.  The
     // loop is unrolled by two so the set indices are compile-time constants.
+    // The MFMAs run at raised wave priority (3), dropped before the
+    // barrier: of the two waves on a SIMD, the one still multiplying issues
+    // ahead of the one that has reached the barrier or its tile writes
+    // (1024^3 B[K,N] 27.6 -> 26.7 us, 4096^3 1360 -> 1314 us).
     auto step = [&](int64_t t, auto set_c) {
         if (t + 1 < ktiles) store_tile(int((t + 1) & 1), (t + 1) * kT32BK, set_c);
         if (t + 3 < ktiles) load_tile((t + 3) * kT32BK, set_c);
+        __builtin_amdgcn_s_setprio(3);
         multiply(int(t & 1));
+        __builtin_amdgcn_s_setprio(0);
         lds_barrier();
     };
     for (int64_t t = 0; t < ktiles; t += 2) {
