@@ -200,11 +200,18 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
             wait_vmcnt<0>();
         }
         // Every ds_read of the previous tile has returned before the barrier,
-        // so the stage refilled below is free in every wave.
+        // so the stage refilled below is free in every wave.  The copy burst
+        // is issued at raised wave priority: with two workgroups per CU it
+        // then enters the load queue ahead of the other workgroup's
+        // instructions (2048 x 5120 x 1024: 30.3 / 30.2 -> 29.6 / 29.1 us,
+        // 2304 x 5120 x 1024: 31.5 / 31.2 -> 30.9 / 30.5 us; raising it over
+        // the MFMAs instead cost 4-10%).
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_setprio(3);
         if (u + AHEAD < ktiles) issue(u + AHEAD, free_stage);
+        __builtin_amdgcn_s_setprio(0);
     };
 
     if constexpr (SP) {
@@ -256,9 +263,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         // 19.1 us in two runs (20.0 / 19.4 at priority 1), 4096^3 120.5 ->
         // 117.3 us, 64 x 64 tiles on 512 x 4096 x 1024 9.2 / 8.5 -> 8.5 /
         // 8.0 us and 2048 x 1024 x 2048 14.9 / 14.2 -> 14.1 / 13.6 us; no
-        // change with one wave per SIMD.  (The 2-deep burst schedule, two
-        // 128 x 128 workgroups per CU, lost 4-10% with it and keeps the
-        // default priority.)
+        // change with one wave per SIMD.  (The 2-deep burst schedule below
+        // raises it for its copies instead.)
         auto k_tile = [&](int t, auto copy_c) {
             constexpr bool COPY = decltype(copy_c)::value;
             const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
