@@ -189,6 +189,17 @@ def benchmark_ms(torch, launch, warmup: int, repeats: int, trials: int = 7) -> t
     return graph, plain
 
 
+def reference_inputs(torch, m: int, n: int, k: int):
+    """A[M,K] and B[K,N] (fp32, CPU) from the reference's deterministic
+    generators (gemm_bench.cu:296-305): multiples of 1/32 in [-15/32, 15/32]
+    and [-14/32, 14/32], exact in fp16 and bf16."""
+    ia = torch.arange(m * k, dtype=torch.int64)
+    ib = torch.arange(k * n, dtype=torch.int64)
+    a = (((ia * 17 + 3) % 31 - 15).to(torch.float32) * 0.03125).reshape(m, k)
+    b = (((ib * 11 + 5) % 29 - 14).to(torch.float32) * 0.03125).reshape(k, n)
+    return a, b
+
+
 def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
     """The reference's GEMM benchmark matrix on this GPU, one CSV row per
     (dtype, shape) as run_shape writes it (gemm_bench.cu:284-450,
@@ -223,10 +234,8 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
     rows = []
     for dt, dname in dtypes or ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
         for label, m, n, k in W.QWEN35_SHAPES:
-            ia = torch.arange(m * k, dtype=torch.int64)
-            ib = torch.arange(k * n, dtype=torch.int64)
-            a = (((ia * 17 + 3) % 31 - 15).to(torch.float32) * 0.03125).reshape(m, k).to(dt).to(dev)
-            b = (((ib * 11 + 5) % 29 - 14).to(torch.float32) * 0.03125).reshape(k, n).to(dt).to(dev)
+            a, b = reference_inputs(torch, m, n, k)
+            a, b = a.to(dt).to(dev), b.to(dt).to(dev)
             w = b.t().contiguous()
             flops = 2.0 * m * n * k
             repeats = min(max(int(2.0e10 / max(flops, 1.0)), 10), 200)

@@ -1,0 +1,35 @@
+"""bench.py's contract on the CPU: more than one GPU is refused with a
+message, and the shape-matrix inputs are the reference's generators
+(gemm_bench.cu:296-305, restated in the oracle)."""
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from oracle import gemm_oracle as orc
+
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_matrix_inputs_are_the_reference_generators():
+    for m, n, k in ((1, 7, 64), (16, 33, 130), (5, 4, 3)):
+        a, b = bench.reference_inputs(torch, m, n, k)
+        assert np.array_equal(a.numpy() * 32, orc.kat_bench_a_int(m, k).astype(np.float32))
+        assert np.array_equal(b.numpy() * 32, orc.kat_bench_b_int(k, n).astype(np.float32))
+        # exact in both half formats
+        for dt in (torch.float16, torch.bfloat16):
+            assert torch.equal(a.to(dt).float(), a) and torch.equal(b.to(dt).float(), b)
