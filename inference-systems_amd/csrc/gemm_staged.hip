@@ -473,8 +473,8 @@ int launch_tile(const Problem& p, hipStream_t s) {
 //     on a 3-deep ring with spread copies (against a 2-deep burst ring:
 //     1024^3 6.85 -> 6.57 us, 512 x 4096 x 1024 8.49 -> 8.04, 256 x 6144 x
 //     1024 8.03 -> 7.46, 2048 x 1024 x 2048 14.2 -> 14.0, 512 x 1024 x 3584
-//     27.3 -> 17.2); SiLU pairs take 64 x 128 with a 3-deep ring from
-//     K = 2048;
+//     27.3 -> 17.2); SiLU pairs take 64 x 128, also with spread copies on
+//     a 3-deep ring;
 //   * 128 < wide <= 256 or wide > 384: one 8-wave workgroup per CU on
 //     128 x 256 (half the A reads of two 128 x 128 tiles), 3-deep ring,
 //     copies spread between the MFMAs.  Against the 2-deep 128 x 128 burst
@@ -500,13 +500,15 @@ int launch_epi(const Problem& p, hipStream_t s) {
     const int64_t n_tiles = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
     const int64_t tiles = ((p.m + 127) / 128) * ((n_tiles + 127) / 128);
     if (tiles <= kSmallGridTiles) {
-        const bool deep = p.k >= 2048;
         if constexpr (EPI == EPI_NONE) {
             return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI, RS, 1>(p, s);
         } else if constexpr (EPI == EPI_SILU_MUL) {
-            // gate/up pairs need two 32-row W blocks per wave
-            if (deep) return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS, 0>(p, s);
-            return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 2, EPI, RS, 0>(p, s);
+            // gate/up pairs need two 32-row W blocks per wave: 64 x 128
+            // tiles, spread copies on a 3-deep ring (gate_up n = 3584, K =
+            // 1024, M = 96 / 128 / 256: 9.4 / 9.4-9.7 / 9.6-10.5 -> 8.7 /
+            // 8.6-8.9 / 8.8-9.4 us against the 2-deep burst ring, and
+            // 15.7-17.0 -> 14.5-14.8 us at K = 2048 against the 3-deep one)
+            return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS, 1>(p, s);
         }
     }
     if constexpr (EPI != EPI_ARGMAX) {
