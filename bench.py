@@ -569,8 +569,10 @@ def main() -> int:
         del s_w
 
         # ----------------------------- greedy LM head (argmax, no logits)
-        # Against the reference's path: fp32 logits [M, 151936] from the GEMM,
-        # then float_logits.argmax(dim=-1) (sampler.py:8-21) on the GPU.
+        # Against the reference's path: bf16 logits [M, 151936] from the GEMM
+        # (F.linear in the model dtype, embed_head.py:61), then
+        # logits.float().argmax(dim=-1) (sampler.py:15, 21) on the GPU.  The
+        # fused head ranks the same bf16-rounded logits.
         lw = W.WORKLOADS["bf16_lm_head_n151936_k1024"]
         _, l_w0 = W.make_inputs("bf16_lm_head_n151936_k1024", 1, device=dev)
         l_ws = [l_w0, l_w0.clone()]
@@ -581,33 +583,33 @@ def main() -> int:
             l_val = torch.empty(lm, dtype=torch.float32, device=dev)
             l_need = L.argmax_workspace_bytes(lm, lw.n, lw.k, lw.k, lw.k, L.BF16)
             l_ws_buf = torch.empty(l_need, dtype=torch.uint8, device=dev)
-            l_logits = torch.empty(lm, lw.n, dtype=torch.float32, device=dev)
+            l_logits = torch.empty(lm, lw.n, dtype=torch.bfloat16, device=dev)
 
             def greedy(wt, l_a=l_a, l_tok=l_tok, l_val=l_val, l_ws_buf=l_ws_buf, lm=lm, l_need=l_need):
                 args_ = (l_a.data_ptr(), wt.data_ptr(), l_tok.data_ptr(), l_val.data_ptr(), lm, lw.n, lw.k, lw.k,
-                         lw.k, L.BF16, l_ws_buf.data_ptr(), l_need)
+                         lw.k, L.BF16, L.BF16, l_ws_buf.data_ptr(), l_need)
 
                 def f():
                     L.argmax_raw(*args_, torch.cuda.current_stream().cuda_stream)
                 return f
 
             def logits_then_argmax(wt, l_a=l_a, l_logits=l_logits, lm=lm):
-                gemm = launcher(l_a, wt, l_logits, lm, lw.n, lw.k, L.B_NK, torch.bfloat16, torch.float32)
+                gemm = launcher(l_a, wt, l_logits, lm, lw.n, lw.k, L.B_NK, torch.bfloat16, torch.bfloat16)
 
                 def f():
                     gemm()
-                    l_logits.argmax(dim=-1)
+                    l_logits.float().argmax(dim=-1)
                 return f
             t_g = median_graph_ms(torch, [greedy(l_ws[i % 2]) for i in range(20)], trials=3)
             t_l = median_graph_ms(torch, [logits_then_argmax(l_ws[i % 2]) for i in range(20)], trials=3)
             l_rows.append({"m": lm, "greedy_us": round(t_g * 1e3, 3), "logits_then_argmax_us": round(t_l * 1e3, 3),
                            "speedup": round(t_l / t_g, 3)})
-            log(f"lm head greedy M={lm}: fused {t_g * 1e3:.1f} us, fp32 logits + torch argmax {t_l * 1e3:.1f} us")
+            log(f"lm head greedy M={lm}: fused {t_g * 1e3:.1f} us, bf16 logits + torch argmax {t_l * 1e3:.1f} us")
         extras["lm_head_greedy_bf16_n151936_k1024"] = l_rows
 
         # ----------------------------- sampled LM head (Sampler, no logits)
         # Every row sampled at temperature 0.8, against the reference's path:
-        # fp32 logits from the GEMM, then Sampler.forward (sampler.py:8-21:
+        # bf16 logits from the GEMM, then Sampler.forward (sampler.py:8-21:
         # softmax, exponential draws, divide, argmax; eager here, the
         # reference wraps it in torch.compile).
         p_rows = []
@@ -618,18 +620,19 @@ def main() -> int:
             p_temp = torch.full((lm,), 0.8, dtype=torch.float32, device=dev)
             p_need = L.argmax_workspace_bytes(lm, lw.n, lw.k, lw.k, lw.k, L.BF16)
             p_ws_buf = torch.empty(p_need, dtype=torch.uint8, device=dev)
-            p_logits = torch.empty(lm, lw.n, dtype=torch.float32, device=dev)
+            p_logits = torch.empty(lm, lw.n, dtype=torch.bfloat16, device=dev)
 
             def sampled(wt, step, l_a=l_a, p_tok=p_tok, p_val=p_val, p_temp=p_temp, p_ws_buf=p_ws_buf, lm=lm,
                         p_need=p_need):
                 def f():
                     L.sample_raw(l_a.data_ptr(), wt.data_ptr(), p_temp.data_ptr(), 1234, step, p_tok.data_ptr(),
-                                 p_val.data_ptr(), lm, lw.n, lw.k, lw.k, lw.k, L.BF16, p_ws_buf.data_ptr(), p_need,
+                                 p_val.data_ptr(), lm, lw.n, lw.k, lw.k, lw.k, L.BF16, L.BF16, p_ws_buf.data_ptr(),
+                                 p_need,
                                  torch.cuda.current_stream().cuda_stream)
                 return f
 
             def logits_then_sampler(wt, l_a=l_a, p_logits=p_logits, p_temp=p_temp, lm=lm):
-                gemm = launcher(l_a, wt, p_logits, lm, lw.n, lw.k, L.B_NK, torch.bfloat16, torch.float32)
+                gemm = launcher(l_a, wt, p_logits, lm, lw.n, lw.k, L.B_NK, torch.bfloat16, torch.bfloat16)
 
                 def f():
                     gemm()
@@ -640,7 +643,7 @@ def main() -> int:
             p_rows.append({"m": lm, "sampled_us": round(t_s * 1e3, 3),
                            "logits_then_sampler_us": round(t_r * 1e3, 3), "speedup": round(t_r / t_s, 3)})
             log(f"lm head sampled (T=0.8) M={lm}: fused {t_s * 1e3:.1f} us, "
-                f"fp32 logits + eager torch Sampler {t_r * 1e3:.1f} us")
+                f"bf16 logits + eager torch Sampler {t_r * 1e3:.1f} us")
         extras["lm_head_sampled_bf16_n151936_k1024"] = p_rows
         del l_ws, l_w0
 

@@ -182,15 +182,23 @@ int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k,
 /*
  * Greedy token of an LM head without its logits:
  *
- *     tokens[i] = argmax_j sum_k a[i,k] w[j,k],   j < n
+ *     tokens[i] = argmax_j L(sum_k a[i,k] w[j,k]),   j < n
  *
  * fp32 accumulation, first index on ties, NaN above every number (the
- * rule of torch.argmax), token ids as int64; max_logits[i] (optional, may
- * be NULL) receives the fp32 logit of the token.  Replaces the [m, n] fp32
- * logits of ParallelLMHead (nanovllm/layers/embed_head.py:61) followed by
- * the greedy branch of Sampler, float_logits.argmax(dim=-1)
- * (nanovllm/layers/sampler.py:8-21).  `workspace` (8-byte aligned, device
- * memory, contents scratch) must hold
+ * rule of torch.argmax), token ids as int64.  L is the logit the head
+ * ranks, chosen by logit_dtype:
+ *   - logit_dtype == dtype_in: the fp32 sum rounded to nearest even in the
+ *     input type, i.e. the logits ParallelLMHead's F.linear returns in the
+ *     model dtype (nanovllm/layers/embed_head.py:61), which Sampler ranks
+ *     after .float() (nanovllm/layers/sampler.py:15, 21).  This is the
+ *     reference's greedy token; equal rounded logits go to the first index;
+ *   - logit_dtype == NANOVLLM_GEMM_F32: the fp32 sum itself (finer ranking
+ *     than the reference; opt-in).
+ * Any other logit_dtype is NANOVLLM_GEMM_EINVAL.  max_logits[i] (optional,
+ * may be NULL) receives L of the token as fp32.  Replaces the [m, n] logits
+ * of ParallelLMHead followed by the greedy branch of Sampler,
+ * float_logits.argmax(dim=-1) (nanovllm/layers/sampler.py:8-21).
+ * `workspace` (8-byte aligned, device memory, contents scratch) must hold
  * nanovllm_gemm_argmax_workspace_bytes() bytes; one call launches the GEMM
  * pass and a small reduction pass on `stream`.  Inputs f16 or bf16 on the
  * vector path (16-byte aligned a and w, k, lda and ldw multiples of 8).
@@ -198,7 +206,7 @@ int nanovllm_gemm_silu_mul_select(int64_t m, int64_t n, int64_t k,
 int nanovllm_gemm_argmax(const void* a, const void* w,
                          int64_t* tokens, float* max_logits,
                          int64_t m, int64_t n, int64_t k,
-                         int64_t lda, int64_t ldw, int dtype_in,
+                         int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
                          void* workspace, int64_t workspace_bytes,
                          void* stream);
 
@@ -213,7 +221,7 @@ int nanovllm_gemm_argmax_with_kernel(int kernel_id,
                                      const void* a, const void* w,
                                      int64_t* tokens, float* max_logits,
                                      int64_t m, int64_t n, int64_t k,
-                                     int64_t lda, int64_t ldw, int dtype_in,
+                                     int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
                                      void* workspace, int64_t workspace_bytes,
                                      void* stream);
 
@@ -231,7 +239,9 @@ int nanovllm_gemm_argmax_select(int64_t m, int64_t n, int64_t k,
  *
  *     tokens[i] = argmax_j (l[i,j] / temperatures[i] - ln E[i,j]),
  *
- * l the fp32 logits, which is the reference's argmax_j of
+ * l the logits as nanovllm_gemm_argmax ranks them (logit_dtype: rounded to
+ * the input type as the reference's F.linear returns them, or fp32), which
+ * is the reference's argmax_j of
  * softmax(l / T)_j / E_j (the Gumbel-max form of a draw from softmax(l / T)).
  * E[i,j] = max(-ln u, 1e-10) with u = ((x >> 8) + 1) / 2^24 and x word
  * j % 4 of Philox4x32-10(counter = {j / 4, i, offset, offset >> 32},
@@ -246,7 +256,7 @@ int nanovllm_gemm_sample(const void* a, const void* w,
                          const float* temperatures, uint64_t seed, uint64_t offset,
                          int64_t* tokens, float* scores,
                          int64_t m, int64_t n, int64_t k,
-                         int64_t lda, int64_t ldw, int dtype_in,
+                         int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
                          void* workspace, int64_t workspace_bytes,
                          void* stream);
 
@@ -257,7 +267,7 @@ int nanovllm_gemm_sample_with_kernel(int kernel_id,
                                      const float* temperatures, uint64_t seed, uint64_t offset,
                                      int64_t* tokens, float* scores,
                                      int64_t m, int64_t n, int64_t k,
-                                     int64_t lda, int64_t ldw, int dtype_in,
+                                     int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
                                      void* workspace, int64_t workspace_bytes,
                                      void* stream);
 

@@ -46,15 +46,15 @@ SIGNATURES = {
     "nanovllm_gemm_silu_mul_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _INT,
                                                   _INT, _VP]),
     "nanovllm_gemm_silu_mul_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT]),
-    "nanovllm_gemm_argmax": (_INT, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP, _I64, _VP]),
+    "nanovllm_gemm_argmax": (_INT, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _VP, _I64, _VP]),
     "nanovllm_gemm_argmax_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _INT]),
-    "nanovllm_gemm_argmax_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP,
-                                                _I64, _VP]),
+    "nanovllm_gemm_argmax_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT,
+                                                _VP, _I64, _VP]),
     "nanovllm_gemm_argmax_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _INT, _INT]),
-    "nanovllm_gemm_sample": (_INT, [_VP, _VP, _VP, _U64, _U64, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP,
-                                    _I64, _VP]),
+    "nanovllm_gemm_sample": (_INT, [_VP, _VP, _VP, _U64, _U64, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT,
+                                    _VP, _I64, _VP]),
     "nanovllm_gemm_sample_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _U64, _U64, _VP, _VP, _I64, _I64, _I64, _I64,
-                                                _I64, _INT, _VP, _I64, _VP]),
+                                                _I64, _INT, _INT, _VP, _I64, _VP]),
     "nanovllm_gemm_gated": (_INT, [_VP, _VP, _VP, _VP] + [_I64] * 9 + [_INT, _INT, _VP, _I64, _VP]),
     "nanovllm_gemm_gated_workspace_bytes": (_I64, [_I64, _I64, _I64, _INT]),
     "nanovllm_gemm_gated_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP] + [_I64] * 9 + [_INT, _INT, _VP, _I64, _VP]),
@@ -166,31 +166,33 @@ def argmax_select(m, n, k, lda, ldw, dtype_in, aligned16=True) -> int:
     return load().nanovllm_gemm_argmax_select(m, n, k, lda, ldw, dtype_in, int(bool(aligned16)))
 
 
-def argmax_raw(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in, ws_ptr, ws_bytes, stream,
-               kernel: int | None = None) -> None:
-    """Enqueue the greedy LM head (GEMM pass + reduction) on `stream`; raise on error."""
+def argmax_raw(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in, logit_dtype, ws_ptr, ws_bytes,
+               stream, kernel: int | None = None) -> None:
+    """Enqueue the greedy LM head (GEMM pass + reduction) on `stream`; raise
+    on error.  logit_dtype: ``dtype_in`` ranks the logits rounded to the
+    input type (the reference's bf16 F.linear logits), ``F32`` the fp32 sums."""
     lib = load()
     if kernel is None:
-        rc = lib.nanovllm_gemm_argmax(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in, ws_ptr,
-                                      ws_bytes, stream)
+        rc = lib.nanovllm_gemm_argmax(a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw, dtype_in, logit_dtype,
+                                      ws_ptr, ws_bytes, stream)
     else:
         rc = lib.nanovllm_gemm_argmax_with_kernel(kernel, a_ptr, w_ptr, tokens_ptr, logits_ptr, m, n, k, lda, ldw,
-                                                  dtype_in, ws_ptr, ws_bytes, stream)
+                                                  dtype_in, logit_dtype, ws_ptr, ws_bytes, stream)
     check(rc, "nanovllm_gemm_argmax")
 
 
-def sample_raw(a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr, m, n, k, lda, ldw, dtype_in, ws_ptr,
-               ws_bytes, stream, kernel: int | None = None) -> None:
+def sample_raw(a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr, m, n, k, lda, ldw, dtype_in, logit_dtype,
+               ws_ptr, ws_bytes, stream, kernel: int | None = None) -> None:
     """Enqueue the sampled LM head (GEMM pass + reduction) on `stream`; raise on error."""
     lib = load()
     seed &= (1 << 64) - 1
     offset &= (1 << 64) - 1
     if kernel is None:
         rc = lib.nanovllm_gemm_sample(a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr, m, n, k, lda, ldw,
-                                      dtype_in, ws_ptr, ws_bytes, stream)
+                                      dtype_in, logit_dtype, ws_ptr, ws_bytes, stream)
     else:
         rc = lib.nanovllm_gemm_sample_with_kernel(kernel, a_ptr, w_ptr, t_ptr, seed, offset, tokens_ptr, scores_ptr,
-                                                  m, n, k, lda, ldw, dtype_in, ws_ptr, ws_bytes, stream)
+                                                  m, n, k, lda, ldw, dtype_in, logit_dtype, ws_ptr, ws_bytes, stream)
     check(rc, "nanovllm_gemm_sample")
 
 

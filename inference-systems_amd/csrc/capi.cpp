@@ -270,13 +270,25 @@ int64_t argmax_workspace_bytes(int64_t m, int64_t n) {
     return ((n + cols_per_block - 1) / cols_per_block) * m * int64_t(sizeof(uint64_t));
 }
 
+// The LM head ranks the fp32 accumulator (logit_dt f32) or its rounding to
+// the input type (logit_dt == din: the logits F.linear returns in the model
+// dtype, nanovllm/layers/embed_head.py:61).
+int validate_logit_dtype(int din, int logit_dt) {
+    if (logit_dt != NANOVLLM_GEMM_F32 && logit_dt != din)
+        return set_error(NANOVLLM_GEMM_EINVAL,
+                         "logit_dtype must be NANOVLLM_GEMM_F32 (0) or the input dtype (%d), got %d", din, logit_dt);
+    return NANOVLLM_GEMM_OK;
+}
+
 // `sample`: nullptr for the greedy head; the sampled head passes its
 // per-row temperatures (device memory, required) and noise seed / offset.
 int argmax_entry(int forced_kernel, const void* a, const void* w, int64_t* tokens, float* logits, int64_t m,
-                 int64_t n, int64_t k, int64_t lda, int64_t ldw, int din, void* workspace, int64_t workspace_bytes,
-                 void* stream, const SampleArgs* sample = nullptr) {
+                 int64_t n, int64_t k, int64_t lda, int64_t ldw, int din, int logit_dt, void* workspace,
+                 int64_t workspace_bytes, void* stream, const SampleArgs* sample = nullptr) {
     g_last_error.clear();
     int rc = validate_argmax(m, n, k, lda, ldw, din);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    rc = validate_logit_dtype(din, logit_dt);
     if (rc != NANOVLLM_GEMM_OK) return rc;
     if (m == 0) return NANOVLLM_GEMM_OK;
     if (a == nullptr || w == nullptr || tokens == nullptr || workspace == nullptr)
@@ -306,6 +318,7 @@ int argmax_entry(int forced_kernel, const void* a, const void* w, int64_t* token
     p.keys = static_cast<uint64_t*>(workspace);
     p.key_blocks = &blocks;
     if (sample != nullptr) p.sample = *sample;
+    p.sample.logit_dtype = logit_dt;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     rc = run(kernel, p, s);
     if (rc != NANOVLLM_GEMM_OK) return rc;
@@ -592,41 +605,42 @@ int64_t nanovllm_gemm_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k, in
 }
 
 int nanovllm_gemm_argmax(const void* a, const void* w, int64_t* tokens, float* max_logits, int64_t m, int64_t n,
-                         int64_t k, int64_t lda, int64_t ldw, int dtype_in, void* workspace,
+                         int64_t k, int64_t lda, int64_t ldw, int dtype_in, int logit_dtype, void* workspace,
                          int64_t workspace_bytes, void* stream) {
-    return nvg::argmax_entry(-1, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, workspace, workspace_bytes,
-                             stream);
+    return nvg::argmax_entry(-1, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, logit_dtype, workspace,
+                             workspace_bytes, stream);
 }
 
 int nanovllm_gemm_argmax_with_kernel(int kernel_id, const void* a, const void* w, int64_t* tokens,
                                      float* max_logits, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
-                                     int dtype_in, void* workspace, int64_t workspace_bytes, void* stream) {
+                                     int dtype_in, int logit_dtype, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
     if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
         nvg::g_last_error.clear();
         return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
     }
-    return nvg::argmax_entry(kernel_id, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, workspace,
-                             workspace_bytes, stream);
+    return nvg::argmax_entry(kernel_id, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, logit_dtype,
+                             workspace, workspace_bytes, stream);
 }
 
 int nanovllm_gemm_sample(const void* a, const void* w, const float* temperatures, uint64_t seed, uint64_t offset,
                          int64_t* tokens, float* scores, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
-                         int dtype_in, void* workspace, int64_t workspace_bytes, void* stream) {
+                         int dtype_in, int logit_dtype, void* workspace, int64_t workspace_bytes, void* stream) {
     const nvg::SampleArgs sa{temperatures, seed, offset};
-    return nvg::argmax_entry(-1, a, w, tokens, scores, m, n, k, lda, ldw, dtype_in, workspace, workspace_bytes,
-                             stream, &sa);
+    return nvg::argmax_entry(-1, a, w, tokens, scores, m, n, k, lda, ldw, dtype_in, logit_dtype, workspace,
+                             workspace_bytes, stream, &sa);
 }
 
 int nanovllm_gemm_sample_with_kernel(int kernel_id, const void* a, const void* w, const float* temperatures,
                                      uint64_t seed, uint64_t offset, int64_t* tokens, float* scores, int64_t m,
-                                     int64_t n, int64_t k, int64_t lda, int64_t ldw, int dtype_in, void* workspace,
-                                     int64_t workspace_bytes, void* stream) {
+                                     int64_t n, int64_t k, int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
     if (kernel_id < 0 || kernel_id >= NANOVLLM_GEMM_KERNEL_COUNT) {
         nvg::g_last_error.clear();
         return nvg::set_error(NANOVLLM_GEMM_EINVAL, "unknown kernel id %d", kernel_id);
     }
     const nvg::SampleArgs sa{temperatures, seed, offset};
-    return nvg::argmax_entry(kernel_id, a, w, tokens, scores, m, n, k, lda, ldw, dtype_in, workspace,
+    return nvg::argmax_entry(kernel_id, a, w, tokens, scores, m, n, k, lda, ldw, dtype_in, logit_dtype, workspace,
                              workspace_bytes, stream, &sa);
 }
 
@@ -720,6 +734,6 @@ int nanovllm_gemm_add_rmsnorm_with_kernel(int kernel_id, const void* h, const vo
 
 const char* nanovllm_gemm_last_error(void) { return nvg::g_last_error.c_str(); }
 
-int nanovllm_gemm_version(void) { return (1 << 16) | 5; }
+int nanovllm_gemm_version(void) { return (2 << 16) | 0; }
 
 }  // extern "C"

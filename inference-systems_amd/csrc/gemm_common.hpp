@@ -40,11 +40,17 @@ constexpr int PRO_NONE = 0;
 constexpr int PRO_GATE = 1;
 constexpr int PRO_ADD_NORM = 2;
 
-// Per-row temperatures and noise of the sampled LM head (see sample_score).
+// Per-row temperatures and noise of the sampled LM head (see sample_score),
+// and the type whose rounding of each logit the LM head ranks.
 struct SampleArgs {
     const float* temperature = nullptr;   // [M]; nullptr: every row greedy
     uint64_t seed = 0;
     uint64_t offset = 0;
+    // NANOVLLM_GEMM_F32: the fp32 accumulator itself.  NANOVLLM_GEMM_BF16 /
+    // NANOVLLM_GEMM_F16: the logit rounded (nearest even) to that type, which
+    // is what F.linear in the model dtype hands to the sampler
+    // (nanovllm/layers/embed_head.py:61, nanovllm/layers/sampler.py:15).
+    int logit_dtype = NANOVLLM_GEMM_F32;
 };
 
 // One GEMM problem as it crosses the C ABI (see include/nanovllm_gemm.h).
@@ -308,6 +314,16 @@ __device__ __forceinline__ u32x4_t philox4x32_10(u32x4_t c, uint32_t k0, uint32_
     return c;
 }
 
+// The value the LM head ranks for an fp32 logit: the logit itself, or its
+// round-to-nearest-even image in bf16 / fp16 read back as fp32 (equal
+// rounded logits then go to the first column, as torch.argmax does on the
+// reference's bf16 logits).  logit_dtype is uniform across the launch.
+__device__ __forceinline__ float ranked_logit(float v, const SampleArgs& sa) {
+    if (sa.logit_dtype == NANOVLLM_GEMM_BF16) return bf16_to_f32(round_half<NANOVLLM_GEMM_BF16>(v));
+    if (sa.logit_dtype == NANOVLLM_GEMM_F16) return f16_to_f32(round_half<NANOVLLM_GEMM_F16>(v));
+    return v;
+}
+
 // Temperature of a sampled row, 0 for a greedy one (temperature <= 1e-10)
 // or when the head is greedy altogether.
 __device__ __forceinline__ float sample_temperature(int64_t row, const SampleArgs& sa) {
@@ -331,9 +347,10 @@ __device__ __forceinline__ float gumbel_score(float v, float t, uint32_t word) {
     return v / t - __builtin_amdgcn_logf(e) * kLn2;
 }
 
-// The score that ranks column col of row row: the logit itself on a greedy
-// row, v / T - ln E on a sampled one.
+// The score that ranks column col of row row: the ranked logit v (see
+// ranked_logit) on a greedy row, v / T - ln E on a sampled one.
 __device__ __forceinline__ float sample_score(float v, int64_t row, int64_t col, const SampleArgs& sa) {
+    v = ranked_logit(v, sa);
     const float t = sample_temperature(row, sa);
     if (t == 0.0f) return v;
     const u32x4_t x = sample_words(row, col >> 2, sa);

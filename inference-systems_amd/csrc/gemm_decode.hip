@@ -290,7 +290,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
         if (row < m && t == 0.0f) {
             for (int cc = sub; cc < 16 * RG; cc += TPR) {
                 if (n0 + cc >= n) break;
-                const uint64_t key = argmax_key(total(cc >> 4, row >> 4, cc & 15, row & 15), n0 + cc);
+                const uint64_t key = argmax_key(ranked_logit(total(cc >> 4, row >> 4, cc & 15, row & 15), sa), n0 + cc);
                 best = key > best ? key : best;
             }
         } else if (row < m) {
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                 for (int j = 0; j < 4; ++j) {
                     const int cc = c4 + j;
                     if (n0 + cc >= n) break;
-                    const float v = gumbel_score(total(cc >> 4, row >> 4, cc & 15, row & 15), t, x[j]);
+                    const float v = gumbel_score(ranked_logit(total(cc >> 4, row >> 4, cc & 15, row & 15), sa), t, x[j]);
                     const uint64_t key = argmax_key(v, n0 + cc);
                     best = key > best ? key : best;
                 }

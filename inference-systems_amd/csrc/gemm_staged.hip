@@ -398,7 +398,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
                 for (int j = 0; j < 4; ++j) {
                     const int col = col0 + j;
                     if (n0 + col >= n) break;
-                    const uint64_t key = argmax_key(t != 0.0f ? gumbel_score(rowp[col], t, x[j]) : rowp[col], n0 + col);
+                    const float v = ranked_logit(rowp[col], sa);
+                    const uint64_t key = argmax_key(t != 0.0f ? gumbel_score(v, t, x[j]) : v, n0 + col);
                     best = key > best ? key : best;
                 }
             }

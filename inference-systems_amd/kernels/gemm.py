@@ -257,10 +257,23 @@ def argmax_contract_reason(a: torch.Tensor, w: torch.Tensor) -> Optional[str]:
     return None
 
 
-def _launch_argmax(a: torch.Tensor, w: torch.Tensor, kernel: Optional[int] = None):
+def _logit_code(a: torch.Tensor, logits_dtype: Optional[torch.dtype], op: str) -> int:
+    """The C ABI's logit_dtype: None or a.dtype ranks the logits rounded to
+    the input type (what the reference's F.linear hands to its sampler,
+    nanovllm/layers/embed_head.py:61, sampler.py:15), float32 the fp32 sums."""
+    if logits_dtype is None or logits_dtype == a.dtype:
+        return _CODE[a.dtype]
+    if logits_dtype == torch.float32:
+        return _lib.F32
+    raise RuntimeError(f"nanovllm::{op}: logits_dtype must be None, {a.dtype} or torch.float32, got {logits_dtype}")
+
+
+def _launch_argmax(a: torch.Tensor, w: torch.Tensor, logits_dtype: Optional[torch.dtype] = None,
+                   kernel: Optional[int] = None):
     reason = argmax_contract_reason(a, w)
     if reason is not None:
         raise RuntimeError(f"nanovllm::gemm_argmax: {reason}")
+    code = _logit_code(a, logits_dtype, "gemm_argmax")
     k = a.shape[-1]
     n = w.shape[0]
     m = a.numel() // k
@@ -274,17 +287,19 @@ def _launch_argmax(a: torch.Tensor, w: torch.Tensor, kernel: Optional[int] = Non
     with torch.cuda.device(a.device):
         stream = torch.cuda.current_stream(a.device).cuda_stream
         _lib.argmax_raw(a.data_ptr(), w.data_ptr(), tokens.data_ptr(), logits.data_ptr(), m, n, k, k, k,
-                        _CODE[a.dtype], workspace.data_ptr(), need, stream, kernel)
+                        _CODE[a.dtype], code, workspace.data_ptr(), need, stream, kernel)
     return tokens, logits
 
 
 @torch.library.custom_op("nanovllm::gemm_argmax", mutates_args=())
-def _gemm_argmax_op(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    return _launch_argmax(a, w)
+def _gemm_argmax_op(a: torch.Tensor, w: torch.Tensor,
+                    logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    return _launch_argmax(a, w, logits_dtype)
 
 
 @_gemm_argmax_op.register_fake
-def _gemm_argmax_fake(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def _gemm_argmax_fake(a: torch.Tensor, w: torch.Tensor,
+                      logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
     torch._check(w.dim() == 2)
     torch._check(a.shape[-1] == w.shape[1])
     torch._check(a.dtype == w.dtype)
@@ -292,15 +307,20 @@ def _gemm_argmax_fake(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, t
     return (a.new_empty(a.shape[:-1], dtype=torch.int64), a.new_empty(a.shape[:-1], dtype=torch.float32))
 
 
-def gemm_argmax(a: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """(argmax_j (a @ w.T)[..., j], that maximum in fp32), without the logits;
-    ties go to the first index, as in torch.argmax."""
-    return torch.ops.nanovllm.gemm_argmax(a, w)
+def gemm_argmax(a: torch.Tensor, w: torch.Tensor,
+                logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(argmax_j L(a @ w.T)[..., j], that L as fp32), without the logits;
+    ties go to the first index, as in torch.argmax.  L is the logit rounded
+    to a.dtype (logits_dtype None or a.dtype: the reference's greedy token
+    on the logits F.linear returns in the model dtype) or the fp32 sum
+    itself (logits_dtype=torch.float32)."""
+    return torch.ops.nanovllm.gemm_argmax(a, w, logits_dtype)
 
 
-def gemm_argmax_with_kernel(a: torch.Tensor, w: torch.Tensor, kernel: int) -> tuple[torch.Tensor, torch.Tensor]:
+def gemm_argmax_with_kernel(a: torch.Tensor, w: torch.Tensor, kernel: int,
+                            logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """The greedy head with its GEMM pass on one named kernel."""
-    return _launch_argmax(a, w, kernel)
+    return _launch_argmax(a, w, logits_dtype, kernel)
 
 
 # ---------------------------------------------------------------------------
@@ -323,10 +343,11 @@ def sample_contract_reason(a: torch.Tensor, w: torch.Tensor, temperatures: torch
 
 
 def _launch_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
-                   kernel: Optional[int] = None):
+                   logits_dtype: Optional[torch.dtype] = None, kernel: Optional[int] = None):
     reason = sample_contract_reason(a, w, temperatures)
     if reason is not None:
         raise RuntimeError(f"nanovllm::gemm_sample: {reason}")
+    code = _logit_code(a, logits_dtype, "gemm_sample")
     k = a.shape[-1]
     n = w.shape[0]
     m = a.numel() // k
@@ -340,20 +361,20 @@ def _launch_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor,
     with torch.cuda.device(a.device):
         stream = torch.cuda.current_stream(a.device).cuda_stream
         _lib.sample_raw(a.data_ptr(), w.data_ptr(), temperatures.data_ptr(), int(seed), int(offset),
-                        tokens.data_ptr(), scores.data_ptr(), m, n, k, k, k, _CODE[a.dtype], workspace.data_ptr(),
-                        need, stream, kernel)
+                        tokens.data_ptr(), scores.data_ptr(), m, n, k, k, k, _CODE[a.dtype], code,
+                        workspace.data_ptr(), need, stream, kernel)
     return tokens, scores
 
 
 @torch.library.custom_op("nanovllm::gemm_sample", mutates_args=())
 def _gemm_sample_op(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
-                    offset: int) -> tuple[torch.Tensor, torch.Tensor]:
-    return _launch_sample(a, w, temperatures, seed, offset)
+                    offset: int, logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    return _launch_sample(a, w, temperatures, seed, offset, logits_dtype)
 
 
 @_gemm_sample_op.register_fake
 def _gemm_sample_fake(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
-                      offset: int) -> tuple[torch.Tensor, torch.Tensor]:
+                      offset: int, logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
     torch._check(w.dim() == 2)
     torch._check(a.shape[-1] == w.shape[1])
     torch._check(a.dtype == w.dtype)
@@ -370,22 +391,24 @@ def _as_i64(x: int) -> int:
 
 
 def gemm_sample(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int,
-                offset: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Sampler.forward (nanovllm/layers/sampler.py:8-21) on the fp32 logits
-    a @ w.T without writing them: (token ids, winning scores).  Rows with
+                offset: int, logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Sampler.forward (nanovllm/layers/sampler.py:8-21) on the logits
+    a @ w.T (rounded to a.dtype as the reference's F.linear returns them,
+    or fp32 with logits_dtype=torch.float32, as gemm_argmax ranks them)
+    without writing them: (token ids, winning scores).  Rows with
     temperature <= 1e-10 take the greedy token (score = its logit); the
     others a draw from softmax(logits / T) by the Gumbel-max rule
     argmax_j (l_j / T - ln E_j), the reference's argmax of
     softmax(l / T) / E, with E from the library's Philox4x32-10 stream at
     (seed, offset), both taken modulo 2^64; advance `offset` between calls
     for fresh draws."""
-    return torch.ops.nanovllm.gemm_sample(a, w, temperatures, _as_i64(seed), _as_i64(offset))
+    return torch.ops.nanovllm.gemm_sample(a, w, temperatures, _as_i64(seed), _as_i64(offset), logits_dtype)
 
 
 def gemm_sample_with_kernel(a: torch.Tensor, w: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
-                            kernel: int) -> tuple[torch.Tensor, torch.Tensor]:
+                            kernel: int, logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """The sampled head with its GEMM pass on one named kernel."""
-    return _launch_sample(a, w, temperatures, seed, offset, kernel)
+    return _launch_sample(a, w, temperatures, seed, offset, logits_dtype, kernel)
 
 
 def validate_gemm_backend(backend: str) -> str:
@@ -450,21 +473,31 @@ def silu_mul_linear(x: torch.Tensor, weight: torch.Tensor, *, backend: Optional[
     return gemm_silu_mul(x, weight)
 
 
-def greedy_linear(x: torch.Tensor, weight: torch.Tensor, *,
-                  backend: Optional[str] = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """(argmax, max) of F.linear(x, weight) in fp32 along the last dim, with
-    the backend switch of ``linear``: ``torch`` computes the fp32 logits and
-    takes torch.argmax (Sampler's greedy branch, sampler.py:8-21), ``hip``
-    runs the fused greedy head, ``auto`` the fused head when its contract
-    holds."""
+def _torch_logits(x, weight, logits_dtype):
+    """The logits the torch path ranks, as fp32: F.linear in the model dtype
+    (the reference's ParallelLMHead), or an fp32 GEMM of the same inputs."""
+    if logits_dtype == torch.float32 and x.dtype != torch.float32:
+        return F.linear(x.float(), weight.float())
+    return F.linear(x, weight).float()
+
+
+def greedy_linear(x: torch.Tensor, weight: torch.Tensor, *, backend: Optional[str] = None,
+                  logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(argmax, max) of the logits F.linear(x, weight) along the last dim,
+    read as fp32, with the backend switch of ``linear``: ``torch`` computes
+    the logits and takes torch.argmax (Sampler's greedy branch,
+    sampler.py:8-21), ``hip`` runs the fused greedy head, ``auto`` the fused
+    head when its contract holds.  logits_dtype None (or x.dtype) ranks the
+    logits in the model dtype, as the reference does; torch.float32 ranks
+    fp32 logits."""
     backend = validate_gemm_backend(backend) if backend is not None else default_backend()
     if backend != "torch":
         reason = argmax_contract_reason(x, weight)
         if reason is None:
-            return gemm_argmax(x, weight)
+            return gemm_argmax(x, weight, logits_dtype)
         if backend == "hip":
             raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
-    logits = F.linear(x, weight).float()
+    logits = _torch_logits(x, weight, logits_dtype)
     tokens = logits.argmax(dim=-1)
     return tokens, logits.gather(-1, tokens.unsqueeze(-1)).squeeze(-1)
 
@@ -482,17 +515,19 @@ def torch_sampler(logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Ten
 
 
 def sample_linear(x: torch.Tensor, weight: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int, *,
-                  backend: Optional[str] = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+                  backend: Optional[str] = None,
+                  logits_dtype: Optional[torch.dtype] = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Sampled tokens of F.linear(x, weight) with the backend switch of
-    ``linear``: ``torch`` writes the fp32 logits and runs the reference
-    Sampler (its own exponential draws; no scores, None), ``hip`` the fused
-    sampled head, ``auto`` the fused head when its contract holds.  Returns
-    (tokens, scores)."""
+    ``linear``: ``torch`` writes the logits (model dtype, or fp32 with
+    logits_dtype=torch.float32) and runs the reference Sampler (its own
+    exponential draws; no scores, None), ``hip`` the fused sampled head,
+    ``auto`` the fused head when its contract holds.  Returns (tokens,
+    scores)."""
     backend = validate_gemm_backend(backend) if backend is not None else default_backend()
     if backend != "torch":
         reason = sample_contract_reason(x, weight, temperatures)
         if reason is None:
-            return gemm_sample(x, weight, temperatures, seed, offset)
+            return gemm_sample(x, weight, temperatures, seed, offset, logits_dtype)
         if backend == "hip":
             raise RuntimeError(f"HIP GEMM backend is unavailable: {reason}")
-    return torch_sampler(F.linear(x, weight), temperatures), None
+    return torch_sampler(_torch_logits(x, weight, logits_dtype), temperatures), None

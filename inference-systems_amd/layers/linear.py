@@ -169,13 +169,17 @@ class RowParallelLinear(LinearBase):
 
 
 class ParallelLMHead(nn.Module):
-    """Tied / vocab-parallel LM head (embed_head.py:45-66) producing fp32 logits.
+    """Tied / vocab-parallel LM head (embed_head.py:45-66).
 
     The reference selects the last token of each sequence from the forward
     context in prefill (embed_head.py:57-60); here the caller passes
-    ``last_indices`` (or None in decode).  On the HIP path the GEMM writes
-    fp32 logits directly (out_dtype=float32), which is the dtype the sampler
-    casts to (nanovllm/layers/sampler.py:15)."""
+    ``last_indices`` (or None in decode).  ``logits_dtype`` None (the
+    default) keeps the reference's semantics on every backend: the logits
+    come out in the model dtype, as ``F.linear`` returns them
+    (embed_head.py:61), and the greedy and sampled heads rank those rounded
+    values (Sampler takes ``logits.float()``, sampler.py:15), so the tokens
+    are the reference's.  ``logits_dtype = torch.float32`` opts into fp32
+    logits written by the GEMM directly and fp32 ranking."""
 
     def __init__(self, num_embeddings: int, embedding_dim: int, bias: bool = False):
         super().__init__()
@@ -188,6 +192,7 @@ class ParallelLMHead(nn.Module):
         self.weight = nn.Parameter(torch.empty(self.num_embeddings_per_partition, embedding_dim))
         self.weight.weight_loader = self.weight_loader
         self.gemm_backend: Optional[str] = None
+        self.logits_dtype: Optional[torch.dtype] = None   # None: the model dtype (the reference's)
 
     def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor):
         param_data = param.data
@@ -198,7 +203,7 @@ class ParallelLMHead(nn.Module):
     def forward(self, x: torch.Tensor, last_indices: Optional[torch.Tensor] = None):
         if last_indices is not None:
             x = x[last_indices].contiguous()
-        logits = gemm_linear(x, self.weight, None, out_dtype=torch.float32, backend=self.gemm_backend)
+        logits = gemm_linear(x, self.weight, None, out_dtype=self.logits_dtype, backend=self.gemm_backend)
         if self.tp_size > 1:
             all_logits = [torch.empty_like(logits) for _ in range(self.tp_size)] if self.tp_rank == 0 else None
             dist.gather(logits, all_logits, 0)
@@ -207,16 +212,17 @@ class ParallelLMHead(nn.Module):
 
     def greedy(self, x: torch.Tensor, last_indices: Optional[torch.Tensor] = None):
         """Greedy tokens without the logits: the temperature-0 branch of
-        Sampler (nanovllm/layers/sampler.py:8-21, argmax of the fp32 logits,
-        first index on ties) applied to this head's output.  Returns (token
-        ids int64, their fp32 logits); on the HIP path one fused launch
+        Sampler (nanovllm/layers/sampler.py:8-21, argmax of the logits read
+        as fp32, first index on ties) applied to this head's output (model
+        dtype, or fp32 with logits_dtype = torch.float32).  Returns (token
+        ids int64, their logits as fp32); on the HIP path one fused launch
         replaces the [M, vocab] logits write and the argmax read-back.  With
         tensor parallelism every rank finds the best token of its vocabulary
         shard and rank 0 keeps the best pair, the lower rank on equal logits
         (the first index of the gathered logits); other ranks return None."""
         if last_indices is not None:
             x = x[last_indices].contiguous()
-        tokens, values = greedy_linear(x, self.weight, backend=self.gemm_backend)
+        tokens, values = greedy_linear(x, self.weight, backend=self.gemm_backend, logits_dtype=self.logits_dtype)
         if self.tp_size > 1:
             tokens = tokens + self.vocab_start_idx
             rank0 = self.tp_rank == 0
@@ -249,7 +255,8 @@ class ParallelLMHead(nn.Module):
         if last_indices is not None:
             x = x[last_indices].contiguous()
         if self.tp_size == 1:
-            return sample_linear(x, self.weight, temperatures, seed, offset, backend=self.gemm_backend)
+            return sample_linear(x, self.weight, temperatures, seed, offset, backend=self.gemm_backend,
+                                 logits_dtype=self.logits_dtype)
         backend = validate_gemm_backend(self.gemm_backend) if self.gemm_backend is not None else default_backend()
         if backend == "torch" or sample_contract_reason(x, self.weight, temperatures) is not None:
             if backend == "hip":
@@ -258,7 +265,7 @@ class ParallelLMHead(nn.Module):
             logits = self.forward(x)
             return (torch_sampler(logits, temperatures), None) if self.tp_rank == 0 else (None, None)
         rank_seed = (int(seed) ^ (self.tp_rank * 0x9E3779B97F4A7C15)) & ((1 << 64) - 1)
-        tokens, scores = gemm_sample(x, self.weight, temperatures, rank_seed, offset)
+        tokens, scores = gemm_sample(x, self.weight, temperatures, rank_seed, offset, self.logits_dtype)
         tokens = tokens + self.vocab_start_idx
         rank0 = self.tp_rank == 0
         all_tokens = [torch.empty_like(tokens) for _ in range(self.tp_size)] if rank0 else None

@@ -401,6 +401,41 @@ def greedy_token_admissible(token: np.ndarray, r64: np.ndarray, s64: np.ndarray,
     return chosen >= best - bound[rows, token] - bound.max(axis=-1)
 
 
+def rounded_logit_bounds(r64: np.ndarray, s64: np.ndarray, k: int, dtype: str):
+    """(lo, hi) in float64: the smallest and largest value a logit can take
+    once an fp32 sum within the accumulation bound of its exact value r is
+    rounded to nearest even in `dtype` ("bf16", "f16"), as the reference's
+    F.linear in the model dtype does (nanovllm/layers/embed_head.py:61).
+    Rounding is monotone, so the ends of [r - b, r + b] bound it."""
+    r64 = np.asarray(r64, dtype=np.float64)
+    b = fp32_accumulation_bound(s64, k)
+    return to_f64(round_f64(r64 - b, dtype), dtype), to_f64(round_f64(r64 + b, dtype), dtype)
+
+
+def first_argmax_candidates(lo: np.ndarray, hi: np.ndarray) -> np.ndarray:
+    """mask[i, j]: column j is the first-index argmax of row i for some
+    choice of every logit l within [lo, hi] (torch.argmax's rule on the
+    reference's logits): l_j can exceed every earlier column's lowest value
+    and reach every later column's lowest value, i.e.
+    hi_j > max_{c < j} lo_c and hi_j >= max_{c > j} lo_c."""
+    lo = np.asarray(lo, dtype=np.float64)
+    hi = np.asarray(hi, dtype=np.float64)
+    pad = np.full(lo.shape[:-1] + (1,), -np.inf)
+    before = np.concatenate([pad, np.maximum.accumulate(lo, axis=-1)[..., :-1]], axis=-1)
+    after = np.concatenate([np.maximum.accumulate(lo[..., ::-1], axis=-1)[..., ::-1][..., 1:], pad], axis=-1)
+    return (hi > before) & (hi >= after)
+
+
+def rounded_greedy_candidates(r64: np.ndarray, s64: np.ndarray, k: int, dtype: str) -> np.ndarray:
+    """Tokens the reference's greedy rule (argmax of the logits rounded to
+    `dtype`, first index on ties; sampler.py:15, 21) can return when each
+    logit is summed in fp32 in some order.  A row with a single candidate
+    has one right answer whatever the summation order; a row with more
+    straddles a rounding boundary within the accumulation bound."""
+    lo, hi = rounded_logit_bounds(r64, s64, k, dtype)
+    return first_argmax_candidates(lo, hi)
+
+
 # ---------------------------------------------------------------------------
 # Sampled rows of the LM head (Sampler.forward, layers/sampler.py:8-21)
 # ---------------------------------------------------------------------------
@@ -476,14 +511,26 @@ def sampler_reference_f64(logits: np.ndarray, temperatures: np.ndarray, e: np.nd
 
 
 def sample_token_admissible(token: np.ndarray, r64: np.ndarray, s64: np.ndarray, k: int,
-                            temperatures: np.ndarray, e: np.ndarray) -> np.ndarray:
+                            temperatures: np.ndarray, e: np.ndarray, logit_dtype: str = "f32") -> np.ndarray:
     """True where `token` is a correct choice of the sampled head for fp32
     logits: its exact score is within the error budget of the best exact
     score.  The budget is the fp32 accumulation bound of each logit over T
     (twice, as two logits may swap), plus 4e-6 (1 + |score|) for the fp32
-    division, the hardware logarithms and the draw's fp32 E."""
+    division, the hardware logarithms and the draw's fp32 E.
+
+    logit_dtype "bf16" / "f16": the logits are rounded to that type first
+    (the reference's model-dtype logits); every logit then lies in
+    rounded_logit_bounds, and the token's highest possible score must reach
+    the best lowest possible score of the row."""
     t = np.asarray(temperatures, dtype=np.float32)
     greedy = t <= np.float32(1e-10)
+    if logit_dtype != "f32":
+        lo, hi = rounded_logit_bounds(r64, s64, k, logit_dtype)
+        sc_lo = sample_scores_f64(lo, temperatures, e)
+        sc_hi = sample_scores_f64(hi, temperatures, e)
+        slack = np.where(greedy[:, None], 0.0, 4e-6 * (1.0 + np.abs(sc_hi)))
+        rows = np.arange(sc_hi.shape[0])
+        return sc_hi[rows, token] + slack[rows, token] >= (sc_lo - slack).max(axis=-1)
     scale = np.where(greedy, 1.0, 1.0 / np.where(greedy, 1.0, t.astype(np.float64)))[:, None]
     sc = sample_scores_f64(r64, temperatures, e)
     bound = fp32_accumulation_bound(s64, k) * scale + np.where(greedy[:, None], 0.0, 4e-6 * (1.0 + np.abs(sc)))

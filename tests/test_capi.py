@@ -35,7 +35,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_version_and_names(lib):
-    assert lib.nanovllm_gemm_version() >> 16 == 1
+    assert lib.nanovllm_gemm_version() >> 16 == 2
     expected = ["fp32_naive", "fp32_tiled", "mfma_direct", "mfma_staged", "splitk_decode", "gemv_decode"]
     assert [L.kernel_name(i) for i in range(L.KERNEL_COUNT)] == expected
     assert L.kernel_name(99) == "unknown" and L.kernel_name(-1) == "unknown"
@@ -250,43 +250,59 @@ def test_argmax_rejects_invalid(args, code, msg):
 
 
 def test_argmax_validates_before_launch(lib):
-    assert lib.nanovllm_gemm_argmax(None, None, None, None, 0, 64, 16, 16, 16, BF16, None, 0, None) == L.OK
-    rc = lib.nanovllm_gemm_argmax(None, None, None, None, 4, 64, 16, 16, 16, BF16, None, 0, None)
+    assert lib.nanovllm_gemm_argmax(None, None, None, None, 0, 64, 16, 16, 16, BF16, BF16, None, 0, None) == L.OK
+    rc = lib.nanovllm_gemm_argmax(None, None, None, None, 4, 64, 16, 16, 16, BF16, BF16, None, 0, None)
     assert rc == L.EINVAL and "non-null" in L.last_error()
     dummy = 1 << 20
     need = L.argmax_workspace_bytes(4, 64, 16, 16, 16, BF16)
-    rc = lib.nanovllm_gemm_argmax(dummy, dummy, dummy, None, 4, 64, 16, 16, 16, BF16, dummy, need - 8, None)
+    rc = lib.nanovllm_gemm_argmax(dummy, dummy, dummy, None, 4, 64, 16, 16, 16, BF16, BF16, dummy, need - 8, None)
     assert rc == L.EINVAL and f"needs {need}" in L.last_error()
-    rc = lib.nanovllm_gemm_argmax(dummy, dummy, dummy, None, 4, 64, 16, 16, 16, BF16, dummy + 4, need, None)
+    rc = lib.nanovllm_gemm_argmax(dummy, dummy, dummy, None, 4, 64, 16, 16, 16, BF16, BF16, dummy + 4, need, None)
     assert rc == L.EINVAL and "8-byte aligned" in L.last_error()
     rc = lib.nanovllm_gemm_argmax_with_kernel(L.KERNEL_GEMV_DECODE, dummy, dummy, dummy, None, 4, 64, 16, 16, 16,
-                                              BF16, dummy, need, None)
+                                              BF16, F32, dummy, need, None)
     assert rc == L.EUNSUPPORTED and "gemv_decode" in L.last_error()
     rc = lib.nanovllm_gemm_argmax_with_kernel(L.KERNEL_SPLITK_DECODE, dummy, dummy, dummy, None, 33, 64, 16, 16, 16,
-                                              BF16, dummy, 10 ** 6, None)
+                                              BF16, BF16, dummy, 10 ** 6, None)
     assert rc == L.EUNSUPPORTED
+
+
+@pytest.mark.parametrize("din,logit,ok", [(BF16, BF16, True), (BF16, F32, True), (BF16, F16, False),
+                                          (F16, F16, True), (F16, F32, True), (F16, BF16, False), (BF16, 7, False)])
+def test_argmax_logit_dtype(lib, din, logit, ok):
+    """The LM head ranks the logits rounded to the input type (the
+    reference's F.linear output) or the fp32 sums; any other ranking type is
+    rejected before anything is launched (m = 0 launches nothing when valid)."""
+    rc = lib.nanovllm_gemm_argmax(None, None, None, None, 0, 64, 16, 16, 16, din, logit, None, 0, None)
+    rc_s = lib.nanovllm_gemm_sample(None, None, None, 1, 2, None, None, 0, 64, 16, 16, 16, din, logit, None, 0, None)
+    if ok:
+        assert rc == L.OK and rc_s == L.OK
+    else:
+        assert rc == L.EINVAL and "logit_dtype" in L.last_error()
+        assert rc_s == L.EINVAL
 
 
 def test_sample_validates_before_launch(lib):
     """The sampled head shares the greedy head's checks and adds its own:
     temperatures must be a non-null, 4-byte aligned device pointer."""
-    assert lib.nanovllm_gemm_sample(None, None, None, 1, 2, None, None, 0, 64, 16, 16, 16, BF16, None, 0,
+    assert lib.nanovllm_gemm_sample(None, None, None, 1, 2, None, None, 0, 64, 16, 16, 16, BF16, BF16, None, 0,
                                     None) == L.OK
     dummy = 1 << 20
     need = L.argmax_workspace_bytes(4, 64, 16, 16, 16, BF16)
-    rc = lib.nanovllm_gemm_sample(dummy, dummy, None, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16, dummy, need, None)
+    rc = lib.nanovllm_gemm_sample(dummy, dummy, None, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16, BF16, dummy, need,
+                                  None)
     assert rc == L.EINVAL and "temperatures" in L.last_error()
-    rc = lib.nanovllm_gemm_sample(dummy, dummy, dummy + 2, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16, dummy, need,
-                                  None)
+    rc = lib.nanovllm_gemm_sample(dummy, dummy, dummy + 2, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16, BF16, dummy,
+                                  need, None)
     assert rc == L.EINVAL and "4-byte aligned" in L.last_error()
-    rc = lib.nanovllm_gemm_sample(dummy, dummy, dummy, 1, 2, dummy, None, 4, 64, 16, 16, 16, L.F32, dummy, need,
-                                  None)
+    rc = lib.nanovllm_gemm_sample(dummy, dummy, dummy, 1, 2, dummy, None, 4, 64, 16, 16, 16, L.F32, L.F32, dummy,
+                                  need, None)
     assert rc == L.EUNSUPPORTED
     rc = lib.nanovllm_gemm_sample_with_kernel(L.KERNEL_FP32_TILED, dummy, dummy, dummy, 1, 2, dummy, None, 4, 64,
-                                              16, 16, 16, BF16, dummy, need, None)
+                                              16, 16, 16, BF16, BF16, dummy, need, None)
     assert rc == L.EUNSUPPORTED and "fp32_tiled" in L.last_error()
     rc = lib.nanovllm_gemm_sample_with_kernel(99, dummy, dummy, dummy, 1, 2, dummy, None, 4, 64, 16, 16, 16, BF16,
-                                              dummy, need, None)
+                                              BF16, dummy, need, None)
     assert rc == L.EINVAL and "unknown kernel" in L.last_error()
 
 

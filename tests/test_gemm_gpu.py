@@ -550,12 +550,16 @@ ARGMAX_CASES = [(L.KERNEL_SPLITK_DECODE, m) for m in (1, 5, 17, 32)] + [(L.KERNE
 @pytest.mark.parametrize("kernel,m", ARGMAX_CASES, ids=[f"{L.kernel_name(k)}-M{m}" for k, m in ARGMAX_CASES])
 @pytest.mark.parametrize("n", [1000, 70001])
 @pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-def test_argmax_equals_argmax_of_own_logits(kernel, m, n, din):
+@pytest.mark.parametrize("rank", ["model", "f32"])
+def test_argmax_equals_argmax_of_own_logits(kernel, m, n, din, rank):
     """The greedy head and the fp32-output GEMM on the same kernel compute the
-    same fp32 logits, so the tokens are exactly torch.argmax of those logits
-    (first index on ties; rows 3 and n - 2 of W are copies of row 1, so some
-    logits tie exactly) and the values exactly the chosen logits; the tokens
-    are also admissible against the float64 logits."""
+    same fp32 logits.  Ranking the model dtype (the default, the
+    reference's), the tokens are exactly torch.argmax of those logits rounded
+    to the input type -- which is also the narrow-output GEMM on the same
+    kernel -- and the values the chosen rounded logits; ranking fp32, the
+    argmax of the fp32 logits.  Rows 3 and n - 2 of W are copies of row 1,
+    so some logits tie exactly (first index wins).  The tokens are also
+    admissible against the float64 logits."""
     gen = torch.Generator().manual_seed(m * 7 + n)
     k = 256
     a = torch.randn((m, k), generator=gen).to(din)
@@ -564,29 +568,40 @@ def test_argmax_equals_argmax_of_own_logits(kernel, m, n, din):
     w[n - 2] = w[1]
     a[0] = w[1] * 4        # row 0's best token is 1, tied with 3 and n - 2
     ad, wd = a.to(DEV), w.to(DEV)
-    _say(f"argmax {L.kernel_name(kernel)} {NAME[din]} M={m} N={n}")
-    tokens, values = G.gemm_argmax_with_kernel(ad, wd, kernel)
+    _say(f"argmax {L.kernel_name(kernel)} {NAME[din]} M={m} N={n} rank={rank}")
+    ldt = None if rank == "model" else torch.float32
+    tokens, values = G.gemm_argmax_with_kernel(ad, wd, kernel, ldt)
     logits = G.gemm_with_kernel(ad, wd, kernel, torch.float32)
+    narrow = G.gemm_with_kernel(ad, wd, kernel, din) if rank == "model" else None
     torch.cuda.synchronize()
     assert tokens.dtype == torch.int64 and values.dtype == torch.float32
-    assert torch.equal(tokens, logits.argmax(-1))
-    assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
+    ranked = logits.to(din).float() if rank == "model" else logits
+    if narrow is not None:
+        assert torch.equal(narrow.float(), ranked)
+    assert torch.equal(tokens, ranked.argmax(-1))
+    assert torch.equal(values, ranked.gather(-1, tokens[:, None]).squeeze(-1))
     assert int(tokens[0]) == 1
     a64, w64 = a.double().numpy(), w.double().numpy()
     r = orc.gemm_f64(a64, w64)
-    assert orc.greedy_token_admissible(tokens.cpu().numpy(), r, orc.abs_products_f64(a64, w64), k).all()
+    s = orc.abs_products_f64(a64, w64)
+    if rank == "model":
+        cand = orc.rounded_greedy_candidates(r, s, k, NAME[din])
+        assert cand[np.arange(m), tokens.cpu().numpy()].all()
+    else:
+        assert orc.greedy_token_admissible(tokens.cpu().numpy(), r, s, k).all()
 
 
 @pytest.mark.parametrize("m", [1, 32])
 def test_argmax_lm_head_shape_and_graph(m):
-    """Qwen3.5 LM head (151936 x 1024): the selected path, then captured in a
-    HIP graph (workspace from the graph's pool) and replayed."""
+    """Qwen3.5 LM head (151936 x 1024): the selected path ranks the bf16
+    logits the plain GEMM writes with bf16 output (same configuration), then
+    captured in a HIP graph (workspace from the graph's pool) and replayed."""
     gen = torch.Generator().manual_seed(70 + m)
     a = torch.randn((m, 1024), generator=gen).bfloat16().to(DEV)
     w = (torch.randn((151936, 1024), generator=gen) * 0.02).bfloat16().to(DEV)
     _say(f"argmax lm head M={m}")
     tokens, values = G.gemm_argmax(a, w)
-    logits = G.gemm(a, w, torch.float32)      # same splitk configuration at these shapes
+    logits = G.gemm(a, w).float()      # bf16 logits from the same splitk configuration
     torch.cuda.synchronize()
     assert torch.equal(tokens, logits.argmax(-1))
     assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
@@ -609,6 +624,107 @@ def test_argmax_lm_head_shape_and_graph(m):
         assert torch.equal(t_static, t_eager) and torch.equal(v_static, v_eager), f"replay {step}"
 
 
+def _exact_head_inputs(m, n, k, seed):
+    """Integer numerators over 32 in the ranges of the reference's
+    known-answer generators (|a| <= 15/32, |w| <= 14/32): every product is
+    a multiple of 1/1024 and every partial sum of K = 1024 of them stays
+    below 2^24 / 1024, so the fp32 logits are exact in any summation order.
+    Per row of A, an earlier column is planted whose exact logit is just
+    below the row's best but rounds to the same bf16 value (the reference's
+    first-index rule must pick it; fp32 ranking would not), and the best row
+    of W is copied to a later column (an exact tie)."""
+    rng = np.random.default_rng(seed)
+    a_int = rng.integers(-15, 16, size=(m, k)).astype(np.int64)
+    w_int = rng.integers(-14, 15, size=(n, k)).astype(np.int64)
+    w64 = w_int.astype(np.float64)      # integer sums below 2^53 are exact in float64
+    for i in range(m):
+        exact = w64 @ a_int[i].astype(np.float64)
+        best = int(exact.argmax())
+        w_int[(best + 5000) % n] = w_int[best]                 # exact tie, later column when it wraps
+        w64[(best + 5000) % n] = w64[best]
+        target = int(rng.integers(0, max(best, 1)))            # an earlier column (or 0)
+        if target == best:
+            continue
+        # W[target] = W[best] with one numerator lowered by 1 where a is +-1 or
+        # +-2: the logit drops by 1/1024 or 2/1024, under a bf16 step here
+        for kk in np.flatnonzero(np.abs(a_int[i]) <= 2):
+            cand = w_int[best].copy()
+            step = 1 if a_int[i, kk] > 0 else -1
+            if not -14 <= cand[kk] - step <= 14:
+                continue
+            cand[kk] -= step
+            v_best = exact[best] / 1024.0
+            v_new = float(a_int[i] @ cand) / 1024.0
+            rb = orc.to_f64(orc.round_f64(np.array([v_best, v_new]), "bf16"), "bf16")
+            if v_new < v_best and rb[0] == rb[1] and a_int[i, kk] != 0:
+                w_int[target] = cand
+                w64[target] = cand
+                break
+    return a_int, w_int
+
+
+@pytest.mark.parametrize("m,kernel", [(1, None), (8, None), (32, None), (40, None), (32, L.KERNEL_MFMA_STAGED)],
+                         ids=["M1", "M8", "M32", "M40-staged", "M32-staged"])
+def test_lm_head_exact_inputs_reference_tokens(m, kernel):
+    """At the LM-head shape (151936 x 1024) on exact inputs (fp32 logits
+    exact in any order), the greedy head's default ranking returns exactly
+    the reference's token: the first index of the maximum of the exact
+    logits rounded to bf16 (F.linear in bf16, then .float().argmax(-1),
+    embed_head.py:61, sampler.py:15, 21), and its bf16 logit; the rows carry
+    planted earlier columns that only tie after rounding.  fp32 ranking
+    returns the exact fp32 argmax instead."""
+    n, k = 151936, 1024
+    a_int, w_int = _exact_head_inputs(m, n, k, 400 + m)
+    a = torch.from_numpy(a_int.astype(np.float32) / 32).bfloat16()
+    w = torch.from_numpy(w_int.astype(np.float32) / 32).bfloat16()
+    exact = (a_int.astype(np.float64) @ w_int.T.astype(np.float64)) / 1024.0   # float64, exact
+    rounded = orc.to_f64(orc.round_f64(exact, "bf16"), "bf16")
+    want = rounded.argmax(-1)                                 # numpy: first index on ties
+    want_f32 = exact.argmax(-1)
+    assert (want != want_f32).sum() >= max(1, m // 2), "planted near-ties missing"
+    ad, wd = a.to(DEV), w.to(DEV)
+    _say(f"lm head exact inputs M={m} kernel={kernel}")
+    if kernel is None:
+        tokens, values = G.gemm_argmax(ad, wd)
+        t32, _ = G.gemm_argmax(ad, wd, torch.float32)
+    else:
+        tokens, values = G.gemm_argmax_with_kernel(ad, wd, kernel)
+        t32, _ = G.gemm_argmax_with_kernel(ad, wd, kernel, torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(tokens.cpu().numpy(), want)
+    np.testing.assert_array_equal(values.cpu().numpy().astype(np.float64), rounded[np.arange(m), want])
+    np.testing.assert_array_equal(t32.cpu().numpy(), want_f32)
+
+
+@pytest.mark.parametrize("m", [1, 32, 40])
+def test_lm_head_random_inputs_match_torch_reference(m):
+    """Random Qwen-like inputs at the LM-head shape: the fused greedy head
+    against the reference's composition on this GPU (torch's bf16 F.linear,
+    then .float().argmax(-1)).  A row whose oracle candidate set (every
+    token an fp32 sum within the accumulation bound can give after bf16
+    rounding) has one member must give that token on both paths; a row whose
+    top logits straddle a rounding boundary within the bound may differ, but
+    both tokens must be candidates.  The straddling count is printed."""
+    n, k = 151936, 1024
+    gen = torch.Generator().manual_seed(500 + m)
+    a = torch.randn((m, k), generator=gen).bfloat16()
+    w = (torch.randn((n, k), generator=gen) * 0.02).bfloat16()
+    ad, wd = a.to(DEV), w.to(DEV)
+    _say(f"lm head vs torch M={m}")
+    tokens, _ = G.gemm_argmax(ad, wd)
+    ref_tokens = torch.nn.functional.linear(ad, wd).float().argmax(-1)
+    torch.cuda.synchronize()
+    tokens, ref_tokens = tokens.cpu().numpy(), ref_tokens.cpu().numpy()
+    a64, w64 = a.double().numpy(), w.double().numpy()
+    cand = orc.rounded_greedy_candidates(orc.gemm_f64(a64, w64), orc.abs_products_f64(a64, w64), k, "bf16")
+    rows = np.arange(m)
+    assert cand[rows, tokens].all() and cand[rows, ref_tokens].all()
+    determined = cand.sum(-1) == 1
+    np.testing.assert_array_equal(tokens[determined], ref_tokens[determined])
+    _say(f"  rows {m}: {int(determined.sum())} determined (equal), {int((~determined).sum())} straddling, "
+         f"{int((tokens != ref_tokens).sum())} differing")
+
+
 # ---------------------------------------------------------------------------
 # Sampled LM head (Sampler.forward without logits: greedy rows + Gumbel-max)
 # ---------------------------------------------------------------------------
@@ -626,11 +742,13 @@ def _sample_temps(m, gen):
 
 @pytest.mark.parametrize("kernel,m,n", SAMPLE_CASES, ids=[f"{L.kernel_name(k)}-M{m}-N{n}" for k, m, n in SAMPLE_CASES])
 @pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-def test_sample_admissible_against_oracle(kernel, m, n, din):
+@pytest.mark.parametrize("rank", ["model", "f32"])
+def test_sample_admissible_against_oracle(kernel, m, n, din, rank):
     """Every token is an admissible winner of the oracle's scores (same
-    Philox noise, float64 logits); greedy rows are exactly the greedy head's
-    token and logit on the same kernel; a sampled row's score is its
-    token's l / T - ln E within the fp32 budget."""
+    Philox noise, float64 logits, rounded to the input type when the head
+    ranks the model dtype); greedy rows are exactly the greedy head's token
+    and logit on the same kernel; a sampled row's score is its token's
+    l / T - ln E within the budget."""
     gen = torch.Generator().manual_seed(m * 13 + n)
     k = 256
     a = torch.randn((m, k), generator=gen).to(din)
@@ -639,8 +757,9 @@ def test_sample_admissible_against_oracle(kernel, m, n, din):
     seed, offset = 0x5EED0000 + m, (3 << 32) | n
     ad, wd, td = a.to(DEV), w.to(DEV), temps.to(DEV)
     _say(f"sample {L.kernel_name(kernel)} {NAME[din]} M={m} N={n}")
-    tokens, scores = G.gemm_sample_with_kernel(ad, wd, td, seed, offset, kernel)
-    g_tokens, g_values = G.gemm_argmax_with_kernel(ad, wd, kernel)
+    ldt = None if rank == "model" else torch.float32
+    tokens, scores = G.gemm_sample_with_kernel(ad, wd, td, seed, offset, kernel, ldt)
+    g_tokens, g_values = G.gemm_argmax_with_kernel(ad, wd, kernel, ldt)
     torch.cuda.synchronize()
     tokens, scores = tokens.cpu().numpy(), scores.cpu().numpy()
     greedy = (temps <= 1e-10).numpy()
@@ -648,11 +767,23 @@ def test_sample_admissible_against_oracle(kernel, m, n, din):
     np.testing.assert_array_equal(scores[greedy], g_values.cpu().numpy()[greedy])
     a64, w64 = a.double().numpy(), w.double().numpy()
     r = orc.gemm_f64(a64, w64)
+    s = orc.abs_products_f64(a64, w64)
     e = orc.sample_exponential(orc.sample_uniform(m, n, seed, offset))
-    ok = orc.sample_token_admissible(tokens, r, orc.abs_products_f64(a64, w64), k, temps.numpy(), e)
+    ldn = NAME[din] if rank == "model" else "f32"
+    ok = orc.sample_token_admissible(tokens, r, s, k, temps.numpy(), e, ldn)
     assert ok.all(), f"rows {np.flatnonzero(~ok)[:8]}"
-    sc = orc.sample_scores_f64(r, temps.numpy(), e)[np.arange(m), tokens]
-    np.testing.assert_allclose(scores[~greedy], sc[~greedy], rtol=1e-5, atol=1e-3)
+    rows = np.arange(m)
+    if rank == "model":
+        # the score of the token lies between its lowest and highest
+        # possible rounded-logit scores (plus the fp32 score budget)
+        lo, hi = orc.rounded_logit_bounds(r, s, k, ldn)
+        sc_lo = orc.sample_scores_f64(lo, temps.numpy(), e)[rows, tokens]
+        sc_hi = orc.sample_scores_f64(hi, temps.numpy(), e)[rows, tokens]
+        slack = 1e-5 * (1 + np.abs(sc_hi))
+        assert ((scores >= sc_lo - slack) & (scores <= sc_hi + slack))[~greedy].all()
+    else:
+        sc = orc.sample_scores_f64(r, temps.numpy(), e)[rows, tokens]
+        np.testing.assert_allclose(scores[~greedy], sc[~greedy], rtol=1e-5, atol=1e-3)
 
 
 @pytest.mark.parametrize("kernel,m", [(L.KERNEL_SPLITK_DECODE, 32), (L.KERNEL_MFMA_STAGED, 64)],

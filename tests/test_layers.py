@@ -61,7 +61,9 @@ def test_merged_and_qkv_loaders():
     assert torch.equal(qkv(x), F.linear(x, torch.cat([q, k, v])))
 
 
-def test_lm_head_last_indices_and_fp32_logits():
+def test_lm_head_last_indices_and_logits_dtype():
+    """The head's logits are the reference's (F.linear in the model dtype,
+    embed_head.py:61) unless fp32 logits are asked for."""
     head = Lyr.ParallelLMHead(100, 16)
     w = torch.randn(100, 16).bfloat16()
     head.weight.data = torch.empty(100, 16, dtype=torch.bfloat16)
@@ -70,7 +72,11 @@ def test_lm_head_last_indices_and_fp32_logits():
     x = torch.randn(7, 16).bfloat16()
     last = torch.tensor([2, 6])
     logits = head(x, last)
-    assert logits.shape == (2, 100) and logits.dtype == torch.float32
+    assert logits.shape == (2, 100) and logits.dtype == torch.bfloat16
+    assert torch.equal(logits, F.linear(x[last], w))
+    head.logits_dtype = torch.float32
+    logits = head(x, last)
+    assert logits.dtype == torch.float32
     assert torch.equal(logits, F.linear(x[last], w).float())
 
 

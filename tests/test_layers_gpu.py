@@ -49,6 +49,8 @@ def test_layers_hip_match_op():
 
 @pytest.mark.parametrize("m", [1, 8, 300])
 def test_lm_head_fp32_logits(m):
+    """The fp32-logit opt-in of the LM head: the GEMM writes fp32 logits
+    within the fp32 bound of the float64 product."""
     gen = torch.Generator().manual_seed(22)
     vocab, hidden = 151936, 1024
     head = Lyr.ParallelLMHead(vocab, hidden)
@@ -56,6 +58,7 @@ def test_lm_head_fp32_logits(m):
         head.weight.copy_(torch.randn(vocab, hidden, generator=gen) * 0.02)
     head = head.to(DEV, torch.bfloat16)
     head.gemm_backend = "hip"
+    head.logits_dtype = torch.float32
     x = torch.randn(m + 3, hidden, generator=gen).bfloat16()
     last = torch.arange(m) + 3
     with torch.inference_mode():        # the reference runs its model in inference mode
@@ -189,15 +192,24 @@ def test_qwen35_mlp_fused_graph_capture(m):
 @pytest.mark.parametrize("m", [1, 8, 32])
 def test_lm_head_greedy_hip(m):
     """ParallelLMHead.greedy on the HIP path equals the argmax of the head's
-    own fp32 logits (same kernel configuration for the Qwen3.5 vocabulary)."""
+    own logits (bf16 by default, as the reference's F.linear returns them;
+    fp32 when opted in), from the same kernel configuration for the Qwen3.5
+    vocabulary."""
     gen = torch.Generator().manual_seed(80 + m)
     head = _init(Lyr.ParallelLMHead(151936, 1024), gen).to(DEV, torch.bfloat16)
     head.gemm_backend = "hip"
     x = torch.randn(m + 3, 1024, generator=gen).bfloat16().to(DEV)
     last = torch.arange(m, device=DEV) + 3
+    head.logits_dtype = torch.float32
+    t32, v32 = head.greedy(x, last)
+    l32 = head(x, last)
+    head.logits_dtype = None
     tokens, values = head.greedy(x, last)
     logits = head(x, last)
     torch.cuda.synchronize()
+    assert logits.dtype == torch.bfloat16 and l32.dtype == torch.float32
+    assert torch.equal(t32, l32.argmax(-1)) and torch.equal(v32, l32.gather(-1, t32[:, None]).squeeze(-1))
+    logits = logits.float()
     assert torch.equal(tokens, logits.argmax(-1))
     assert torch.equal(values, logits.gather(-1, tokens[:, None]).squeeze(-1))
 
@@ -208,8 +220,12 @@ def test_lm_head_sample_hip(m):
     """ParallelLMHead.sample on the HIP path (Qwen3.5 vocabulary): greedy
     rows equal ParallelLMHead.greedy, sampled rows are admissible draws for
     the oracle's noise (checked on the oracle's float64 logits of the head's
-    own bf16 weights), and the torch backend (the reference Sampler on the
-    logits) agrees on the greedy rows."""
+    own bf16 weights, rounded to bf16 as the reference's logits are), and
+    the torch backend (the reference Sampler on torch's bf16 logits) returns
+    the same greedy token on every row whose token the oracle fixes whatever
+    the fp32 summation order (one candidate); on a row whose top logits
+    straddle a bf16 rounding boundary within the accumulation bound both
+    tokens must be candidates."""
     gen = torch.Generator().manual_seed(90 + m)
     head = _init(Lyr.ParallelLMHead(151936, 1024), gen).to(DEV, torch.bfloat16)
     head.gemm_backend = "hip"
@@ -227,16 +243,20 @@ def test_lm_head_sample_hip(m):
     assert t_scores is None
     assert torch.equal(tokens.cpu()[greedy], g_tokens.cpu()[greedy])
     assert ((t_tokens >= 0) & (t_tokens < 151936)).all()
-    # The torch path's logits come out of a bf16 GEMM: its greedy tokens are
-    # the best up to one bf16 rounding of the logit.
-    best = logits[greedy].max(-1).values
-    picked = logits[greedy].gather(-1, t_tokens.cpu()[greedy][:, None]).squeeze(-1)
-    assert (picked >= best - best.abs() * 2.0 ** -7).all()
+    assert logits.dtype == torch.bfloat16          # the reference's model-dtype logits
     a64 = x.double().cpu().numpy()
     w64 = head.weight.double().cpu().numpy()
     r = orc.gemm_f64(a64, w64)
+    s = orc.abs_products_f64(a64, w64)
+    cand = orc.rounded_greedy_candidates(r[greedy.numpy()], s[greedy.numpy()], 1024, "bf16")
+    ours, theirs = tokens.cpu()[greedy].numpy(), t_tokens.cpu()[greedy].numpy()
+    rows = np.arange(len(ours))
+    assert cand[rows, ours].all() and cand[rows, theirs].all()
+    one = cand.sum(-1) == 1
+    np.testing.assert_array_equal(ours[one], theirs[one])
+    print(f"greedy rows {len(ours)}: {int(one.sum())} with one candidate, {int((~one).sum())} straddling", flush=True)
     e = orc.sample_exponential(orc.sample_uniform(m, 151936, seed, offset))
-    ok = orc.sample_token_admissible(tokens.cpu().numpy(), r, orc.abs_products_f64(a64, w64), 1024, temps.numpy(), e)
+    ok = orc.sample_token_admissible(tokens.cpu().numpy(), r, s, 1024, temps.numpy(), e, "bf16")
     assert ok.all()
 
 

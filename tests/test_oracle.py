@@ -377,6 +377,85 @@ def test_greedy_tokens_first_index_on_ties_and_admissible():
     assert not orc.greedy_token_admissible(np.array([0, 1]), r, s, k).any()    # clearly smaller logits are not
 
 
+@pytest.mark.parametrize("dtype,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16)])
+def test_rounded_greedy_candidates_exact_logits_match_torch(dtype, tdt):
+    """With exact logits (zero accumulation bound) there is one candidate
+    per row: torch's argmax of the logits converted to the model dtype and
+    read back as float32 (the reference's F.linear output and Sampler's
+    .float().argmax(-1)).  The logits are float32 values, so torch's
+    conversion rounds once.  Many rows hold values that differ in fp32 but
+    tie once rounded, where the first index must win."""
+    gen = torch.Generator().manual_seed(3)
+    base = torch.randn(64, 300, generator=gen) * 3
+    # near-ties: copies of each row's best value nudged by less than a
+    # rounding step, placed before and after it
+    best = base.argmax(-1)
+    for i in range(64):
+        v = float(base[i, best[i]])
+        base[i, (int(best[i]) + 7) % 300] = v * (1 - 2.0 ** -12)
+        base[i, (int(best[i]) + 150) % 300] = v * (1 + 2.0 ** -13)
+    r32 = base.numpy().astype(np.float32)
+    cand = orc.rounded_greedy_candidates(r32.astype(np.float64), np.zeros_like(r32, dtype=np.float64), 1024, dtype)
+    assert (cand.sum(-1) == 1).all()
+    want = torch.from_numpy(r32).to(tdt).float().argmax(-1).numpy()
+    np.testing.assert_array_equal(cand.argmax(-1), want)
+    # ranking the fp32 values instead picks another column on some rows
+    assert (r32.argmax(-1) != want).any()
+
+
+def test_first_argmax_candidates_brute_force():
+    """Every column the candidate mask admits is reached by its extremal
+    assignment (that logit at its top, every other at its bottom), every
+    assignment drawn inside the intervals picks an admitted column, and a
+    column the mask rejects is never picked."""
+    rng = np.random.default_rng(5)
+    for trial in range(300):
+        n = int(rng.integers(1, 7))
+        lo = rng.integers(-4, 5, size=(1, n)).astype(np.float64) / 4
+        hi = lo + rng.integers(0, 3, size=(1, n)) / 4
+        mask = orc.first_argmax_candidates(lo, hi)[0]
+        for j in range(n):
+            if mask[j]:
+                x = lo[0].copy()
+                x[j] = hi[0, j]
+                assert int(np.argmax(x)) == j, (lo, hi, j)
+        grid = [np.unique(np.concatenate([[lo[0, c], hi[0, c]], np.arange(lo[0, c], hi[0, c], 0.25)]))
+                for c in range(n)]
+        for _ in range(40):
+            x = np.array([rng.choice(g) for g in grid])
+            assert mask[int(np.argmax(x))], (lo, hi, x)
+
+
+def test_rounded_greedy_candidates_catch_planted_mistakes():
+    """The tie rule (first index), the rounding type and the accumulation
+    bound each change the candidate set on constructed rows."""
+    # bf16 spacing at 2.0 is 2^-6: 2.0 and 2.0 + 2^-8 round to the same value
+    r = np.array([[1.0, 2.0, 2.0 + 2.0 ** -8, -1.0]])
+    s = np.zeros_like(r)
+    cand = orc.rounded_greedy_candidates(r, s, 1024, "bf16")
+    np.testing.assert_array_equal(cand[0], [False, True, False, False])     # first index of the tie
+    last_index = np.flatnonzero(orc.to_f64(orc.round_f64(r, "bf16"), "bf16")[0] == 2.0)[-1]
+    assert not cand[0, last_index]                                            # the last-index rule would differ
+    cand16 = orc.rounded_greedy_candidates(r, s, 1024, "f16")                # f16 resolves the pair
+    np.testing.assert_array_equal(cand16[0], [False, False, True, False])
+    # a bound wide enough to cross a rounding boundary admits the other column
+    wide = orc.rounded_greedy_candidates(r, np.full_like(r, 1.0e3), 1024, "bf16")   # bound 0.061
+    assert wide[0, 1] and wide[0, 2]
+
+
+def test_sample_admissibility_rounded_logits():
+    """With model-dtype logits a column whose exact score is slightly lower
+    but whose rounded logit ties the best is admissible; one a full rounding
+    step below is not."""
+    r = np.array([[0.0, 2.0 + 2.0 ** -8, 2.0, 2.0 - 2.0 ** -5]])
+    s = np.zeros_like(r)
+    temps = np.array([0.5], dtype=np.float32)
+    e = np.ones_like(r)
+    assert orc.sample_token_admissible(np.array([2]), r, s, 1024, temps, e, "bf16").all()
+    assert not orc.sample_token_admissible(np.array([2]), r, s, 1024, temps, e).any()    # fp32 ranking
+    assert not orc.sample_token_admissible(np.array([3]), r, s, 1024, temps, e, "bf16").any()
+
+
 # ---------------------------------------------------------------------------
 # Sampled LM head: Philox noise and the Gumbel-max form of Sampler.forward
 # ---------------------------------------------------------------------------
