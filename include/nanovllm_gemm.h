@@ -210,6 +210,25 @@ int nanovllm_gemm_argmax(const void* a, const void* w,
                          void* workspace, int64_t workspace_bytes,
                          void* stream);
 
+/*
+ * nanovllm_gemm_argmax without a workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  The partial keys go to a scratch array the library holds in
+ * device memory: 8 MiB per device (1 << 23 bytes), enough for every
+ * problem whose nanovllm_gemm_argmax_workspace_bytes() is at most that
+ * (the 151936-entry vocabulary up to m = 512); larger problems return
+ * NANOVLLM_GEMM_EINVAL before anything is launched.  Calls no allocator.
+ * Every call on one device shares that device's array: calls that overlap
+ * on one device (two streams, two threads) race and must be ordered by the
+ * caller.  Same arguments and results as nanovllm_gemm_argmax otherwise.
+ */
+int nanovllm_gemm_argmax_noalloc(const void* a, const void* w,
+                                 int64_t* tokens, float* max_logits,
+                                 int64_t m, int64_t n, int64_t k,
+                                 int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
+                                 void* stream);
+
 /* Workspace bytes nanovllm_gemm_argmax needs for this problem (enough for
  * any kernel that can run it), or a negative code.  Pure host function. */
 int64_t nanovllm_gemm_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k,

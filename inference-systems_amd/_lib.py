@@ -47,6 +47,7 @@ SIGNATURES = {
                                                   _INT, _VP]),
     "nanovllm_gemm_silu_mul_select": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT]),
     "nanovllm_gemm_argmax": (_INT, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _VP, _I64, _VP]),
+    "nanovllm_gemm_argmax_noalloc": (_INT, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _VP]),
     "nanovllm_gemm_argmax_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _INT]),
     "nanovllm_gemm_argmax_with_kernel": (_INT, [_INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT,
                                                 _VP, _I64, _VP]),

@@ -623,6 +623,28 @@ int nanovllm_gemm_argmax_with_kernel(int kernel_id, const void* a, const void* w
                              workspace, workspace_bytes, stream);
 }
 
+int nanovllm_gemm_argmax_noalloc(const void* a, const void* w, int64_t* tokens, float* max_logits, int64_t m,
+                                 int64_t n, int64_t k, int64_t lda, int64_t ldw, int dtype_in, int logit_dtype,
+                                 void* stream) {
+    nvg::g_last_error.clear();
+    int rc = nvg::validate_argmax(m, n, k, lda, ldw, dtype_in);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    rc = nvg::validate_logit_dtype(dtype_in, logit_dtype);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    const int64_t need = nvg::argmax_workspace_bytes(m, n);
+    if (need > nvg::kArgmaxScratchBytes)
+        return nvg::set_error(NANOVLLM_GEMM_EINVAL,
+                              "argmax_noalloc: this problem needs %lld bytes of scratch (m=%lld n=%lld), above the "
+                              "%lld bytes the library holds per device; call nanovllm_gemm_argmax with a workspace",
+                              (long long)need, (long long)m, (long long)n, (long long)nvg::kArgmaxScratchBytes);
+    if (m == 0) return NANOVLLM_GEMM_OK;
+    void* scratch = nullptr;
+    rc = nvg::argmax_scratch(static_cast<hipStream_t>(stream), &scratch);
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    return nvg::argmax_entry(-1, a, w, tokens, max_logits, m, n, k, lda, ldw, dtype_in, logit_dtype, scratch,
+                             nvg::kArgmaxScratchBytes, stream);
+}
+
 int nanovllm_gemm_sample(const void* a, const void* w, const float* temperatures, uint64_t seed, uint64_t offset,
                          int64_t* tokens, float* scores, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldw,
                          int dtype_in, int logit_dtype, void* workspace, int64_t workspace_bytes, void* stream) {

@@ -4,10 +4,24 @@
 // the token id and its logit.  It stands in for Sampler's greedy branch,
 // float_logits.argmax(dim=-1) (nanovllm/layers/sampler.py:8-21), which
 // reads back the [M, vocab] fp32 logits the GEMM wrote.
+#include <mutex>
+
 #include "gemm_common.hpp"
 
 namespace nvg {
 namespace {
+
+// Scratch of the no-allocation greedy head (nanovllm_gemm_argmax_noalloc):
+// the [m, blocks] partial keys live in this file-scope device array instead
+// of a caller workspace.  Each device that runs the entry point holds its
+// own copy, at its own address, until the process ends.  In host code the
+// array's name is only a stand-in for the symbol; kernels get the device
+// address that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint64_t scratch[kArgmaxScratchBytes / sizeof(uint64_t)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
 
 // One workgroup per row; a row's keys are contiguous ([m, blocks]).  Each
 // thread issues kFinalizeUnroll independent loads per round, so up to 10240
@@ -53,6 +67,34 @@ __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(
 }
 
 }  // namespace
+
+int argmax_scratch(hipStream_t stream, void** ptr) {
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess)
+        return set_error(NANOVLLM_GEMM_ELAUNCH, "argmax_noalloc: cannot find the stream's device");
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(NANOVLLM_GEMM_ELAUNCH, "argmax_noalloc: device %d beyond the %d this library tracks",
+                         int(dev), kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        // Resolved once per device, with that device current: every device
+        // has its own copy of the array.
+        int prev = 0;
+        if (hipGetDevice(&prev) != hipSuccess || hipSetDevice(dev) != hipSuccess)
+            return set_error(NANOVLLM_GEMM_ELAUNCH, "argmax_noalloc: cannot select device %d", int(dev));
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t back = hipSetDevice(prev);
+        if (err != hipSuccess || p == nullptr)
+            return set_error(NANOVLLM_GEMM_ELAUNCH, "argmax_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                             int(dev), hipGetErrorString(err));
+        if (back != hipSuccess)
+            return set_error(NANOVLLM_GEMM_ELAUNCH, "argmax_noalloc: cannot restore device %d", prev);
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return NANOVLLM_GEMM_OK;
+}
 
 int launch_argmax_finalize(const uint64_t* keys, int64_t blocks, int64_t m, int64_t* tokens, float* logits,
                            hipStream_t s) {

@@ -418,6 +418,11 @@ int launch_add_norm_prologue(const void* h, int64_t ldh, const void* r, int64_t 
 int launch_argmax_finalize(const uint64_t* keys, int64_t blocks, int64_t m, int64_t* tokens, float* logits,
                            hipStream_t s);
 
+// Bytes of the device scratch array behind nanovllm_gemm_argmax_noalloc, and
+// its address on the device of `stream` (resolved once per device).
+constexpr int64_t kArgmaxScratchBytes = int64_t(8) << 20;
+int argmax_scratch(hipStream_t stream, void** ptr);
+
 // Records a message for nanovllm_gemm_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...);
 

@@ -282,6 +282,21 @@ def test_argmax_logit_dtype(lib, din, logit, ok):
         assert rc_s == L.EINVAL
 
 
+def test_argmax_noalloc_validates_before_launch(lib):
+    """The no-allocation greedy head: the argmax checks, then the bound of
+    its 8 MiB scratch, all before any device call (m = 0 returns at once)."""
+    assert lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, 0, 64, 16, 16, 16, BF16, BF16, None) == L.OK
+    rc = lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, 4, 64, 16, 16, 16, L.F32, F32, None)
+    assert rc == L.EUNSUPPORTED
+    rc = lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, 4, 64, 16, 16, 16, BF16, F16, None)
+    assert rc == L.EINVAL and "logit_dtype" in L.last_error()
+    # the Qwen vocabulary fits up to m = 512 on the staged head's 128 columns per key
+    assert L.argmax_workspace_bytes(512, 151936, 1024, 1024, 1024, BF16) <= 8 << 20
+    assert L.argmax_workspace_bytes(1024, 151936, 1024, 1024, 1024, BF16) > 8 << 20
+    rc = lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, 1024, 151936, 1024, 1024, 1024, BF16, BF16, None)
+    assert rc == L.EINVAL and "scratch" in L.last_error() and "nanovllm_gemm_argmax" in L.last_error()
+
+
 def test_sample_validates_before_launch(lib):
     """The sampled head shares the greedy head's checks and adds its own:
     temperatures must be a non-null, 4-byte aligned device pointer."""
