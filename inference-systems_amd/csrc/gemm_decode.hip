@@ -88,6 +88,12 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     // group 2s + 1 the up rows of the same 16 output columns.
     static_assert(EPI != EPI_SILU_MUL || RG % 2 == 0, "gate/up group pairs");
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;   // 16-column output groups per workgroup
+    // Consecutive column blocks go to consecutive workgroups, which the
+    // hardware hands to the 8 XCDs round robin.  Giving each XCD a contiguous
+    // run of blocks instead (xcd_remap, so the two workgroups writing one
+    // 128-byte output line share an L2) measured 0.3 us slower on every
+    // decode shape (N = 6144, K = 1024, M = 1-64; 1024 x 3584): W streams
+    // better when each XCD's reads spread over the whole matrix.
     const int64_t n0 = int64_t(blockIdx.x) * 16 * OG;         // first output column
     const uint16_t* wsrc[IW];
 #pragma unroll
@@ -442,10 +448,14 @@ int launch_cfg(const Problem& p, hipStream_t s) {
 
 // Configurations measured on MI355X.  AROWS is M rounded up to 8, 16, 32 or
 // 64; "rows" counts the W rows read (2 N for SiLU-and-mul).
-//   * rows < 65536: 32 W rows per 8-wave workgroup, one line per wave in
-//     flight; N = 6144, K = 1024, M = 1 / 4 / 8 / 16 / 32: 4.42 / 4.48 /
-//     4.62 / 4.96 / 5.99 us (the register-loading kernel: 4.91 / 5.15 /
-//     5.42 / 5.87 / 7.25 us).  With at most 2048 rows (N = 1024, K = 3584,
+//   * rows < 65536: 32 W rows per 16-wave workgroup, one line per wave, so
+//     all 16 lines of K = 1024 are in flight at once; N = 6144, K = 1024,
+//     W streamed from HBM, M = 4 / 8 / 16 / 32: 4.54 / 4.57 / 4.81 / 5.58 us
+//     against 4.72 / 4.76 / 4.94 / 5.75 us with 8 waves of two lines each
+//     (and 5.42 / 5.87 / 7.25 us for the register-loading kernel at M = 8 /
+//     16 / 32).  The same W read by a plain streaming kernel takes 3.55 us,
+//     and these copies alone 4.01 us (M = 8) / 4.58 us (M = 32); an empty
+//     kernel costs 1.56 us per graph node.  With at most 2048 rows (N = 1024, K = 3584,
 //     the down and output projections) 16 rows per workgroup give twice the
 //     workgroups, with 16 waves along K up to M = 16 (M = 1 / 16 / 32: 4.7 /
 //     6.6 / 8.5 us, against 7.0 / 9.0 / 11.7 us with 32 rows).
@@ -496,7 +506,11 @@ int launch_rows(const Problem& p, hipStream_t s) {
             else return launch_cfg<DT, DT_OUT, AROWS, 1, 16, 1, 16, EPI, PRO>(p, s);
         }
     }
-    return launch_cfg<DT, DT_OUT, AROWS, 2, 8, 1, 16, EPI, PRO>(p, s);
+    // 16 waves, one line each: every line of a 1024-wide K is in flight at
+    // once.  With 32 rows of A and a prologue operand the copies need 192 KiB
+    // of LDS, so that case keeps 8 waves of two lines.
+    if constexpr (PRO == PRO_NONE || AROWS <= 16) return launch_cfg<DT, DT_OUT, AROWS, 2, 16, 1, 16, EPI, PRO>(p, s);
+    else return launch_cfg<DT, DT_OUT, AROWS, 2, 8, 1, 16, EPI, PRO>(p, s);
 }
 
 template <int DT, int DT_OUT, int EPI, int PRO = PRO_NONE>
