@@ -256,6 +256,78 @@ def test_tolerance_accepts_fp32_accumulation_and_catches_planted_mistakes():
     assert not ok(bad)                                                       # one wrong element
 
 
+def _fp16_down_sample(seed=3, m=48, n=96, k=3584):
+    """Inputs of the fp16 down-projection workload's distributions
+    (A ~ N(0, 0.5), W ~ N(0, 0.02), K = 3584), rounded to fp16."""
+    rng = np.random.default_rng(seed)
+    a = (rng.standard_normal((m, k)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    return a, w
+
+
+def test_narrow_parity_accepts_another_fp32_order():
+    """An fp32 GEMM summing K in another order (numpy's float32 BLAS on the
+    reversed K axis) is within 2 fp16 ulp of torch's fp32 GEMM rounded once
+    on every element but a few cancellations, fewer than the cap."""
+    a, w = _fp16_down_sample()
+    a64, w64 = a.astype(np.float64), w.astype(np.float64)
+    r = orc.gemm_f64(a64, w64)
+    s = orc.abs_products_f64(a64, w64)
+    other = (a[:, ::-1].astype(np.float32) @ w[:, ::-1].astype(np.float32).T).astype(np.float16)
+    ref = (torch.from_numpy(a).float() @ torch.from_numpy(w).float().T).to(torch.float16).numpy()
+    stats = orc.narrow_parity(other, ref, r, s, "f16")
+    assert stats["ok"].all() and stats["max_ulp_checked"] <= 2
+    assert stats["cancel_beyond"] <= orc.cancellation_cap(r.size)
+
+
+def test_narrow_parity_catches_what_the_fraction_rule_passed():
+    """The earlier bar (every element within 2 ulp + the fp32 accumulation
+    bound of the float64 product, and >= 99% within 2 ulp of it) passes a
+    kernel that mis-rounds 0.5% of the fp16 down-projection outputs by 10
+    ulp: the accumulation bound is tens of fp16 ulp at K = 3584.  The
+    elementwise bar against the fp32 reference rejects it."""
+    a, w = _fp16_down_sample()
+    a64, w64 = a.astype(np.float64), w.astype(np.float64)
+    r = orc.gemm_f64(a64, w64)
+    s = orc.abs_products_f64(a64, w64)
+    k = a.shape[1]
+    ref = (torch.from_numpy(a).float() @ torch.from_numpy(w).float().T).to(torch.float16).numpy()
+    bad = ref.copy()
+    tol = orc.gemm_tolerance(r, s, k, "f16")
+    # 0.5% of the outputs, among those (three in four) where 10 ulp is still
+    # inside the old absolute bound
+    rng = np.random.default_rng(0)
+    loose = np.flatnonzero((12 * orc.ulp_at(r, "f16") < tol).reshape(-1))
+    assert loose.size > 0.5 * bad.size
+    idx = rng.choice(loose, size=bad.size // 200, replace=False)
+    flat = bad.reshape(-1).view(np.uint16)
+    flat[idx] = flat[idx] + 10          # 10 fp16 ulp away (same sign, no overflow at these magnitudes)
+    # the old rule passes it
+    assert (np.abs(bad.astype(np.float64) - r) <= tol).all()
+    assert float((orc.ulp_distance(bad, orc.round_f64(r, "f16"), "f16") <= 2).mean()) >= 0.99
+    # the elementwise bar does not: non-cancellation elements beyond 2 ulp,
+    # or more cancellation elements than the cap
+    stats = orc.narrow_parity(bad, ref, r, s, "f16")
+    assert stats["beyond"] >= bad.size // 200
+    assert not stats["ok"].all() or stats["cancel_beyond"] > orc.cancellation_cap(bad.size)
+
+
+def test_narrow_parity_exempts_only_cancellations():
+    """An element whose exact value cancels (|r| under 2^-6 of the sum of
+    its terms' magnitudes) may exceed 2 ulp (its low bits follow the
+    summation order); an ordinary element one step beyond 2 ulp may not."""
+    r = np.array([[1e-4, 1.0]])
+    scale = np.array([[1.0, 1.0]])
+    ref = np.array([[0.0, 1.0]], dtype=np.float16)
+    three_up = np.nextafter(np.nextafter(np.nextafter(np.float16(1.0), np.float16(2)), np.float16(2)), np.float16(2))
+    got = np.array([[np.float16(1e-4), three_up]], dtype=np.float16)
+    stats = orc.narrow_parity(got, ref, r, scale, "f16")
+    assert stats["beyond"] == 2 and stats["cancel_beyond"] == 1
+    np.testing.assert_array_equal(stats["ok"], [[True, False]])
+    assert stats["max_ulp_checked"] == 3
+    assert orc.cancellation_cap(100) == 8 and orc.cancellation_cap(10 ** 6) == 1000
+
+
 def test_rel_frobenius_and_checks():
     ref = np.array([[1.0, 2.0], [3.0, 4.0]])
     assert orc.rel_frobenius(ref, ref) == 0.0

@@ -165,7 +165,12 @@ def _norm_oracle(h, r, nw, w, eps, dtype):
     return y64, scale, res
 
 
-def _check_add_norm(out, res_out, h, r, nw, w, eps, dtype, dout, min_within_2ulp=0.99):
+def _check_add_norm(out, res_out, h, r, nw, w, eps, dtype, dout):
+    """The new residual bit-exact; the output within the oracle's bound of
+    scale * (y w^T) in float64 and, for narrow outputs, every element within
+    2 ulp of the fp32 reference (host fp32 GEMM of the same operand y, times
+    the fp32 row scale, rounded once) but a few cancellation elements
+    (oracle.narrow_parity)."""
     y64, scale, res = _norm_oracle(h, r, nw, w, eps, dtype)
     assert np.array_equal(_store(res_out), res), "new residual differs from round(h + r)"
     w64 = _value(w)
@@ -177,8 +182,14 @@ def _check_add_norm(out, res_out, h, r, nw, w, eps, dtype, dout, min_within_2ulp
     err = np.abs(got - r64)
     assert (err <= tol).all(), f"{int((err > tol).sum())} outside; worst excess {float((err - tol).max()):.3g}"
     if dout != torch.float32:
-        ulps = orc.ulp_distance(_store(out), orc.round_f64(r64, NAME[dout]), NAME[dout])
-        assert float((ulps <= 2).mean()) >= min_within_2ulp
+        y32 = torch.from_numpy(y64.astype(np.float32))
+        scale32 = torch.from_numpy(scale.astype(np.float32))
+        ref32 = (y32 @ torch.from_numpy(w64.astype(np.float32)).T) * scale32[:, None]
+        ref = _store(ref32.to(dout))
+        stats = orc.narrow_parity(_store(out), ref, r64, scale[:, None] * orc.abs_products_f64(y64, w64), NAME[dout])
+        ok = stats.pop("ok")
+        assert ok.all(), f"{int((~ok).sum())} elements beyond 2 ulp of the fp32 reference ({stats})"
+        assert stats["cancel_beyond"] <= orc.cancellation_cap(ok.size), stats
 
 
 NORM_SHAPES = [(6144, 1024), (1000, 1000), (1024, 3584), (3000, 3592)]
