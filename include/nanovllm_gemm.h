@@ -357,8 +357,10 @@ int nanovllm_sigmoid_gate(const void* a, const void* gate, void* out,
  * (one launch, no workspace); otherwise a prologue kernel writes the
  * operand and the row scales to the workspace
  * (nanovllm_gemm_add_rmsnorm_workspace_bytes()) and mfma_staged scales its
- * output rows.  Inputs f16 or bf16 (h, residual, w_norm and w alike), output
- * the input type or f32; 16-byte aligned h, residual, w_norm, w and
+ * output rows.  Inputs bf16 (h, residual, w_norm and w alike; f16 gets
+ * NANOVLLM_GEMM_EUNSUPPORTED, because the unscaled operand s (1 + w_norm)
+ * can leave f16's range where the reference's normalised one does not),
+ * output bf16 or f32; 16-byte aligned h, residual, w_norm, w and
  * residual_out, with k, ldh, ldr, ldres and ldw multiples of 8.
  * Asynchronous, no allocation, capturable. */
 int nanovllm_gemm_add_rmsnorm(const void* h, const void* residual, const void* norm_weight, float eps,

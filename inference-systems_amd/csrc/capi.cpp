@@ -437,9 +437,25 @@ int gated_entry(int forced_kernel, const void* a, const void* gate, const void* 
     return run(kernel, p, s);
 }
 
+// The fused norm rounds s (1 + w) to the input type and applies the row scale
+// rsqrt(mean s^2 + eps) after the GEMM, where the reference rounds the O(1)
+// product s rsqrt(...) (1 + w).  bf16 has fp32's exponent range, so both
+// orders stay finite and normal on any fp32 s; fp16 would overflow where
+// |s (1 + w)| > 65504 and go subnormal on rows of small s, where the
+// reference stays finite and normal.  fp16 is therefore refused.
+int validate_add_norm_dtypes(int din, int dout) {
+    const int rc = validate_prologue_dtypes(din, dout, "gemm_add_rmsnorm");
+    if (rc != NANOVLLM_GEMM_OK) return rc;
+    if (din != NANOVLLM_GEMM_BF16)
+        return set_error(NANOVLLM_GEMM_EUNSUPPORTED,
+                         "gemm_add_rmsnorm takes bfloat16 inputs only: it rounds s*(1+w) before the row scale, "
+                         "which overflows or underflows float16 on rows the reference normalises first");
+    return NANOVLLM_GEMM_OK;
+}
+
 int validate_add_norm(int64_t m, int64_t n, int64_t k, int64_t ldh, int64_t ldr, int64_t ldw, int64_t ldc,
                       int64_t ldres, float eps, int din, int dout) {
-    int rc = validate_prologue_dtypes(din, dout, "gemm_add_rmsnorm");
+    int rc = validate_add_norm_dtypes(din, dout);
     if (rc != NANOVLLM_GEMM_OK) return rc;
     if (m < 0) return set_error(NANOVLLM_GEMM_EINVAL, "m must be non-negative (m=%lld)", (long long)m);
     if (n < 1) return set_error(NANOVLLM_GEMM_EINVAL, "n must be positive (n=%lld)", (long long)n);
@@ -724,7 +740,7 @@ int nanovllm_sigmoid_gate(const void* a, const void* gate, void* out, int64_t m,
 
 int64_t nanovllm_gemm_add_rmsnorm_workspace_bytes(int64_t m, int64_t k, int dtype_in) {
     nvg::g_last_error.clear();
-    const int rc = nvg::validate_prologue_dtypes(dtype_in, dtype_in, "gemm_add_rmsnorm");
+    const int rc = nvg::validate_add_norm_dtypes(dtype_in, dtype_in);
     if (rc != NANOVLLM_GEMM_OK) return rc;
     if (m < 0 || k < 1)
         return nvg::set_error(NANOVLLM_GEMM_EINVAL, "need m >= 0 and k >= 1 (m=%lld k=%lld)", (long long)m,

@@ -15,6 +15,8 @@
         gate_up_proj ``w[2N, K]`` and SiluAndMul (qwen3_5.py:157-159,
         200-203, 117).  residual_out = round(h + residual) as there; the
         per-row scale rsqrt(mean s^2 + eps) is applied to the fp32 sums.
+        bfloat16 inputs only (the unscaled operand s * (1 + w) needs bf16's
+        exponent range).
 
     sigmoid_gate(a, gate) -> round(a * round(sigmoid(gate))), the gate alone.
 
@@ -175,8 +177,11 @@ def add_rmsnorm_contract_reason(h: torch.Tensor, residual: torch.Tensor, norm_we
         return "h, residual, norm_weight and w must be CUDA (HIP) tensors"
     if len({t.device for t in tensors}) != 1:
         return "h, residual, norm_weight and w must be on the same device"
-    if h.dtype not in _HALF:
-        return "the add + RMSNorm GEMM takes float16 or bfloat16 inputs"
+    if h.dtype != torch.bfloat16:
+        # The fused norm rounds s * (1 + w) before the row scale; bf16 holds
+        # that for any fp32 s, fp16 overflows or underflows where the
+        # reference's normalised operand does not.
+        return "the add + RMSNorm GEMM takes bfloat16 inputs"
     if any(t.dtype != h.dtype for t in tensors):
         return "h, residual, norm_weight and w must have the same dtype"
     if out_dtype not in (None, h.dtype, torch.float32):

@@ -332,7 +332,8 @@ def test_prologue_workspace_bytes():
     assert L.gated_workspace_bytes(4, 100, 40, BF16) == L.EINVAL      # group does not divide K
     assert L.gated_workspace_bytes(4, 128, 64, F32) == L.EUNSUPPORTED
     assert L.add_rmsnorm_workspace_bytes(32, 1024, BF16) == 32 * 2048 + 256
-    assert L.add_rmsnorm_workspace_bytes(33, 1000, F16) == (33 * 2000 + 255) // 256 * 256 + 256
+    assert L.add_rmsnorm_workspace_bytes(33, 1000, BF16) == (33 * 2000 + 255) // 256 * 256 + 256
+    assert L.add_rmsnorm_workspace_bytes(33, 1000, F16) == L.EUNSUPPORTED
     assert L.add_rmsnorm_workspace_bytes(-1, 1024, BF16) == L.EINVAL
 
 
@@ -384,6 +385,9 @@ def test_add_rmsnorm_validates_before_launch(lib):
     assert rc == L.EUNSUPPORTED and "aligned" in L.last_error()
     rc = call(d, d, d, 1e-6, d, d, d, 4, 64, 512, 512, 512, 512, 64, 512, 0, BF16, F16, None, 0, None)
     assert rc == L.EUNSUPPORTED and "dtype" in L.last_error()
+    # fp16 is refused: the unscaled operand s (1 + w) can leave its range
+    rc = call(d, d, d, 1e-6, d, d, d, 4, 64, 512, 512, 512, 512, 64, 512, 0, F16, F16, None, 0, None)
+    assert rc == L.EUNSUPPORTED and "bfloat16 inputs only" in L.last_error()
     rc = call(d, d, d, 1e-6, d, d, d, 40, 64, 512, 512, 512, 512, 64, 512, 0, BF16, BF16, None, 0, None)
     assert rc == L.EINVAL and "workspace" in L.last_error()
     rc = lib.nanovllm_gemm_add_rmsnorm_with_kernel(L.KERNEL_SPLITK_DECODE, d, d, d, 1e-6, d, d, d, 40, 64, 512,

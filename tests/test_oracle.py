@@ -696,6 +696,27 @@ def test_add_norm_operand_and_scale_by_hand():
     assert orc.norm_scale_f64(np.zeros((1, 8)), 1e-6)[0] == 1.0 / math.sqrt(1e-6)
 
 
+def test_add_norm_operand_order_needs_bf16_range():
+    """Why the fused norm takes bf16 only: its operand s (1 + w) is rounded
+    before the row scale.  With |s| ~ 2e4 and 1 + w = 4 that is 8e4, beyond
+    fp16's 65504, and a row of s ~ 1e-6 lands in fp16's subnormals, while the
+    reference's operand s rsqrt(mean s^2 + eps) (1 + w) (layernorm.py:126-130)
+    is a finite, normal fp16 number on both rows.  In bf16 (fp32's exponent range) both orders stay
+    finite and normal."""
+    s = np.array([[2.0e4, -1.5e4, 1.0e4, 2.0e4], [1.0e-6, -2.0e-6, 1.5e-6, 1.0e-6]], dtype=np.float32)
+    w = np.full(4, 3.0, dtype=np.float32)                       # 1 + w = 4
+    zero = np.zeros_like(s)
+    _, y16, _ = orc.add_norm_operand(s.astype(np.float16), zero.astype(np.float16), w.astype(np.float16), "f16")
+    assert np.isinf(orc.to_f64(y16[0], "f16")).any()              # overflow on the large row
+    tiny = np.abs(orc.to_f64(y16[1], "f16"))
+    assert (tiny < 2.0 ** -14).all() and (tiny > 0).all()         # subnormal on the small row
+    ref = s.astype(np.float64) * orc.norm_scale_f64(s, 1e-6)[:, None] * 4.0
+    assert (np.abs(ref) >= 2.0 ** -14).all() and (np.abs(ref) < 65504).all()   # normal, finite fp16
+    _, yb, _ = orc.add_norm_operand(orc.encode(s, "bf16"), orc.encode(zero, "bf16"), orc.encode(w, "bf16"), "bf16")
+    yb64 = np.abs(orc.to_f64(yb, "bf16"))
+    assert np.isfinite(yb64).all() and (yb64 >= 2.0 ** -126).all()
+
+
 def test_add_norm_residual_matches_reference_and_gemm_close():
     """Qwen3_5RMSNorm.forward(h, residual) in torch (layernorm.py:131-142):
     the new residual is the oracle's bit for bit; normalized @ W^T of the

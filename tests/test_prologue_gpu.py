@@ -197,8 +197,8 @@ NORM_SHAPES = [(6144, 1024), (1000, 1000), (1024, 3584), (3000, 3592)]
 
 @pytest.mark.parametrize("n,k", NORM_SHAPES, ids=[f"N{n}-K{k}" for n, k in NORM_SHAPES])
 @pytest.mark.parametrize("m", [1, 7, 16, 32])
-@pytest.mark.parametrize("dtype,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
-                         ids=["bf16", "f16-f32"])
+@pytest.mark.parametrize("dtype,dout", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32)],
+                         ids=["bf16", "bf16-f32"])
 def test_add_rmsnorm_fused(n, k, m, dtype, dout):
     gen = torch.Generator().manual_seed(n + k + m)
     h, r, nw, w = _norm_inputs(m, n, k, dtype, gen)
