@@ -6,6 +6,13 @@ file.  The library is loaded with ctypes by ``_lib.py``; it has no
 dependency on torch.
 
 Usage: ``python inference-systems_amd/build.py`` or ``build()`` from Python.
+
+``build(sanitize=True, out=path)`` (``build.py --sanitize PATH``) builds a
+copy whose host code in capi.cpp (argument validation, the selection table,
+workspace sizes, error reporting) carries AddressSanitizer and
+UndefinedBehaviorSanitizer; device code is built as usual.  It is loaded
+through ``NANOVLLM_GEMM_LIB`` with the sanitizer runtime preloaded
+(``sanitizer_runtime()``), for the CPU tests of the C ABI.
 """
 from __future__ import annotations
 
@@ -46,6 +53,28 @@ SOURCES = [
 ]
 
 
+# Host-only sanitizers for capi.cpp: each -fsanitize= goes to the host pass
+# alone (-Xarch_host), so no GPU code is instrumented.
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-g",
+]
+SANITIZED_SOURCES = ("capi.cpp",)
+
+
+def sanitizer_runtime() -> Path:
+    """The ASan runtime of the ROCm clang that built the sanitized library
+    (it carries the UBSan handlers too); preloaded into the Python that loads it."""
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    found = sorted((rocm / "llvm" / "lib" / "clang").glob("*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not found:
+        raise RuntimeError("libclang_rt.asan-x86_64.so not found under the ROCm clang")
+    return found[-1]
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     path = Path(rocm) / "bin" / "hipcc"
@@ -70,9 +99,16 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+def build(verbose: bool = False, extra_flags: list[str] | None = None, sanitize: bool = False,
+          out: Path | None = None) -> Path:
+    """Compile every source and link the shared library; returns its path.
+
+    sanitize: capi.cpp's host code with ASan + UBSan (needs `out`, so the
+    in-tree library is never replaced by an instrumented one)."""
     extra = list(extra_flags or [])
+    if sanitize and out is None:
+        raise ValueError("a sanitized build needs an output path outside the package")
+    target = Path(out) if out is not None else LIB_PATH
     with tempfile.TemporaryDirectory(prefix="nvgemm_build_") as tmp:
         tmpdir = Path(tmp)
         jobs = []
@@ -80,23 +116,30 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
             for name in SOURCES:
                 src = CSRC / name
                 obj = tmpdir / (name + ".o")
-                jobs.append((obj, pool.submit(_compile, src, obj, extra)))
+                flags = extra + (SANITIZE_FLAGS if sanitize and name in SANITIZED_SOURCES else [])
+                jobs.append((obj, pool.submit(_compile, src, obj, flags)))
             for _, fut in jobs:
                 fut.result()
         out_tmp = tmpdir / LIB_NAME
+        # A sanitized library leaves the runtime's symbols undefined: the
+        # runtime is preloaded into the process that loads it.
         cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(out_tmp),
                *[str(o) for o, _ in jobs]]
         proc = subprocess.run(cmd, capture_output=True, text=True)
         if proc.returncode != 0:
             raise RuntimeError(f"link failed:\n{proc.stderr}")
         # Replace atomically so a process that has the old file mapped keeps it.
-        final_tmp = LIB_PATH.with_suffix(".so.tmp")
+        target.parent.mkdir(parents=True, exist_ok=True)
+        final_tmp = target.with_suffix(".so.tmp")
         shutil.copyfile(out_tmp, final_tmp)
-        os.replace(final_tmp, LIB_PATH)
+        os.replace(final_tmp, target)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {target}")
+    return target
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    if len(sys.argv) == 3 and sys.argv[1] == "--sanitize":
+        build(verbose=True, sanitize=True, out=Path(sys.argv[2]))
+    else:
+        build(verbose=True)
