@@ -65,6 +65,9 @@ def parse_args():
     p.add_argument("--m", type=int, default=None, help="M of --workload (default: its largest)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run 10 device copies of MIB MiB (reference kernel for HBM counter scaling)")
+    p.add_argument("--probes", action="store_true",
+                   help="only run the microbenchmarks of the hardware ceilings (launch floor, streaming read, LDS "
+                        "reads, global -> LDS copies, MFMA rate, clocks) and print them as one JSON line")
     p.add_argument("--matrix", action="store_true",
                    help="only run the reference's shape matrix (fp16 and bf16 over its Qwen3.5 shapes) and print "
                         "it as CSV")
@@ -187,6 +190,47 @@ def benchmark_ms(torch, launch, warmup: int, repeats: int, trials: int = 7) -> t
         ramp += timer.time_ms()
     graph = sorted(timer.time_ms() / repeats for _ in range(trials))[trials // 2]
     return graph, plain
+
+
+def run_probes(torch) -> int:
+    """The hardware ceilings the GEMM kernels are measured against, measured
+    on this box (inference-systems_amd/probes.py, csrc/probes.hip)."""
+    import importlib
+
+    P = importlib.import_module("inference_systems_amd.probes")
+    P.load()
+    out = {"probes": "MI355X ceilings on this box", "cus": P.CUS}
+    # Clocks ramp under load: run the MFMA probe for ~0.3 s first.
+    for _ in range(60):
+        P.mfma_rate(torch, iters=512)
+    out["launch_floor"] = P.launch_floor(torch)
+    log(f"launch floor: {out['launch_floor']}")
+    out["mfma_bf16_32x32x16"] = [P.mfma_rate(torch, workgroups=w) for w in (P.CUS, 2 * P.CUS)]
+    log(f"mfma: {out['mfma_bf16_32x32x16']}")
+    out["lds_read_b128"] = [P.lds_read(torch, workgroups=w) for w in (P.CUS, 2 * P.CUS)]
+    log(f"lds reads: {out['lds_read_b128']}")
+    # Copies from a window small enough for the vector L1 (16 KiB), for L2
+    # (256 KiB and 4 MiB, read by every CU of an XCD), one workgroup per CU.
+    # With three 1 KiB fragment reads per copied KiB (about a GEMM K-tile's
+    # mix): whether the LDS serves the copies' writes and the reads at once.
+    out["copy"] = [P.copy_rate(torch, mode, workgroups=P.CUS, inflight=f, window=win, reads=r)
+                   for win in (16 << 10, 4 << 20) for mode in (0, 1, 2) for f in (8, 16) for r in (0, 3)
+                   if mode != 1 or r == 0]
+    for r in out["copy"]:
+        log(f"copy: {r}")
+    # The C tiles of the bf16 prefill headline (2048 x 4096, 16.8 MB), written
+    # by 256 workgroups at once as its epilogue does, one buffer and 16 in
+    # rotation (past the Infinity Cache).
+    out["write_c_tiles"] = [P.write_tiles(torch, nontemporal=nt, copies=c) for nt in (True, False) for c in (1, 16)]
+    log(f"write C tiles: {out['write_c_tiles']}")
+    decode_w = 6144 * 1024 * 2
+    out["stream_read_decode_w"] = P.stream_read(torch, decode_w, math.ceil(2 * INFINITY_CACHE_BYTES / decode_w) + 1)
+    log(f"stream read 12.6 MB: {out['stream_read_decode_w']}")
+    head_w = 151936 * 1024 * 2
+    out["stream_read_lm_head_w"] = P.stream_read(torch, head_w, 2, per_lane_list=(1, 4), reps_per_copy=2)
+    log(f"stream read 311 MB: {out['stream_read_lm_head_w']}")
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 def reference_inputs(torch, m: int, n: int, k: int):
@@ -315,6 +359,9 @@ def main() -> int:
     L = pkg._lib
     L.load()                      # raises if the HIP library is not built
     W = pkg.workloads
+    if args.probes:
+        torch.cuda.set_device(0)
+        return run_probes(torch)
     if args.matrix:
         torch.cuda.set_device(0)
         rows = reference_matrix(torch, L, W, emit=lambda line: print(line, flush=True))

@@ -31,6 +31,9 @@ LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.
+# -amdgpu-kernarg-preload-count=16: the first 16 SGPRs of kernel arguments
+# arrive preloaded, so a kernel's first copies wait for no argument load
+# (the kernels put the arguments those copies need first).
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -39,6 +42,7 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 SOURCES = [
@@ -51,6 +55,11 @@ SOURCES = [
     "gemm_argmax.hip",
     "gemm_prologue.hip",
 ]
+
+# The microbenchmarks behind `bench.py --probes`: a library of their own, so
+# the GEMM library carries only the product's entry points.
+PROBE_SOURCES = ["probes.hip"]
+PROBE_LIB_PATH = PKG_DIR / "libnanovllm_probes.so"
 
 
 # Host-only sanitizers for capi.cpp: each -fsanitize= goes to the host pass
@@ -135,7 +144,28 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, sanitize:
         os.replace(final_tmp, target)
     if verbose:
         print(f"built {target}")
+    if not sanitize and out is None:
+        build_probes(verbose=verbose, extra_flags=extra)
     return target
+
+
+def build_probes(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
+    """Compile the microbenchmark library (libnanovllm_probes.so)."""
+    with tempfile.TemporaryDirectory(prefix="nvgemm_probes_") as tmp:
+        out_tmp = Path(tmp) / PROBE_LIB_PATH.name
+        cmd = [hipcc(), "-x", "hip", *HIP_FLAGS, *(extra_flags or []), "-shared", "-o", str(out_tmp),
+               *[str(CSRC / name) for name in PROBE_SOURCES]]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        noise = "'-packed-fp32-ops' is not a recognized feature"
+        err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed for the probes:\n{err}")
+        final_tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
+        shutil.copyfile(out_tmp, final_tmp)
+        os.replace(final_tmp, PROBE_LIB_PATH)
+    if verbose:
+        print(f"built {PROBE_LIB_PATH}")
+    return PROBE_LIB_PATH
 
 
 if __name__ == "__main__":

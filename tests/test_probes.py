@@ -1,0 +1,37 @@
+"""CPU tests of the microbenchmark library behind ``bench.py --probes``: it
+loads, and every entry point refuses sizes it would read or write out of
+bounds before launching anything (no GPU is touched here)."""
+from __future__ import annotations
+
+import importlib
+
+from conftest import PKG  # noqa: F401  (registers the package)
+
+P = importlib.import_module("inference_systems_amd.probes")
+
+
+def test_probe_library_loads_with_every_entry_point():
+    lib = P.load()
+    for name in P._SIGS:
+        assert hasattr(lib, name), name
+
+
+def test_probes_refuse_unsafe_sizes_before_launch():
+    lib = P.load()
+    assert lib.nvprobe_empty(0, None) == -1
+    # the buffer must be exactly workgroups x 256 lanes x loads x 16 bytes
+    assert lib.nvprobe_stream_read(None, 4096 * 16 + 16, 16, 1, None, None, None) == -1
+    assert lib.nvprobe_stream_read(None, 4096 * 16, 16, 3, None, None, None) == -1
+    assert lib.nvprobe_stream_read(None, 0, 0, 1, None, None, None) == -1
+    assert lib.nvprobe_lds_read(256, 12, None, None, None) == -1
+    assert lib.nvprobe_lds_read(0, 16, None, None, None) == -1
+    # copy window: a positive multiple of 1 KiB; in-flight 8 or 16; iterations a multiple of it
+    assert lib.nvprobe_copy(0, None, 1000, 256, 64, 8, 0, None, None, None) == -1
+    assert lib.nvprobe_copy(0, None, 4096, 256, 64, 4, 0, None, None, None) == -1
+    assert lib.nvprobe_copy(0, None, 4096, 256, 60, 8, 0, None, None, None) == -1
+    assert lib.nvprobe_copy(0, None, 4096, 256, 64, 8, 2, None, None, None) == -1
+    assert lib.nvprobe_copy(3, None, 4096, 256, 64, 8, 0, None, None, None) == -1
+    assert lib.nvprobe_mfma(256, 16, 3, None, None, None) == -1
+    # each 128-row tile writes 512 bytes per row: ld must cover tiles_n of them
+    assert lib.nvprobe_write_tiles(None, 8192 - 16, 16, 16, 1, None, None) == -1
+    assert lib.nvprobe_write_tiles(None, 8192 + 8, 16, 16, 1, None, None) == -1
