@@ -258,10 +258,12 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
     * every output is compared to the exact product (an fp64 GEMM, exact on
       these inputs) as compare does: max |error|, and pass if every error is
       within 5e-2 + 1e-2 |ref| and finite (gemm_bench.cu:225-250);
-    * direct_* is mfma_direct on the reference's B[K,N] layout, staged_*
-      mfma_staged and dispatch_* the kernel the selection table picks, both
-      on the same matrix in the W[N,K] (nn.Linear) layout the library's
-      fast kernels read;
+    * direct_*, staged_* and dispatch_* run on the reference's B[K,N]
+      layout, as its columns do: mfma_direct, mfma_staged (B transposed in
+      registers on its way to LDS) and the kernel the selection table picks
+      for B[K,N]; the *_nk columns after the reference's run the same
+      matrix transposed into the W[N,K] (nn.Linear) layout, where the decode
+      kernels (gemv_decode, splitk_decode) also apply;
     * timing as benchmark_ms: 10 warm-up launches, repeats =
       clamp(2e10 / flops, 10, 200), median of 7 trials (gemm_bench.cu:371-379),
       each group of repeats replayed as one HIP graph (these kernels run for
@@ -273,7 +275,8 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
     cols = ["dtype", "label", "M", "N", "K", "repeats", "vendor_ms", "vendor_tflops", "direct_ms", "direct_tflops",
             "staged_ms", "staged_tflops", "vendor_max_abs", "direct_max_abs", "staged_max_abs", "dispatch",
             "dispatch_ms", "dispatch_tflops", "dispatch_max_abs", "dispatch_vs_vendor", "status",
-            "dispatch_plain_launch_ms"]
+            "dispatch_plain_launch_ms", "staged_nk_ms", "staged_nk_max_abs", "dispatch_nk", "dispatch_nk_ms",
+            "dispatch_nk_max_abs", "dispatch_nk_plain_launch_ms"]
     emit(",".join(cols))
     rows = []
     for dt, dname in dtypes or ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
@@ -318,12 +321,15 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
                 vendor_ms, vendor_err, _ = run(vendor, ref)
             except RuntimeError:   # no fp32-output half GEMM in this torch build: comparison column left empty
                 vendor_ms = vendor_err = float("nan")
-            direct_ms = direct_err = staged_ms = staged_err = float("nan")
+            direct_ms = direct_err = staged_ms = staged_err = staged_nk_ms = staged_nk_err = float("nan")
             if rungs:   # the direct and staged rungs forced, beside the selected kernel
                 direct_ms, direct_err, _ = run(ours(b, L.B_KN, L.KERNEL_MFMA_DIRECT), out)
-                staged_ms, staged_err, _ = run(ours(w, L.B_NK, L.KERNEL_MFMA_STAGED), out)
-            sel = L.select(m, n, k, k, k, n, L.B_NK, code[dt], L.F32)
-            disp_ms, disp_err, disp_plain = run(ours(w, L.B_NK), out)
+                staged_ms, staged_err, _ = run(ours(b, L.B_KN, L.KERNEL_MFMA_STAGED), out)
+                staged_nk_ms, staged_nk_err, _ = run(ours(w, L.B_NK, L.KERNEL_MFMA_STAGED), out)
+            sel = L.select(m, n, k, k, n, n, L.B_KN, code[dt], L.F32)
+            disp_ms, disp_err, disp_plain = run(ours(b, L.B_KN), out)
+            sel_nk = L.select(m, n, k, k, k, n, L.B_NK, code[dt], L.F32)
+            disp_nk_ms, disp_nk_err, disp_nk_plain = run(ours(w, L.B_NK), out)
 
             def tf(ms):
                 return flops / (ms * 1e9)
@@ -331,7 +337,9 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
                    f"{tf(direct_ms):.6f}", f"{staged_ms:.6f}", f"{tf(staged_ms):.6f}", f"{vendor_err:.6f}",
                    f"{direct_err:.6f}",
                    f"{staged_err:.6f}", L.kernel_name(sel), f"{disp_ms:.6f}", f"{tf(disp_ms):.6f}",
-                   f"{disp_err:.6f}", f"{vendor_ms / disp_ms:.6f}", "PASS" if ok else "FAIL", f"{disp_plain:.6f}"]
+                   f"{disp_err:.6f}", f"{vendor_ms / disp_ms:.6f}", "PASS" if ok else "FAIL", f"{disp_plain:.6f}",
+                   f"{staged_nk_ms:.6f}", f"{staged_nk_err:.6f}", L.kernel_name(sel_nk), f"{disp_nk_ms:.6f}",
+                   f"{disp_nk_err:.6f}", f"{disp_nk_plain:.6f}"]
             emit(",".join("NA" if x == "nan" else str(x) for x in row))
             rows.append(dict(zip(cols, row)))
             del a, b, w, ref, out, expect
@@ -484,8 +492,34 @@ def main() -> int:
         "roofline": roof,
     }
 
-    # ------------------------------------------------------------ decode rows
     extras = {}
+    # ----------------------------------------- headline with W read cold
+    # The headline reuses one W, which stays in the 256 MB Infinity Cache
+    # across launches; a model's prefill reads each layer's W once.  Here W
+    # rotates over enough copies that every launch reads it from HBM (A and
+    # C stay one buffer each), timed the same way.
+    if not args.no_extras and wl.bound == "mfma":
+        r_copies = math.ceil(2 * INFINITY_CACHE_BYTES / (w.numel() * w.element_size())) + 1
+        r_ws = [w] + [w.clone() for _ in range(r_copies - 1)]
+        r_steps = [launcher(a, r_ws[i % r_copies], out, m, n, k, wl.b_layout, wl.dtype_in, wl.dtype_out)
+                   for i in range(r_copies * 4)]
+        for f in r_steps:
+            f()
+        torch.cuda.synchronize()
+        r_start, r_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        r_start.record()
+        for f in r_steps:
+            f()
+        r_end.record()
+        torch.cuda.synchronize()
+        r_ms = r_start.elapsed_time(r_end) / len(r_steps)
+        extras["headline_w_from_hbm"] = {"us": round(r_ms * 1e3, 3), "TFLOP/s": round(flops / (r_ms * 1e-3) / 1e12, 2),
+                                         "frac_mfma": round(flops / (r_ms * 1e-3) / 1e12 / peak, 4),
+                                         "w_buffers": r_copies, "launches": len(r_steps)}
+        log(f"headline with W rotated over {r_copies} buffers: {r_ms * 1e3:.2f} us/step")
+        del r_ws, r_steps
+
+    # ------------------------------------------------------------ decode rows
     if not args.no_extras:
         dname_ = "bf16_decode_n6144_k1024"
         dw = W.WORKLOADS[dname_]
@@ -796,12 +830,14 @@ def main() -> int:
         mrows = reference_matrix(torch, L, W, dtypes=((torch.bfloat16, "bf16"),), emit=lambda line: None,
                                  rungs=False)
         extras["reference_shape_matrix_bf16"] = [
-            {"shape": r["label"], "m": r["M"], "n": r["N"], "k": r["K"], "kernel": r["dispatch"],
-             "us": round(float(r["dispatch_ms"]) * 1e3, 3),
+            {"shape": r["label"], "m": r["M"], "n": r["N"], "k": r["K"], "kernel_b_kn": r["dispatch"],
+             "us_b_kn": round(float(r["dispatch_ms"]) * 1e3, 3), "kernel_w_nk": r["dispatch_nk"],
+             "us_w_nk": round(float(r["dispatch_nk_ms"]) * 1e3, 3),
              "torch_gpu_gemm_us": None if r["vendor_ms"] == "nan" else round(float(r["vendor_ms"]) * 1e3, 3),
              "exact": r["status"] == "PASS"} for r in mrows]
-        log("reference shape matrix (bf16, fp32 out): " + ", ".join(
-            f"{r['label']} {float(r['dispatch_ms']) * 1e3:.2f} us" for r in mrows))
+        log("reference shape matrix (bf16, fp32 out; B[K,N] / W[N,K]): " + ", ".join(
+            f"{r['label']} {float(r['dispatch_ms']) * 1e3:.2f} / {float(r['dispatch_nk_ms']) * 1e3:.2f} us"
+            for r in mrows))
 
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:
@@ -831,12 +867,37 @@ def main() -> int:
         cb = cpu_baseline.time_cpu_gemm(a_cpu, w_cpu, wl.b_layout == L.B_NK, wl.dtype_out,
                                         budget_s=args.cpu_budget)
         cpu_tf = flops / cb["seconds"] / 1e12
+        call = "F.linear(a, W)" if wl.b_layout == L.B_NK else "torch.matmul(a, B)"
+        # kind "reference": the timed call is the reference's own operation
+        # (F.linear at nanovllm/layers/linear.py:51, torch.matmul as the FP32
+        # ladder's differential target) on PyTorch's CPU kernels, not the
+        # oracle's float64 restatement.
         result["cpu_baseline"] = {
-            "value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
-            "sample": f"full {m}x{n}x{k} {dname[wl.dtype_in]} GEMM on the host CPU ({cb['cpu_model']}, "
-                      f"{cb['threads']} threads of {cb['cpu_count']}), median of {cb['samples']} calls",
+            "value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "reference",
+            "sample": f"full {m}x{n}x{k} {dname[wl.dtype_in]} GEMM, torch {call} on the host CPU "
+                      f"({cb['cpu_model']}, {cb['threads']} threads of {cb['cpu_count']}), median of "
+                      f"{cb['samples']} calls",
         }
         log(f"cpu baseline: {cb['seconds'] * 1e3:.1f} ms/call  {cpu_tf:.3f} TFLOP/s on {cb['threads']} threads")
+        # Every configuration of the workload table on the same host, same
+        # seeded inputs and dtypes (TFLOP/s and GB/s of the same algorithmic
+        # work as the GPU rows).
+        rows_cpu = []
+        for cname, cw in W.WORKLOADS.items():
+            for cm in cw.ms:
+                a_c, b_c = W.make_inputs(cname, cm)
+                cbc = cpu_baseline.time_cpu_gemm(a_c, b_c, cw.b_layout == L.B_NK, cw.dtype_out,
+                                                 budget_s=max(1.0, args.cpu_budget / 4))
+                fl = W.problem_flops(cm, cw.n, cw.k)
+                by = W.problem_bytes(cm, cw.n, cw.k, cw.dtype_in, cw.dtype_out)
+                rows_cpu.append({"workload": cname, "m": cm, "ms_per_call": round(cbc["seconds"] * 1e3, 4),
+                                 "TFLOP/s": round(fl / cbc["seconds"] / 1e12, 4),
+                                 "GB/s": round(by / cbc["seconds"] / 1e9, 2), "samples": cbc["samples"],
+                                 "call": "F.linear" if cw.b_layout == L.B_NK else "torch.matmul"})
+                log(f"cpu baseline {cname} M={cm}: {cbc['seconds'] * 1e3:.2f} ms/call")
+                del a_c, b_c
+        extras["cpu_baseline_configs"] = {"kind": "reference", "cores": cb["threads"], "cpu_model": cb["cpu_model"],
+                                          "cpu_count": cb["cpu_count"], "rows": rows_cpu}
 
     result.update(extras)
     print(json.dumps(result), flush=True)

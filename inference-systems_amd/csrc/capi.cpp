@@ -56,6 +56,12 @@ bool vector_ok(int64_t k, int64_t lda, int64_t ldb, int b_layout, int aligned16)
     return aligned16 && k % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && b_layout == NANOVLLM_GEMM_B_NK;
 }
 
+// B[K,N] problems mfma_staged reads in 16-byte chunks: rows of A as above,
+// and rows of B in whole 8-column chunks (N a multiple of 8).
+bool kn_vector_ok(int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_layout, int aligned16) {
+    return aligned16 && k % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && n % 8 == 0 && b_layout == NANOVLLM_GEMM_B_KN;
+}
+
 // M at or below this is streamed by splitk_decode: the problem is bound by
 // reading W once (arithmetic intensity ~M flop/byte, far under the
 // ~312 flop/byte bf16 ridge of MI355X).
@@ -85,7 +91,9 @@ bool supports(int kernel_id, int64_t m, int64_t n, int64_t k, int64_t lda, int64
         case NANOVLLM_GEMM_KERNEL_FP32_NAIVE:
         case NANOVLLM_GEMM_KERNEL_FP32_TILED: return din == NANOVLLM_GEMM_F32;
         case NANOVLLM_GEMM_KERNEL_MFMA_DIRECT: return is_half(din);
-        case NANOVLLM_GEMM_KERNEL_MFMA_STAGED: return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16);
+        case NANOVLLM_GEMM_KERNEL_MFMA_STAGED:
+            return is_half(din) &&
+                   (vector_ok(k, lda, ldb, b_layout, aligned16) || kn_vector_ok(n, k, lda, ldb, b_layout, aligned16));
         case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE:
             return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && splitk_plain_ok(m, n);
         case NANOVLLM_GEMM_KERNEL_GEMV_DECODE:
@@ -113,6 +121,11 @@ int select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_layo
             return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
         return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
     }
+    // B[K,N] (the reference bench's layout): the staged kernel above decode
+    // sizes; the decode kernels read W[N,K] only, and at M <= 32 the direct
+    // rung streams B[K,N] as fast as a mostly empty 64-row tile would.
+    if (kn_vector_ok(n, k, lda, ldb, b_layout, aligned16) && m > kDecodeMaxM)
+        return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
     return NANOVLLM_GEMM_KERNEL_MFMA_DIRECT;
 }
 

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* src[IPW];
     int koff[IPW];
 #pragma unroll
-    for (int j = 0; j < IPW; ++j) {
+    for (int j = 0; j < (SP == 5 ? 0 : IPW); ++j) {   // (SP 5 addresses its operands itself)
         const int row = 8 * (wave * IPW + j) + (lane >> 3);
         const int chunk = (lane & 7) ^ lds_swizzle(row);
         koff[j] = chunk * 8;
@@ -225,7 +225,164 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         __builtin_amdgcn_s_setprio(0);
     };
 
-    if constexpr (SP == 3) {
+    if constexpr (SP == 5) {
+        // B given as B[K,N] (the reference bench's layout, ldb >= N, N a
+        // multiple of 8), staged through registers into two ring stages.
+        // The W part of a stage is the same n-major, swizzled layout the
+        // other schedules copy from W[N,K], so the fragment reads and MFMAs
+        // do not change (and the sums are bit-identical to W[N,K]'s).  Lane
+        // (kq, nb) of the workgroup loads KB consecutive k-rows of one
+        // 8-column chunk of B (k-group kq, column chunk nb; the 8 lanes of a
+        // wave that share a k-group read 128 consecutive bytes of a row),
+        // transposes the KB x 8 block in registers (v_perm_b32) and writes 8
+        // pieces of KB k-values, one per column, into W rows 8 nb .. 8 nb + 7.
+        // A moves as 16-byte chunks in the layout of the copy instructions.
+        // R register sets: during tile t, K-step 0 writes tile t + 1's A
+        // chunks (loaded during tile t + 1 - R) into the stage tile t - 1
+        // used and loads tile t + R's into the freed set; K-step 1 does the
+        // same for the B block.  Past the last K-tile the loads read the
+        // zero chunk, so every tile issues the same loads and waits.
+        static_assert(EPI == EPI_NONE && !RS && STAGES == 2, "B[K,N]: plain GEMM, 2-deep ring");
+        // (Three register sets where the tile's MFMAs per K-tile are few;
+        // with 8 waves of 64 x 64 two sets, whose K-tile is long enough and
+        // whose 256-register budget holds no third.)
+        constexpr int R = NT >= 512 ? 2 : 3;
+        constexpr int IA = BM * kChunks / NT;        // A chunks per lane and tile
+        constexpr int KB = 8 * BN / NT;              // k-rows of B per lane and tile
+        constexpr int NQ = kBK / KB;                 // k-groups per tile
+        static_assert(IA * NT == BM * kChunks && KB * NT == 8 * BN && NQ % 8 == 0 && (KB == 2 || KB == 4),
+                      "B[K,N] lane mapping");
+        constexpr int WQ = NQ / 8;                   // waves that share one 8-chunk column band
+        constexpr int PER = IA + KB;                 // loads per lane and tile
+        typedef const __attribute__((address_space(1))) u32x4_t* global_chunk;
+        const int kq = 8 * (wave % WQ) + (lane & 7);
+        const int nb = 8 * (wave / WQ) + (lane >> 3);
+        const bool n_in = n0 + 8 * nb < n;          // N % 8 == 0: a chunk is in or out whole
+        const uint16_t* bsrc = w + (n_in ? n0 + 8 * nb : 0);
+        const int kc = (KB * kq) / 8, koff_b = (KB * kq) % 8;   // k chunk and element offset in it
+        // A chunk c = tid + NT j: row c / 8, LDS position c % 8 (logical chunk position ^ swizzle(row)).
+        const uint16_t* asrc[IA];
+        int akoff[IA];
+#pragma unroll
+        for (int j = 0; j < IA; ++j) {
+            const int c = tid + NT * j, row = c / kChunks;
+            akoff[j] = ((c % kChunks) ^ lds_swizzle(row)) * 8;
+            asrc[j] = a + min_i64(m0 + row, m - 1) * lda + akoff[j];
+        }
+        u32x4_t sa_[R][IA], sb[R][KB];
+        auto load_a = [&](int t, auto set_c) {
+            constexpr int S = decltype(set_c)::value;
+            const int64_t k0 = int64_t(t) * kBK;
+#pragma unroll
+            for (int j = 0; j < IA; ++j) {
+                const void* p = k0 + akoff[j] < k ? static_cast<const void*>(asrc[j] + k0) : zero;
+                sa_[S][j] = *reinterpret_cast<global_chunk>(reinterpret_cast<uintptr_t>(p));
+            }
+        };
+        auto load_b = [&](int t, auto set_c) {
+            constexpr int S = decltype(set_c)::value;
+            const int64_t k0 = int64_t(t) * kBK + KB * kq;
+#pragma unroll
+            for (int r = 0; r < KB; ++r) {
+                const void* p = n_in && k0 + r < k ? static_cast<const void*>(bsrc + (k0 + r) * ldb) : zero;
+                sb[S][r] = *reinterpret_cast<global_chunk>(reinterpret_cast<uintptr_t>(p));
+            }
+        };
+        auto store_a = [&](int stage, auto set_c) {
+            constexpr int S = decltype(set_c)::value;
+#pragma unroll
+            for (int j = 0; j < IA; ++j) ring[stage * STAGE_CHUNKS + tid + NT * j] = sa_[S][j];
+        };
+        auto store_b = [&](int stage, auto set_c) {
+            constexpr int S = decltype(set_c)::value;
+            char* base = reinterpret_cast<char*>(ring + stage * STAGE_CHUNKS);
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int row = BM + 8 * nb + jj;
+                const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
+                char* dst = base + row * (kChunks * 16) + ((kc ^ lds_swizzle(row)) * 16) + koff_b * 2;
+                const uint32_t lo = __builtin_amdgcn_perm(sb[S][1][jj >> 1], sb[S][0][jj >> 1], sel);
+                if constexpr (KB == 4) {
+                    const uint32_t hi = __builtin_amdgcn_perm(sb[S][3][jj >> 1], sb[S][2][jj >> 1], sel);
+                    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{lo, hi};
+                } else {
+                    *reinterpret_cast<uint32_t*>(dst) = lo;
+                }
+            }
+        };
+        auto barrier = [] {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        };
+        auto reads = [&](const u32x4_t* tile, int kk, u32x4_t (&af)[MJ], u32x4_t (&wf)[NI]) {
+            read_frags(tile, kk, af, wf);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto mfmas_pinned = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI]) {
+            mfmas(af, wf);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        load_a(0, S0{});
+        load_b(0, S0{});
+        hold_epilogue_args();
+        load_a(1, S1{});
+        load_b(1, S1{});
+        if constexpr (R == 3) {
+            load_a(2, S2{});
+            load_b(2, S2{});
+        }
+        wait_vmcnt<(R - 1) * PER>();
+        store_a(0, S0{});
+        store_b(0, S0{});
+        barrier();
+        reads(ring, 0, af0, wf0);
+        // Tile t = R i + P: its data in set P, tile t + 1's in set (P + 1) % R.
+        auto k_tile = [&](int t, auto phase_c) {
+            constexpr int P = decltype(phase_c)::value;
+            using WS = std::integral_constant<int, (P + 1) % R>;
+            using LS = std::integral_constant<int, P>;
+            const bool store = t + 1 < ktiles;
+            const int cur = t & 1, nxt = cur ^ 1;
+            const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
+            __builtin_amdgcn_s_setprio(3);
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): K-step 0's fragments
+            reads(tile, 1, af1, wf1);
+            wait_vmcnt<(R - 2) * PER + KB>();      // tile t + 1's A chunks
+            if (store) store_a(nxt, WS{});
+            load_a(t + R, LS{});
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_pinned(af0, wf0);
+            reads(tile, 2, af0, wf0);
+            wait_vmcnt<(R - 2) * PER + IA>();      // tile t + 1's B rows
+            if (store) store_b(nxt, WS{});
+            load_b(t + R, LS{});
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_pinned(af1, wf1);
+            reads(tile, 3, af1, wf1);
+            mfmas_pinned(af0, wf0);
+            __builtin_amdgcn_s_setprio(0);
+            if (store) {
+                barrier();
+                reads(ring + nxt * STAGE_CHUNKS, 0, af0, wf0);
+            }
+            mfmas_pinned(af1, wf1);
+        };
+        int t = 0;
+        for (; t + R - 1 < ktiles; t += R) {
+            k_tile(t, S0{});
+            k_tile(t + 1, S1{});
+            if constexpr (R == 3) k_tile(t + 2, S2{});
+        }
+        if (t < ktiles) k_tile(t, S0{});
+        if constexpr (R == 3) {
+            if (t + 1 < ktiles) k_tile(t + 1, S1{});
+        }
+        wait_vmcnt<0>();   // the zero-chunk loads past the last tile
+    } else if constexpr (SP == 3) {
         // Copies staged through registers: each wave loads its IPW chunks of
         // a K-tile with global_load_dwordx4 into `stg` and writes them to the
         // ring with ds_write_b128, at the same LDS positions the copy
@@ -642,8 +799,26 @@ int launch_epi(const Problem& p, hipStream_t s) {
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS, 0>(p, s);
 }
 
+// B[K,N]: the same tiles by grid size as W[N,K] (64 x 64 up to 128 tiles
+// of 128 x 128, 128 x 256 one workgroup per CU where those fill the CUs,
+// else 128 x 128), each with copies staged through registers.
+template <int DT, int DT_OUT>
+int launch_kn(const Problem& p, hipStream_t s) {
+    const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+    if (tiles <= kSmallGridTiles) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 2, EPI_NONE, 0, 5>(p, s);
+    const int64_t wide = ((p.m + 127) / 128) * ((p.n + 255) / 256);
+    if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2))
+        return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 2, EPI_NONE, 0, 5>(p, s);
+    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI_NONE, 0, 5>(p, s);
+}
+
 template <int DT, int DT_OUT>
 int launch_typed(const Problem& p, hipStream_t s) {
+    if (p.b_layout == NANOVLLM_GEMM_B_KN) {
+        if (p.row_scale != nullptr || p.epi != EPI_NONE)
+            return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "mfma_staged: B[K,N] takes the plain GEMM only");
+        return launch_kn<DT, DT_OUT>(p, s);
+    }
     if (p.row_scale != nullptr) {
         if (p.epi == EPI_SILU_MUL) return launch_epi<DT, DT_OUT, EPI_SILU_MUL, 1>(p, s);
         return launch_epi<DT, DT_OUT, EPI_NONE, 1>(p, s);
