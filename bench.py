@@ -600,9 +600,19 @@ def main() -> int:
                     off += rows
             t_one = median_graph_ms(torch, merged)
             t_four = median_graph_ms(torch, separate) * len(g_rows)   # per step of four launches
+
+            def merged_contiguous(f):
+                def g():
+                    f()
+                    for part in g_out.split(g_rows, dim=-1):
+                        part.contiguous()   # the copies GdnInputProjection.forward(contiguous=True) avoids
+                return g
+            t_cont = median_graph_ms(torch, [merged_contiguous(f) for f in merged])
             g_rows_out.append({"m": gm, "merged_us": round(t_one * 1e3, 3), "four_launches_us": round(t_four * 1e3, 3),
-                               "speedup": round(t_four / t_one, 3)})
-            log(f"gdn input projection M={gm}: merged {t_one * 1e3:.2f} us, four launches {t_four * 1e3:.2f} us")
+                               "speedup": round(t_four / t_one, 3),
+                               "merged_with_contiguous_parts_us": round(t_cont * 1e3, 3)})
+            log(f"gdn input projection M={gm}: merged {t_one * 1e3:.2f} us (with contiguous parts "
+                f"{t_cont * 1e3:.2f} us), four launches {t_four * 1e3:.2f} us")
         extras["gdn_input_projection_bf16_k1024"] = g_rows_out
         del g_ws, g_w
 

@@ -110,6 +110,14 @@ def test_gdn_projection_matches_four_linears(dims):
     assert [o.shape[-1] for o in outs] == [2 * kh * kd + vh * vd, vh * vd, vh, vh]
     for out, sid in zip(outs, ("qkv", "z", "b", "a")):
         torch.testing.assert_close(out, F.linear(x, full[sid]))
+    # several rows: views by default; contiguous outputs on request, as
+    # gdn_decode_core's CUDA path asks (nanovllm/kernels/gdn.py:186)
+    assert not outs[0].is_contiguous()
+    parts = proj(x, contiguous=True)
+    assert all(p.is_contiguous() for p in parts)
+    for part, sid in zip(parts, ("qkv", "z", "b", "a")):
+        torch.testing.assert_close(part, F.linear(x, full[sid]))
+    assert all(o.is_contiguous() for o in proj(x[:1]))
     with pytest.raises(ValueError, match="shard id"):
         proj.weight.weight_loader(proj.weight, full["z"], "v")
 

@@ -146,6 +146,9 @@ def test_gdn_merged_projection_bit_exact(m):
         single = G.gemm(x.to(DEV), w.to(DEV))
         torch.cuda.synchronize()
         assert torch.equal(out, single), sid
+    # contiguous outputs (four GEMMs on the weight's row ranges) are the same values
+    for out, part in zip(merged, proj(x.to(DEV), contiguous=True)):
+        assert part.is_contiguous() and torch.equal(out, part)
     got = torch.cat(merged, dim=-1).cpu()
     wall = torch.cat([parts[s].bfloat16() for s in ("qkv", "z", "b", "a")], dim=0)
     a64, w64 = x.double().numpy(), wall.double().numpy()
