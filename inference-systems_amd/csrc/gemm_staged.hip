@@ -52,8 +52,9 @@ __device__ __forceinline__ int lds_swizzle(int row) { return (row >> 1) & 7; }
 // RS: output row i is multiplied by row_scale[i] before rounding (with
 // EPI_NONE or EPI_SILU_MUL, where it scales both sums of a pair).
 // SP: copy schedule.  0: each K-tile's copies as one burst after the
-// barrier; 1: spread between the MFMAs (3-deep ring only); 3: through
-// registers (global_load_dwordx4 + ds_write_b128, 2-deep ring).
+// barrier; 1: spread between the MFMAs (3-deep ring only); 5: B given as
+// B[K,N], staged through registers and transposed on the way to LDS (2-deep
+// ring).
 template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP>
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, int64_t m, int64_t n, int64_t k, int64_t lda,
@@ -75,7 +76,6 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     static_assert(IPW * 8 * NW == ROWS && WM % 32 == 0 && WN % 32 == 0, "tile shape");
     static_assert(AHEAD >= 1 && AHEAD <= 3 && AHEAD * IPW < 64, "vmcnt range");
     static_assert(SP != 1 || STAGES == 3, "the spread schedule refills the stage of tile t - 1 with tile t + 2");
-    static_assert(SP != 3 || STAGES == 2, "register-staged copies fill the stage of tile t - 1 with tile t + 1");
     // EPI_SILU_MUL: the W rows of a tile alternate 32 gate rows and the 32 up
     // rows of the same output columns, so block pair (2i, 2i + 1) of a wave
     // holds gate and up values of one 32-column group in the same lanes.
@@ -382,115 +382,6 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
             if (t + 1 < ktiles) k_tile(t + 1, S1{});
         }
         wait_vmcnt<0>();   // the zero-chunk loads past the last tile
-    } else if constexpr (SP == 3) {
-        // Copies staged through registers: each wave loads its IPW chunks of
-        // a K-tile with global_load_dwordx4 into `stg` and writes them to the
-        // ring with ds_write_b128, at the same LDS positions the copy
-        // instructions of the other schedules fill.  On gfx950 the copy
-        // instruction (global_load_lds_dwordx4) and the fragment reads do not
-        // overlap in the LDS: a probe mixing one 1 KiB copy with three 1 KiB
-        // ds_read_b128 ran as long as the copies alone plus the reads alone,
-        // while loads through registers plus ds_write_b128 overlapped with
-        // the reads (bench.py --probes, "copy").  Two ring stages: during
-        // tile t the K-steps 0, 1, 2 each write G0, G1, G2 of the chunks of
-        // tile t + 1 (loaded during tile t - 1) into the stage tile t - 1
-        // used, and load the same chunks of tile t + 2 into the freed
-        // registers, so every load has a K-tile to land.
-        constexpr int G0 = (IPW + 2) / 3, G1 = (IPW - G0 + 1) / 2, G2 = IPW - G0 - G1;
-        constexpr int STEP = NI * MJ;   // MFMAs per K-step
-        u32x4_t stg[IPW];
-        typedef const __attribute__((address_space(1))) u32x4_t* global_chunk;
-        auto load_one = [&](int t, int j) {
-            const int64_t k0 = int64_t(t) * kBK;
-            const void* p = k0 + koff[j] < k ? static_cast<const void*>(src[j] + k0) : zero;
-            stg[j] = *reinterpret_cast<global_chunk>(reinterpret_cast<uintptr_t>(p));
-        };
-        auto store_one = [&](int stage, int j) { ring[stage * STAGE_CHUNKS + (wave * IPW + j) * 64 + lane] = stg[j]; };
-        auto barrier = [] {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-        };
-        auto reads = [&](const u32x4_t* tile, int kk, u32x4_t (&af)[MJ], u32x4_t (&wf)[NI]) {
-            read_frags(tile, kk, af, wf);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        auto mfmas_pinned = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI]) {
-            mfmas(af, wf);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        // One K-step's MFMAs with chunks J0 .. J0 + CNT - 1: their tile t + 1
-        // values written to `stage` after the first MFMA (once loaded: the
-        // loads after them and, with `load`, the tile t + 2 loads of the
-        // earlier chunks may still be in flight), their tile t + 2 loads
-        // issued after the second.
-        auto step = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI], int t, int stage, auto j0_c, auto cnt_c,
-                        auto store_c, auto load_c) {
-            constexpr int J0 = decltype(j0_c)::value, CNT = decltype(cnt_c)::value;
-            constexpr bool STORE = decltype(store_c)::value, LOAD = decltype(load_c)::value;
-#pragma unroll
-            for (int x = 0; x < STEP; ++x) {
-                acc[x / MJ][x % MJ] = mfma_32x32x16<DT>(wf[x / MJ], af[x % MJ], acc[x / MJ][x % MJ]);
-                if (x == 0 && STORE) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    if constexpr (LOAD) wait_vmcnt<IPW - CNT>();
-                    else wait_vmcnt<IPW - J0 - CNT>();
-#pragma unroll
-                    for (int j = J0; j < J0 + CNT; ++j) store_one(stage, j);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                if (x == (STEP > 1 ? 1 : 0) && LOAD) {
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int j = J0; j < J0 + CNT; ++j) load_one(t + 2, j);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        using C0 = std::integral_constant<int, 0>;
-        using CG0 = std::integral_constant<int, G0>;
-        using CG1 = std::integral_constant<int, G1>;
-        using CG2 = std::integral_constant<int, G2>;
-        using CG01 = std::integral_constant<int, G0 + G1>;
-#pragma unroll
-        for (int j = 0; j < IPW; ++j) load_one(0, j);
-        hold_epilogue_args();
-        wait_vmcnt<0>();
-#pragma unroll
-        for (int j = 0; j < IPW; ++j) store_one(0, j);
-        if (ktiles > 1) {
-#pragma unroll
-            for (int j = 0; j < IPW; ++j) load_one(1, j);
-        }
-        barrier();
-        reads(ring, 0, af0, wf0);
-        int cur = 0;
-        // STORE: tile t + 1 exists; LOAD: tile t + 2 exists.
-        auto k_tile = [&](int t, auto store_c, auto load_c) {
-            constexpr bool STORE = decltype(store_c)::value;
-            const int nxt = cur ^ 1;
-            const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
-            __builtin_amdgcn_s_setprio(3);
-            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): K-step 0's fragments
-            reads(tile, 1, af1, wf1);
-            step(af0, wf0, t, nxt, C0{}, CG0{}, store_c, load_c);
-            reads(tile, 2, af0, wf0);
-            step(af1, wf1, t, nxt, CG0{}, CG1{}, store_c, load_c);
-            reads(tile, 3, af1, wf1);
-            step(af0, wf0, t, nxt, CG01{}, CG2{}, store_c, load_c);
-            __builtin_amdgcn_s_setprio(0);
-            if constexpr (STORE) {
-                barrier();
-                reads(ring + nxt * STAGE_CHUNKS, 0, af0, wf0);
-            }
-            cur = nxt;
-            mfmas_pinned(af1, wf1);
-        };
-        int t = 0;
-        for (; t + 2 < ktiles; ++t) k_tile(t, std::true_type{}, std::true_type{});
-        if (t + 1 < ktiles) k_tile(t++, std::true_type{}, std::false_type{});
-        k_tile(t, std::false_type{}, std::false_type{});
     } else if constexpr (SP == 1) {
         // Tile t's K-steps 0, 1 and 2 each carry D0, D1, D2 of the wave's IPW
         // copy instructions for tile t + 2, which go to the stage tile t - 1
