@@ -259,9 +259,9 @@ def reference_matrix(torch, L, W, dtypes=None, emit=print, rungs=True) -> list:
       these inputs) as compare does: max |error|, and pass if every error is
       within 5e-2 + 1e-2 |ref| and finite (gemm_bench.cu:225-250);
     * direct_*, staged_* and dispatch_* run on the reference's B[K,N]
-      layout, as its columns do: mfma_direct, mfma_staged (B transposed in
-      registers on its way to LDS) and the kernel the selection table picks
-      for B[K,N]; the *_nk columns after the reference's run the same
+      layout, as its columns do: mfma_direct, mfma_staged (B's k-rows copied
+      as they lie, read back with the transposing LDS read) and the kernel
+      the selection table picks for B[K,N]; the *_nk columns after the reference's run the same
       matrix transposed into the W[N,K] (nn.Linear) layout, where the decode
       kernels (gemv_decode, splitk_decode) also apply;
     * timing as benchmark_ms: 10 warm-up launches, repeats =

@@ -48,14 +48,27 @@ __device__ u32x4_t g_zero_chunk = {0u, 0u, 0u, 0u};
 
 __device__ __forceinline__ int lds_swizzle(int row) { return (row >> 1) & 7; }
 
+// B[K,N] stages: k-row r of the W part holds its 16-byte column chunks in
+// position chunk ^ kn_swizzle(r).  A transposing fragment read touches 8
+// k-rows (r, r+1, r+2, r+3, r+8, ..., r+11) x 64 bytes; flipping bits 2-3
+// of the chunk position by r % 4 (by bit 1 of r with 8 chunks per row,
+// whose rows alternate between two 128-byte halves of the banks) puts two
+// of those rows in each quarter of the 64 banks.
+template <int BN>
+__device__ __forceinline__ int kn_swizzle(int r) {
+    if constexpr (BN >= 128) return (r & 3) << 2;
+    else return ((r >> 1) & 1) << 2;
+}
+
 
 // RS: output row i is multiplied by row_scale[i] before rounding (with
 // EPI_NONE or EPI_SILU_MUL, where it scales both sums of a pair).
 // SP: copy schedule.  0: each K-tile's copies as one burst after the
-// barrier; 1: spread between the MFMAs (3-deep ring only); 5: B given as
-// B[K,N], staged through registers and transposed on the way to LDS (2-deep
-// ring).
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP>
+// barrier; 1: spread between the MFMAs (3-deep ring only).
+// KN: B is given as B[K,N] (row stride ldb >= N, N a multiple of 8); the W
+// part of a stage then holds 64 k-rows of BN columns, copied as they lie in
+// memory, and the W fragments are read with gfx950's transposing LDS read.
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP, int KN = 0>
 __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, int64_t m, int64_t n, int64_t k, int64_t lda,
     int64_t ldb, void* __restrict__ c, int64_t ldc, int c_vec, uint64_t* __restrict__ keys,
@@ -81,6 +94,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // holds gate and up values of one 32-column group in the same lanes.
     static_assert(EPI != EPI_SILU_MUL || NI % 2 == 0, "gate/up pairs per wave");
     static_assert(!RS || EPI != EPI_ARGMAX, "row scale with a stored output");
+    static_assert(!KN || (EPI == EPI_NONE && !RS && (SP == 0 || SP == 1)), "B[K,N]: plain GEMM, copy schedules");
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;   // output columns per tile
 
     // LDS: the ring of K-tile stages, reused after the K loop for the C tile.
@@ -118,14 +132,34 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // DMA instruction j of this wave fills LDS rows 8 i .. 8 i + 7 of a stage,
     // i = wave * IPW + j; lane L writes row 8 i + L / 8, position L % 8, which
     // holds logical chunk (L % 8) ^ swizzle(row).
+    //
+    // KN: instruction i >= BM / 8 copies chunks q = 64 (i - BM / 8) + L of the
+    // W part instead, k-row q / (BN / 8), position q % (BN / 8), which holds
+    // logical chunk (8 columns) position ^ swizzle_kn(row).  kpos[j] is the
+    // k position the instruction's chunk starts at (chunk offset in an A row,
+    // k-row of B; K for a B chunk past N, which is then always the zero
+    // chunk), kn_row[j] whether it advances by rows of B.
     const uint16_t* src[IPW];
     int koff[IPW];
+    int kpos[IPW];
+    bool kn_row[IPW];
 #pragma unroll
-    for (int j = 0; j < (SP == 5 ? 0 : IPW); ++j) {   // (SP 5 addresses its operands itself)
+    for (int j = 0; j < IPW; ++j) {
         const int row = 8 * (wave * IPW + j) + (lane >> 3);
         const int chunk = (lane & 7) ^ lds_swizzle(row);
         koff[j] = chunk * 8;
-        if (row < BM) {
+        kpos[j] = koff[j];
+        kn_row[j] = false;
+        if (KN && row >= BM) {
+            constexpr int CPRB = BN / 8;   // chunks per k-row of the W part
+            const int q = 64 * (wave * IPW + j - BM / 8) + lane;
+            const int kr = q / CPRB;
+            const int64_t col = n0 + 8 * ((q % CPRB) ^ kn_swizzle<BN>(kr));
+            const bool in = col < n;       // N % 8 == 0: a chunk is in or out whole
+            src[j] = w + (in ? int64_t(kr) * ldb + col : 0);
+            kpos[j] = in ? kr : int(k < INT32_MAX ? k : INT32_MAX);
+            kn_row[j] = true;
+        } else if (row < BM) {
             src[j] = a + min_i64(m0 + row, m - 1) * lda + koff[j];
         } else if constexpr (EPI == EPI_SILU_MUL) {
             const int wr = row - BM;
@@ -145,10 +179,18 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // scalar load at every use).
     const void* zero = &g_zero_chunk;
     asm volatile("" : "+s"(zero));
+    // Source of instruction j's chunk of the K-tile starting at k0.
+    auto chunk_src = [&](int j, int64_t k0) -> const void* {
+        if (k0 + kpos[j] >= k) return zero;
+        return src[j] + (KN && kn_row[j] ? k0 * ldb : k0);
+    };
     auto issue = [&](int t, int stage) {
         const int64_t k0 = int64_t(t) * kBK;
         const uint32_t dst = ring_lds + uint32_t(stage * STAGE_CHUNKS + 64 * wave * IPW) * 16u;
-        if (k0 + kBK <= k) {
+        if constexpr (KN) {
+#pragma unroll
+            for (int j = 0; j < IPW; ++j) dma16(chunk_src(j, k0), dst + 1024u * j);
+        } else if (k0 + kBK <= k) {
 #pragma unroll
             for (int j = 0; j < IPW; ++j) dma16(src[j] + k0, dst + 1024u * j);
         } else {
@@ -163,7 +205,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     auto issue_one = [&](int t, int stage, int j) {
         const int64_t k0 = int64_t(t) * kBK;
         const uint32_t dst = ring_lds + uint32_t(stage * STAGE_CHUNKS + 64 * wave * IPW) * 16u + 1024u * j;
-        dma16(k0 + koff[j] < k ? static_cast<const void*>(src[j] + k0) : zero, dst);
+        dma16(chunk_src(j, k0), dst);
     };
 
     f32x16_t acc[NI][MJ];
@@ -181,12 +223,42 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // Two fragment register sets: the MFMAs of K-step kk run from one while
     // the ds_reads of kk + 1 fill the other.
     u32x4_t af0[MJ], wf0[NI], af1[MJ], wf1[NI];
+    // KN: W fragment i of K-step kk is two ds_read_b64_tr_b16.  Within each
+    // 16-lane group the instruction returns, to lane i, element i % 4 of the
+    // 8 bytes lanes i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12 point at; lane j
+    // of the group points at k-row (4 r + j / 4) and columns 4 (j % 4) .. +3
+    // of its 16-column half, so lane l ends with k = 16 kk + 8 (l / 32) +
+    // 4 r + 0..3 of column l % 32: the operand layout above, 4 k at a time.
+    // The swizzle spreads the 8 k-rows one read touches over all 64 banks.
+    constexpr int KN_PITCH = BN * 2;   // bytes per k-row of the W part
+    const int kn_q = (lane & 15) >> 2;
+    const uint32_t kn_row_off = uint32_t(8 * (lane >> 5) + kn_q) * KN_PITCH;
+    uint32_t kn_col_off[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int col = wn * WN + 32 * i + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        kn_col_off[i] = uint32_t(((col >> 3) ^ kn_swizzle<BN>(kn_q)) * 16 + (col & 7) * 2);
+    }
     auto read_frags = [&](const u32x4_t* tile, int kk, u32x4_t (&af)[MJ], u32x4_t (&wf)[NI]) {
         const int chunk = (2 * kk + half) ^ swz;
 #pragma unroll
         for (int j = 0; j < MJ; ++j) af[j] = tile[(a_row0 + 32 * j) * kChunks + chunk];
+        if constexpr (KN) {
+            typedef short v4i16_t __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) v4i16_t* lds_v4;
+            const uint32_t wpart = lds_address(tile + BM * kChunks) + kn_row_off + uint32_t(16 * kk) * KN_PITCH;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) wf[i] = tile[(w_row0 + 32 * i) * kChunks + chunk];
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t a0 = wpart + kn_col_off[i];
+                const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4)(uintptr_t)a0);
+                const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4)(uintptr_t)(a0 + 4 * KN_PITCH));
+                const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+                wf[i] = u32x4_t{l2[0], l2[1], h2[0], h2[1]};
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) wf[i] = tile[(w_row0 + 32 * i) * kChunks + chunk];
+        }
     };
     auto mfmas = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI]) {
 #pragma unroll
@@ -225,164 +297,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
         __builtin_amdgcn_s_setprio(0);
     };
 
-    if constexpr (SP == 5) {
-        // B given as B[K,N] (the reference bench's layout, ldb >= N, N a
-        // multiple of 8), staged through registers into two ring stages.
-        // The W part of a stage is the same n-major, swizzled layout the
-        // other schedules copy from W[N,K], so the fragment reads and MFMAs
-        // do not change (and the sums are bit-identical to W[N,K]'s).  Lane
-        // (kq, nb) of the workgroup loads KB consecutive k-rows of one
-        // 8-column chunk of B (k-group kq, column chunk nb; the 8 lanes of a
-        // wave that share a k-group read 128 consecutive bytes of a row),
-        // transposes the KB x 8 block in registers (v_perm_b32) and writes 8
-        // pieces of KB k-values, one per column, into W rows 8 nb .. 8 nb + 7.
-        // A moves as 16-byte chunks in the layout of the copy instructions.
-        // R register sets: during tile t, K-step 0 writes tile t + 1's A
-        // chunks (loaded during tile t + 1 - R) into the stage tile t - 1
-        // used and loads tile t + R's into the freed set; K-step 1 does the
-        // same for the B block.  Past the last K-tile the loads read the
-        // zero chunk, so every tile issues the same loads and waits.
-        static_assert(EPI == EPI_NONE && !RS && STAGES == 2, "B[K,N]: plain GEMM, 2-deep ring");
-        // (Three register sets where the tile's MFMAs per K-tile are few;
-        // with 8 waves of 64 x 64 two sets, whose K-tile is long enough and
-        // whose 256-register budget holds no third.)
-        constexpr int R = NT >= 512 ? 2 : 3;
-        constexpr int IA = BM * kChunks / NT;        // A chunks per lane and tile
-        constexpr int KB = 8 * BN / NT;              // k-rows of B per lane and tile
-        constexpr int NQ = kBK / KB;                 // k-groups per tile
-        static_assert(IA * NT == BM * kChunks && KB * NT == 8 * BN && NQ % 8 == 0 && (KB == 2 || KB == 4),
-                      "B[K,N] lane mapping");
-        constexpr int WQ = NQ / 8;                   // waves that share one 8-chunk column band
-        constexpr int PER = IA + KB;                 // loads per lane and tile
-        typedef const __attribute__((address_space(1))) u32x4_t* global_chunk;
-        const int kq = 8 * (wave % WQ) + (lane & 7);
-        const int nb = 8 * (wave / WQ) + (lane >> 3);
-        const bool n_in = n0 + 8 * nb < n;          // N % 8 == 0: a chunk is in or out whole
-        const uint16_t* bsrc = w + (n_in ? n0 + 8 * nb : 0);
-        const int kc = (KB * kq) / 8, koff_b = (KB * kq) % 8;   // k chunk and element offset in it
-        // A chunk c = tid + NT j: row c / 8, LDS position c % 8 (logical chunk position ^ swizzle(row)).
-        const uint16_t* asrc[IA];
-        int akoff[IA];
-#pragma unroll
-        for (int j = 0; j < IA; ++j) {
-            const int c = tid + NT * j, row = c / kChunks;
-            akoff[j] = ((c % kChunks) ^ lds_swizzle(row)) * 8;
-            asrc[j] = a + min_i64(m0 + row, m - 1) * lda + akoff[j];
-        }
-        u32x4_t sa_[R][IA], sb[R][KB];
-        auto load_a = [&](int t, auto set_c) {
-            constexpr int S = decltype(set_c)::value;
-            const int64_t k0 = int64_t(t) * kBK;
-#pragma unroll
-            for (int j = 0; j < IA; ++j) {
-                const void* p = k0 + akoff[j] < k ? static_cast<const void*>(asrc[j] + k0) : zero;
-                sa_[S][j] = *reinterpret_cast<global_chunk>(reinterpret_cast<uintptr_t>(p));
-            }
-        };
-        auto load_b = [&](int t, auto set_c) {
-            constexpr int S = decltype(set_c)::value;
-            const int64_t k0 = int64_t(t) * kBK + KB * kq;
-#pragma unroll
-            for (int r = 0; r < KB; ++r) {
-                const void* p = n_in && k0 + r < k ? static_cast<const void*>(bsrc + (k0 + r) * ldb) : zero;
-                sb[S][r] = *reinterpret_cast<global_chunk>(reinterpret_cast<uintptr_t>(p));
-            }
-        };
-        auto store_a = [&](int stage, auto set_c) {
-            constexpr int S = decltype(set_c)::value;
-#pragma unroll
-            for (int j = 0; j < IA; ++j) ring[stage * STAGE_CHUNKS + tid + NT * j] = sa_[S][j];
-        };
-        auto store_b = [&](int stage, auto set_c) {
-            constexpr int S = decltype(set_c)::value;
-            char* base = reinterpret_cast<char*>(ring + stage * STAGE_CHUNKS);
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const int row = BM + 8 * nb + jj;
-                const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-                char* dst = base + row * (kChunks * 16) + ((kc ^ lds_swizzle(row)) * 16) + koff_b * 2;
-                const uint32_t lo = __builtin_amdgcn_perm(sb[S][1][jj >> 1], sb[S][0][jj >> 1], sel);
-                if constexpr (KB == 4) {
-                    const uint32_t hi = __builtin_amdgcn_perm(sb[S][3][jj >> 1], sb[S][2][jj >> 1], sel);
-                    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{lo, hi};
-                } else {
-                    *reinterpret_cast<uint32_t*>(dst) = lo;
-                }
-            }
-        };
-        auto barrier = [] {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-        };
-        auto reads = [&](const u32x4_t* tile, int kk, u32x4_t (&af)[MJ], u32x4_t (&wf)[NI]) {
-            read_frags(tile, kk, af, wf);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        auto mfmas_pinned = [&](const u32x4_t (&af)[MJ], const u32x4_t (&wf)[NI]) {
-            mfmas(af, wf);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        using S0 = std::integral_constant<int, 0>;
-        using S1 = std::integral_constant<int, 1>;
-        using S2 = std::integral_constant<int, 2>;
-        load_a(0, S0{});
-        load_b(0, S0{});
-        hold_epilogue_args();
-        load_a(1, S1{});
-        load_b(1, S1{});
-        if constexpr (R == 3) {
-            load_a(2, S2{});
-            load_b(2, S2{});
-        }
-        wait_vmcnt<(R - 1) * PER>();
-        store_a(0, S0{});
-        store_b(0, S0{});
-        barrier();
-        reads(ring, 0, af0, wf0);
-        // Tile t = R i + P: its data in set P, tile t + 1's in set (P + 1) % R.
-        auto k_tile = [&](int t, auto phase_c) {
-            constexpr int P = decltype(phase_c)::value;
-            using WS = std::integral_constant<int, (P + 1) % R>;
-            using LS = std::integral_constant<int, P>;
-            const bool store = t + 1 < ktiles;
-            const int cur = t & 1, nxt = cur ^ 1;
-            const u32x4_t* tile = ring + cur * STAGE_CHUNKS;
-            __builtin_amdgcn_s_setprio(3);
-            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): K-step 0's fragments
-            reads(tile, 1, af1, wf1);
-            wait_vmcnt<(R - 2) * PER + KB>();      // tile t + 1's A chunks
-            if (store) store_a(nxt, WS{});
-            load_a(t + R, LS{});
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas_pinned(af0, wf0);
-            reads(tile, 2, af0, wf0);
-            wait_vmcnt<(R - 2) * PER + IA>();      // tile t + 1's B rows
-            if (store) store_b(nxt, WS{});
-            load_b(t + R, LS{});
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas_pinned(af1, wf1);
-            reads(tile, 3, af1, wf1);
-            mfmas_pinned(af0, wf0);
-            __builtin_amdgcn_s_setprio(0);
-            if (store) {
-                barrier();
-                reads(ring + nxt * STAGE_CHUNKS, 0, af0, wf0);
-            }
-            mfmas_pinned(af1, wf1);
-        };
-        int t = 0;
-        for (; t + R - 1 < ktiles; t += R) {
-            k_tile(t, S0{});
-            k_tile(t + 1, S1{});
-            if constexpr (R == 3) k_tile(t + 2, S2{});
-        }
-        if (t < ktiles) k_tile(t, S0{});
-        if constexpr (R == 3) {
-            if (t + 1 < ktiles) k_tile(t + 1, S1{});
-        }
-        wait_vmcnt<0>();   // the zero-chunk loads past the last tile
-    } else if constexpr (SP == 1) {
+    if constexpr (SP == 1) {
         // Tile t's K-steps 0, 1 and 2 each carry D0, D1, D2 of the wave's IPW
         // copy instructions for tile t + 2, which go to the stage tile t - 1
         // used (free since the barrier that opened tile t).  All IPW are out
@@ -617,7 +532,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
 
 constexpr int64_t kCus = 256;
 
-template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP>
+template <int DT, int DT_OUT, int BM, int BN, int WGM, int WGN, int STAGES, int EPI, int RS, int SP, int KN = 0>
 int launch_tile(const Problem& p, hipStream_t s) {
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;
     const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BNO - 1) / BNO;
@@ -628,7 +543,7 @@ int launch_tile(const Problem& p, hipStream_t s) {
     // The copy-out writes 16-byte chunks: every row start must be 16-byte aligned.
     const int c_vec = (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && ((p.ldc * out_bytes) % 16 == 0);
     if (EPI == EPI_ARGMAX) *p.key_blocks = tiles_n;
-    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI, RS, SP>), grid, block, 0, s,
+    hipLaunchKernelGGL((mfma_staged_kernel<DT, DT_OUT, BM, BN, WGM, WGN, STAGES, EPI, RS, SP, KN>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.m, p.n, p.k, p.lda,
                        p.ldb, p.c, p.ldc, c_vec, p.keys, p.row_scale, p.sample);
     return check_launch("mfma_staged");
@@ -690,17 +605,19 @@ int launch_epi(const Problem& p, hipStream_t s) {
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS, 0>(p, s);
 }
 
-// B[K,N]: the same tiles by grid size as W[N,K] (64 x 64 up to 128 tiles
-// of 128 x 128, 128 x 256 one workgroup per CU where those fill the CUs,
-// else 128 x 128), each with copies staged through registers.
+// B[K,N]: the same tiles and copy schedules by grid size as W[N,K] (64 x 64
+// up to 128 tiles of 128 x 128, 128 x 256 where those fill the CUs, 128 x
+// 128 otherwise); the W part of each stage is B's k-rows as they lie in
+// memory, read back with the transposing fragment read.
 template <int DT, int DT_OUT>
 int launch_kn(const Problem& p, hipStream_t s) {
     const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
-    if (tiles <= kSmallGridTiles) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 2, EPI_NONE, 0, 5>(p, s);
+    if (tiles <= kSmallGridTiles) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI_NONE, 0, 1, 1>(p, s);
     const int64_t wide = ((p.m + 127) / 128) * ((p.n + 255) / 256);
     if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2))
-        return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 2, EPI_NONE, 0, 5>(p, s);
-    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI_NONE, 0, 5>(p, s);
+        return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI_NONE, 0, 1, 1>(p, s);
+    if (tiles <= kCus) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI_NONE, 0, 1, 1>(p, s);
+    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI_NONE, 0, 0, 1>(p, s);
 }
 
 template <int DT, int DT_OUT>

@@ -111,9 +111,9 @@ def _expected(m, n, k, lda, ldb, layout, din, aligned):
         if m <= 64 and (n <= 4096 or (n <= 10240 and k <= 1024)):
             return L.KERNEL_SPLITK_DECODE
         return L.KERNEL_MFMA_STAGED
-    # B[K,N] with whole 8-column chunks: the staged kernel above decode sizes
+    # B[K,N] with whole 8-column chunks: the staged kernel
     kn_vec = aligned and k % 8 == 0 and lda % 8 == 0 and ldb % 8 == 0 and n % 8 == 0 and layout == KN
-    if kn_vec and m > 32:
+    if kn_vec:
         return L.KERNEL_MFMA_STAGED
     return L.KERNEL_MFMA_DIRECT
 
@@ -159,9 +159,8 @@ def test_selection_on_workloads_and_qwen_shapes():
         want_k = "gemv_decode" if m == 1 else ("splitk_decode" if m <= 64 else "mfma_staged")
         assert L.kernel_name(kid) == want_k, label
         # the reference's B[K,N] layout of the same shapes: the staged rung
-        # above decode sizes, the direct rung at M <= 32
         kid = L.select(m, n, k, k, n, n, KN, BF16, F32, 1)
-        assert L.kernel_name(kid) == ("mfma_direct" if m <= 32 else "mfma_staged"), label
+        assert L.kernel_name(kid) == "mfma_staged", label
 
 
 def test_no_vendor_kernel_id():

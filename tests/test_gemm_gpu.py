@@ -251,24 +251,25 @@ def test_staged_ring_depths_ragged(m, n, k, din, dout):
 
 
 STAGED_GRIDS_KN = [(600, 1000, 1000), (1100, 2000, 1000), (2100, 2000, 1000), (2100, 4104, 1000),
-                   (2100, 7000, 1000), (40, 520, 72), (2048, 4096, 1024)]
+                   (2100, 7000, 1000), (40, 520, 72), (2048, 4096, 1024), (1, 6144, 1024), (5, 200, 136)]
 
 
 @pytest.mark.parametrize("m,n,k", STAGED_GRIDS_KN, ids=["40tiles-64x64", "144tiles-128x128", "wide136-128x256",
-                                                        "wide289-128x128", "wide476-128x256", "tiny", "headline"])
+                                                        "wide289-128x128-2deep", "wide476-128x256", "tiny",
+                                                        "headline", "decode", "ragged-small"])
 @pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
                          ids=["bf16", "f16-f32"])
 def test_staged_kn_ragged(m, n, k, din, dout):
     """mfma_staged on B[K,N] (the reference bench's layout, gemm_bench.cu:103-106,
-    117-196): every tile choice of the grid-size table, B transposed in
-    registers on its way to LDS; ragged M, N a multiple of 8 but not of the
-    tile, K not a multiple of the 64-wide K-tile."""
+    117-196): every tile choice and copy schedule of the grid-size table, B's
+    k-rows copied as they lie and read back with the transposing fragment
+    read; ragged M, N a multiple of 8 but not of the tile, K not a multiple
+    of the 64-wide K-tile, decode-sized M."""
     _say(f"staged B[K,N] M={m} N={n} K={k} {NAME[din]}->{NAME[dout]}")
     gen = torch.Generator().manual_seed(m + 3 * n)
     a = torch.randn((m, k), generator=gen).to(din)
     b = (torch.randn((k, n), generator=gen) * 0.1).to(din)
-    assert L.select(m, n, k, k, n, n, L.B_KN, CODE[din], CODE[dout], True) == (
-        L.KERNEL_MFMA_STAGED if m > 32 else L.KERNEL_MFMA_DIRECT)
+    assert L.select(m, n, k, k, n, n, L.B_KN, CODE[din], CODE[dout], True) == L.KERNEL_MFMA_STAGED
     out = G.gemm_with_kernel(a.to(DEV), b.to(DEV), L.KERNEL_MFMA_STAGED, dout, L.B_KN)
     torch.cuda.synchronize()
     rows = np.unique(np.concatenate([np.linspace(0, m - 1, 48).astype(int), np.arange(max(m - 16, 0), m)]))
@@ -991,5 +992,5 @@ def test_reference_shape_matrix():
         assert r["status"] == "PASS", r
         for c in ("direct_max_abs", "staged_max_abs", "dispatch_max_abs", "staged_nk_max_abs", "dispatch_nk_max_abs"):
             assert float(r[c]) == 0.0, (r["label"], c)
-        # on B[K,N] the table takes the staged rung above decode sizes
-        assert r["dispatch"] == ("mfma_direct" if int(r["M"]) <= 32 else "mfma_staged"), r["label"]
+        # on B[K,N] the table takes the staged rung
+        assert r["dispatch"] == "mfma_staged", r["label"]
