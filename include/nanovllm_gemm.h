@@ -61,7 +61,10 @@ enum {
  *   MFMA_DIRECT    one wave per 32x32 C tile, operands straight from
  *                  global memory, any shape          (gemm_bench.cu:80-115, gemm_wmma.cu:56-104)
  *   MFMA_STAGED    LDS multi-buffered macro-tile MFMA kernel for
- *                  prefill-shaped problems           (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
+ *                  prefill-shaped problems on W[N,K], and for every M on
+ *                  B[K,N] with N a multiple of 8 (B's k-rows copied to
+ *                  LDS as they lie, read back transposed)
+ *                                                    (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
  *   SPLITK_DECODE  split-K wavefront-reduction kernel for M <= 32 (the
  *                  plain GEMM and the fused SiLU-and-mul up to M = 64 below
  *                  65536 W rows) that streams W once, copied to LDS in
