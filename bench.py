@@ -68,6 +68,9 @@ def parse_args():
     p.add_argument("--probes", action="store_true",
                    help="only run the microbenchmarks of the hardware ceilings (launch floor, streaming read, LDS "
                         "reads, global -> LDS copies, MFMA rate, clocks) and print them as one JSON line")
+    p.add_argument("--decode-sweep", action="store_true",
+                   help="only run every configuration of the decode kernels (rows of A and of W per workgroup, "
+                        "waves, lines per wave) on the decode shapes and print them as one JSON line")
     p.add_argument("--matrix", action="store_true",
                    help="only run the reference's shape matrix (fp16 and bf16 over its Qwen3.5 shapes) and print "
                         "it as CSV")
@@ -233,6 +236,59 @@ def run_probes(torch) -> int:
     return 0
 
 
+# (N, K): q/k/v, down, merged GDN input projection, o_proj / GDN out_proj, a wide W
+DECODE_SWEEP_SHAPES = ((6144, 1024), (1024, 3584), (8224, 1024), (1024, 2048), (16384, 1024))
+
+
+def run_decode_sweep(torch, L) -> int:
+    """Every configuration of the LDS-staged and the register-loading decode
+    kernels (inference-systems_amd/csrc/decode_sweep.hip) on the bf16 decode
+    shapes, W rotated past the Infinity Cache, graph replays as for the
+    decode rows; each output checked against torch's fp32 product.  The
+    selected kernel of the GEMM library is timed beside them."""
+    import importlib
+
+    P = importlib.import_module("inference_systems_amd.probes")
+    cfgs = P.sweep_configs()
+    out = {"decode_sweep": "bf16 in and out, W[N,K], W rotated past the Infinity Cache", "rows": []}
+    gen = torch.Generator().manual_seed(2024)
+    for n, k in DECODE_SWEEP_SHAPES:
+        w_cpu = (torch.randn(n, k, generator=gen) * 0.02).bfloat16()
+        w0 = w_cpu.cuda()
+        copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (n * k * 2)) + 1)
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        for m in (1, 4, 8, 16, 32):
+            a = torch.randn(m, k, generator=gen).bfloat16().cuda()
+            ref = (a.float() @ w0.float().T)
+            c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+            kid = L.select(m, n, k, k, k, n, L.B_NK, L.BF16, L.BF16, True)
+
+            def product(wt):
+                args_ = (a.data_ptr(), wt.data_ptr(), c.data_ptr(), m, n, k, k, k, n, L.B_NK, L.BF16, L.BF16)
+                return lambda: L.gemm_raw(*args_, torch.cuda.current_stream().cuda_stream)
+            runs = [("selected " + L.kernel_name(kid), product)]
+            for idx, name, max_m in cfgs:
+                if max_m >= m and max_m < 2 * max(m, 8):   # the configurations with the fewest rows of A that fit
+                    runs.append((name, lambda wt, idx=idx: P.sweep_launcher(torch, idx, a, wt, c)))
+            for name, make in runs:
+                c.zero_()
+                make(w0)()
+                torch.cuda.synchronize()
+                err = float((c.float() - ref).abs().max())
+                tol = float(ref.abs().max()) * 2 ** -7 + 1e-3
+                t_ms = median_graph_ms(torch, [make(ws[i % copies]) for i in range(copies * 10)], trials=3)
+                gbs = (n * k + m * k + m * n) * 2 / (t_ms * 1e-3) / 1e9
+                row = {"n": n, "k": k, "m": m, "config": name, "us": round(t_ms * 1e3, 3), "GB/s": round(gbs, 1),
+                       "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "max_abs_err": err, "ok": err <= tol}
+                out["rows"].append(row)
+                log(f"N={n} K={k} M={m:2d} {name:40s} {row['us']:7.2f} us  {gbs:6.0f} GB/s  "
+                    f"err {err:.3g}{'' if row['ok'] else '  WRONG'}")
+        del ws, w0
+        torch.cuda.empty_cache()
+    print(json.dumps(out), flush=True)
+    return 0 if all(r["ok"] for r in out["rows"]) else 1
+
+
 def reference_inputs(torch, m: int, n: int, k: int):
     """A[M,K] and B[K,N] (fp32, CPU) from the reference's deterministic
     generators (gemm_bench.cu:296-305): multiples of 1/32 in [-15/32, 15/32]
@@ -370,6 +426,9 @@ def main() -> int:
     if args.probes:
         torch.cuda.set_device(0)
         return run_probes(torch)
+    if args.decode_sweep:
+        torch.cuda.set_device(0)
+        return run_decode_sweep(torch, L)
     if args.matrix:
         torch.cuda.set_device(0)
         rows = reference_matrix(torch, L, W, emit=lambda line: print(line, flush=True))

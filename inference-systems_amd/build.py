@@ -56,10 +56,13 @@ SOURCES = [
     "gemm_prologue.hip",
 ]
 
-# The microbenchmarks behind `bench.py --probes`: a library of their own, so
-# the GEMM library carries only the product's entry points.
+# The microbenchmarks behind `bench.py --probes` and the decode
+# configuration sweep behind `bench.py --decode-sweep`: libraries of their
+# own, so the GEMM library carries only the product's entry points.
 PROBE_SOURCES = ["probes.hip"]
 PROBE_LIB_PATH = PKG_DIR / "libnanovllm_probes.so"
+SWEEP_SOURCES = ["decode_sweep.hip"]
+SWEEP_LIB_PATH = PKG_DIR / "libnanovllm_decode_sweep.so"
 
 
 # Host-only sanitizers for capi.cpp: each -fsanitize= goes to the host pass
@@ -149,22 +152,32 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, sanitize:
     return target
 
 
-def build_probes(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
-    """Compile the microbenchmark library (libnanovllm_probes.so)."""
-    with tempfile.TemporaryDirectory(prefix="nvgemm_probes_") as tmp:
-        out_tmp = Path(tmp) / PROBE_LIB_PATH.name
+def _build_aux(sources: list[str], lib_path: Path, verbose: bool, extra_flags: list[str] | None) -> Path:
+    with tempfile.TemporaryDirectory(prefix="nvgemm_aux_") as tmp:
+        out_tmp = Path(tmp) / lib_path.name
         cmd = [hipcc(), "-x", "hip", *HIP_FLAGS, *(extra_flags or []), "-shared", "-o", str(out_tmp),
-               *[str(CSRC / name) for name in PROBE_SOURCES]]
+               *[str(CSRC / name) for name in sources]]
         proc = subprocess.run(cmd, capture_output=True, text=True)
         noise = "'-packed-fp32-ops' is not a recognized feature"
         err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
         if proc.returncode != 0:
-            raise RuntimeError(f"hipcc failed for the probes:\n{err}")
-        final_tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
+            raise RuntimeError(f"hipcc failed for {lib_path.name}:\n{err}")
+        final_tmp = lib_path.with_suffix(".so.tmp")
         shutil.copyfile(out_tmp, final_tmp)
-        os.replace(final_tmp, PROBE_LIB_PATH)
+        os.replace(final_tmp, lib_path)
     if verbose:
-        print(f"built {PROBE_LIB_PATH}")
+        print(f"built {lib_path}")
+    return lib_path
+
+
+def build_probes(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
+    """Compile the microbenchmark library (libnanovllm_probes.so) and the
+    decode configuration sweep (libnanovllm_decode_sweep.so)."""
+    with ThreadPoolExecutor(max_workers=2) as pool:
+        jobs = [pool.submit(_build_aux, PROBE_SOURCES, PROBE_LIB_PATH, verbose, extra_flags),
+                pool.submit(_build_aux, SWEEP_SOURCES, SWEEP_LIB_PATH, verbose, extra_flags)]
+        for j in jobs:
+            j.result()
     return PROBE_LIB_PATH
 
 

@@ -204,3 +204,47 @@ def write_tiles(torch, rows=2048, cols_bytes=8192, nontemporal=True, copies=1, r
     us = 1e3 * ctx.time_ms(g.replay) / reps
     return {"bytes": nbytes, "workgroups": tiles_m * tiles_n, "nontemporal": nontemporal, "buffers": copies,
             "us": round(us, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
+
+# ---------------------------------------------------------------------------
+# Decode configuration sweep (csrc/decode_sweep.hip, libnanovllm_decode_sweep.so)
+# ---------------------------------------------------------------------------
+SWEEP_LIB_PATH = Path(__file__).resolve().parent / "libnanovllm_decode_sweep.so"
+_sweep = None
+
+
+def load_sweep():
+    global _sweep
+    if _sweep is None:
+        if not SWEEP_LIB_PATH.is_file():
+            raise RuntimeError(f"{SWEEP_LIB_PATH.name} is not built; run __graft_entry__.build()")
+        lib = ctypes.CDLL(str(SWEEP_LIB_PATH))
+        lib.nvsweep_decode_count.restype = _INT
+        lib.nvsweep_decode_count.argtypes = []
+        lib.nvsweep_decode_name.restype = ctypes.c_char_p
+        lib.nvsweep_decode_name.argtypes = [_INT]
+        lib.nvsweep_decode_max_m.restype = _INT
+        lib.nvsweep_decode_max_m.argtypes = [_INT]
+        lib.nvsweep_decode.restype = _INT
+        lib.nvsweep_decode.argtypes = [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _VP]
+        _sweep = lib
+    return _sweep
+
+
+def sweep_configs():
+    """(index, name, max M) of every decode configuration in the sweep library."""
+    lib = load_sweep()
+    return [(i, lib.nvsweep_decode_name(i).decode(), lib.nvsweep_decode_max_m(i))
+            for i in range(lib.nvsweep_decode_count())]
+
+
+def sweep_launcher(torch, cfg, a, w, c):
+    """A no-argument launch of configuration `cfg` on bf16 a[M,K], w[N,K] into c[M,N]."""
+    lib = load_sweep()
+    m, k = a.shape
+    n = w.shape[0]
+    args = (cfg, a.data_ptr(), w.data_ptr(), c.data_ptr(), m, n, k)
+
+    def f():
+        _check(lib.nvsweep_decode(*args, torch.cuda.current_stream().cuda_stream), "decode sweep")
+    return f

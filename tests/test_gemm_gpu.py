@@ -296,7 +296,8 @@ def test_splitk_wide_n_ragged(m):
     _check_tolerance(out.cpu(), a, w, L.B_NK, torch.float32)
 
 
-SPLITK_CONFIG_CASES = [(1000, 3592, m) for m in (1, 9, 20, 32)] + [(3000, 1000, m) for m in (1, 7, 16, 25)]
+SPLITK_CONFIG_CASES = ([(1000, 3592, m) for m in (1, 9, 20, 32)] + [(3000, 1000, m) for m in (1, 7, 16, 25)]
+                       + [(8224, 1000, m) for m in (3, 12, 29)] + [(16400, 520, m) for m in (5, 16, 32)])
 
 
 @pytest.mark.parametrize("n,k,m", SPLITK_CONFIG_CASES, ids=[f"N{n}-K{k}-M{m}" for n, k, m in SPLITK_CONFIG_CASES])
@@ -304,10 +305,12 @@ SPLITK_CONFIG_CASES = [(1000, 3592, m) for m in (1, 9, 20, 32)] + [(3000, 1000, 
                          ids=["bf16", "f16-f32"])
 def test_splitk_configs_ragged(n, k, m, din, dout):
     """The LDS-staged splitk_decode configurations below the LM head: at most
-    2048 W rows (16 rows per workgroup, 16 or 8 waves) and above (32 rows, 8
-    waves), every A-row count (8, 16, 32), a ragged N and a K that ends in a
-    partial 64-element line (3592 = 56 x 64 + 8, 1000 = 15 x 64 + 40), so
-    the last line copies zeros past K into both W and A."""
+    2048 W rows (16 rows per workgroup, 16 or 8 waves) and above (32 rows
+    while 32-row workgroups fit the CUs; 48 rows, or 8-wave workgroups
+    several to a CU, on wider N: 8224 and 16400 rows), every A-row count
+    (8, 16, 32), a ragged N and a K that ends in a partial 64-element line
+    (3592 = 56 x 64 + 8, 1000 = 15 x 64 + 40, 520 = 8 x 64 + 8), so the last
+    line copies zeros past K into both W and A."""
     _say(f"splitk config N={n} K={k} M={m} {NAME[din]}->{NAME[dout]}")
     gen = torch.Generator().manual_seed(n + k + m)
     a = torch.randn((m, k), generator=gen).to(din)
@@ -637,7 +640,7 @@ ARGMAX_CASES = [(L.KERNEL_SPLITK_DECODE, m) for m in (1, 5, 17, 32)] + [(L.KERNE
 
 
 @pytest.mark.parametrize("kernel,m", ARGMAX_CASES, ids=[f"{L.kernel_name(k)}-M{m}" for k, m in ARGMAX_CASES])
-@pytest.mark.parametrize("n", [1000, 70001])
+@pytest.mark.parametrize("n", [1000, 9000, 70001])
 @pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("rank", ["model", "f32"])
 def test_argmax_equals_argmax_of_own_logits(kernel, m, n, din, rank):
