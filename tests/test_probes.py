@@ -35,3 +35,26 @@ def test_probes_refuse_unsafe_sizes_before_launch():
     # each 128-row tile writes 512 bytes per row: ld must cover tiles_n of them
     assert lib.nvprobe_write_tiles(None, 8192 - 16, 16, 16, 1, None, None) == -1
     assert lib.nvprobe_write_tiles(None, 8192 + 8, 16, 16, 1, None, None) == -1
+
+
+def test_decode_sweep_library_lists_and_refuses():
+    """The decode configuration sweep: every configuration has a name and an
+    A-row limit; launches with a bad configuration, null pointers, M above
+    the configuration's rows or K not a multiple of 8 are refused before
+    anything is launched."""
+    cfgs = P.sweep_configs()
+    assert len(cfgs) >= 10
+    names = [name for _, name, _ in cfgs]
+    assert len(set(names)) == len(names)
+    assert all(name.split()[0] in ("lds", "lines") for name in names)
+    assert {rows for _, _, rows in cfgs} == {8, 16, 32}
+    lib = P.load_sweep()
+    fake = 1 << 20   # never dereferenced: every call below is refused first
+    assert lib.nvsweep_decode(-1, fake, fake, fake, 1, 64, 64, None) == -1
+    assert lib.nvsweep_decode(len(cfgs), fake, fake, fake, 1, 64, 64, None) == -1
+    assert lib.nvsweep_decode(0, None, fake, fake, 1, 64, 64, None) == -1
+    idx8 = next(i for i, _, rows in cfgs if rows == 8)
+    assert lib.nvsweep_decode(idx8, fake, fake, fake, 9, 64, 64, None) == -1
+    assert lib.nvsweep_decode(idx8, fake, fake, fake, 1, 64, 60, None) == -1
+    assert lib.nvsweep_decode(idx8, fake, fake, fake, 0, 64, 64, None) == -1
+    assert lib.nvsweep_decode_name(len(cfgs)) == b""
