@@ -22,6 +22,23 @@ struct ProArgs {
     int64_t ldres;
 };
 
+// Whether a splitk_decode configuration builds: its LDS (the copy regions
+// and, with the norm prologue, the per-wave sums of squares) within the
+// 160 KiB of a CU, the partition tiles within a wave's region, the copies
+// of a batch within the vmcnt range.  Mirrors the kernel's declarations.
+constexpr int64_t kLdsBytes = 160 * 1024;
+
+template <int AROWS, int RG, int WAVES, int LPB, int PARTS, int PRO>
+constexpr bool decode_cfg_fits() {
+    constexpr int MG = AROWS == 8 ? 1 : AROWS / 16;
+    constexpr int IA = AROWS / 8;
+    constexpr int IL = 2 * RG + IA + (PRO == PRO_NONE ? 0 : IA);
+    constexpr int REGION = LPB * IL * 64;
+    constexpr int PW = PARTS / WAVES;
+    constexpr int64_t lds = int64_t(WAVES) * REGION * 16 + (PRO == PRO_ADD_NORM ? WAVES : 1) * MG * 16 * 4;
+    return lds <= kLdsBytes && PW * RG * MG * 256 <= 4 * REGION && LPB * IL < 64 && PARTS % WAVES == 0;
+}
+
 // RG groups of 16 W rows per workgroup, AROWS rows of A copied per line
 // (8, 16, 32 or 64: M rounded up), WAVES waves splitting K, LPB lines per wave
 // in flight at once, PARTS K partitions (a multiple of WAVES), PRO the

@@ -76,6 +76,76 @@ int launch_rows64(const Problem& p, hipStream_t s) {
     }
 }
 
+constexpr int64_t kDecodeCus = 256;
+
+// Workgroups of a configuration resident on one CU at once (LDS, waves and
+// registers), from the runtime's occupancy query, once per configuration.
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int EPI, int PRO>
+int64_t resident_per_cu() {
+    static const int64_t per_cu = [] {
+        int blocks = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &blocks, reinterpret_cast<const void*>(&splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, 1, 16, EPI, PRO>),
+            WAVES * 64, 0);
+        return int64_t(e == hipSuccess && blocks > 0 ? blocks : 1);
+    }();
+    return per_cu;
+}
+
+// Candidate (RG, WAVES) of the wide-W choice, one line per wave in flight,
+// 16 K partitions; those whose LDS does not fit are skipped at compile time.
+struct RowsChoice {
+    int64_t busiest = INT64_MAX, rounds = 0, grid = 0;
+    int waves = 0, id = -1;
+    bool better_than(const RowsChoice& o) const {
+        if (busiest != o.busiest) return busiest < o.busiest;
+        if (rounds != o.rounds) return rounds < o.rounds;
+        if (grid != o.grid) return grid < o.grid;
+        return waves > o.waves;
+    }
+};
+
+template <int DT, int DT_OUT, int EPI, int AROWS, int PRO, int RG, int WAVES>
+void consider(RowsChoice& best, int id, int64_t rows) {
+    if constexpr (decode_cfg_fits<AROWS, RG, WAVES, 1, 16, PRO>()) {
+        RowsChoice c;
+        c.grid = (rows + 16 * RG - 1) / (16 * RG);
+        c.busiest = (c.grid + kDecodeCus - 1) / kDecodeCus * 16 * RG;
+        const int64_t slots = kDecodeCus * resident_per_cu<DT, DT_OUT, AROWS, RG, WAVES, EPI, PRO>();
+        c.rounds = (c.grid + slots - 1) / slots;
+        c.waves = WAVES;
+        c.id = id;
+        if (c.better_than(best)) best = c;
+    }
+}
+
+template <int DT, int DT_OUT, int EPI, int AROWS, int PRO, int RG, int WAVES>
+int launch_if(int id, int want, const Problem& p, hipStream_t s) {
+    if constexpr (decode_cfg_fits<AROWS, RG, WAVES, 1, 16, PRO>())
+        if (id == want) return launch_cfg<DT, DT_OUT, AROWS, RG, WAVES, 1, 16, EPI, PRO>(p, s);
+    return 1;   // not this candidate
+}
+
+template <int DT, int DT_OUT, int EPI, int AROWS, int PRO>
+int launch_picked(const Problem& p, hipStream_t s, int64_t rows) {
+    RowsChoice best;
+    consider<DT, DT_OUT, EPI, AROWS, PRO, 2, 16>(best, 0, rows);
+    consider<DT, DT_OUT, EPI, AROWS, PRO, 3, 16>(best, 1, rows);
+    consider<DT, DT_OUT, EPI, AROWS, PRO, 1, 16>(best, 2, rows);
+    consider<DT, DT_OUT, EPI, AROWS, PRO, 2, 8>(best, 3, rows);
+    consider<DT, DT_OUT, EPI, AROWS, PRO, 3, 8>(best, 4, rows);
+    consider<DT, DT_OUT, EPI, AROWS, PRO, 1, 8>(best, 5, rows);
+    int rc = 1;
+    if (rc == 1) rc = launch_if<DT, DT_OUT, EPI, AROWS, PRO, 2, 16>(0, best.id, p, s);
+    if (rc == 1) rc = launch_if<DT, DT_OUT, EPI, AROWS, PRO, 3, 16>(1, best.id, p, s);
+    if (rc == 1) rc = launch_if<DT, DT_OUT, EPI, AROWS, PRO, 1, 16>(2, best.id, p, s);
+    if (rc == 1) rc = launch_if<DT, DT_OUT, EPI, AROWS, PRO, 2, 8>(3, best.id, p, s);
+    if (rc == 1) rc = launch_if<DT, DT_OUT, EPI, AROWS, PRO, 3, 8>(4, best.id, p, s);
+    if (rc == 1) rc = launch_if<DT, DT_OUT, EPI, AROWS, PRO, 1, 8>(5, best.id, p, s);
+    if (rc == 1) return set_error(NANOVLLM_GEMM_ELAUNCH, "splitk_decode: no configuration fits");
+    return rc;
+}
+
 template <int DT, int DT_OUT, int EPI, int AROWS, int PRO>
 int launch_rows(const Problem& p, hipStream_t s) {
     const int64_t rows = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
@@ -92,29 +162,21 @@ int launch_rows(const Problem& p, hipStream_t s) {
             else return launch_cfg<DT, DT_OUT, AROWS, 1, 16, 1, 16, EPI, PRO>(p, s);
         }
     }
-    // The plain store and the LM-head epilogues above 2048 rows: 32 W rows
+    // Above 2048 rows (plain store, LM-head epilogues, prologues): 32 W rows
     // per 16-wave workgroup while those workgroups fit the 256 CUs at one
-    // each; past that, 48 rows per workgroup while those fit, and beyond
-    // both, configurations that keep two (M <= 8, M > 16) or three (M <= 16,
-    // 8 waves) workgroups resident per CU.  A grid one workgroup past a
-    // round of the CUs pays for a second round.  Measured on MI355X (W
-    // streamed from HBM, bench.py --decode-sweep), M = 4 / 8 / 16 / 32: N =
-    // 8224 (257 workgroups of 32 rows) 5.74 / 5.91 / 7.31 / 8.45 us with 32
-    // rows throughout, 5.34 / 5.43 / 5.65 us with 48 and 7.44 us with two
-    // 8-wave workgroups per CU at M = 32; N = 16384: M = 16 / 32 9.13 / 10.20
-    // against 8.03 / 8.91 us resident; N = 6144 (192 workgroups) as before.
-    if constexpr (EPI != EPI_SILU_MUL && PRO == PRO_NONE) {
-        constexpr int64_t kCus = 256;
-        const bool fits32 = (rows + 31) / 32 <= kCus, fits48 = (rows + 47) / 48 <= kCus;
-        if constexpr (AROWS == 32) {
-            if (fits32) return launch_cfg<DT, DT_OUT, 32, 2, 16, 1, 16, EPI, PRO>(p, s);
-            return launch_cfg<DT, DT_OUT, 32, 2, 8, 1, 16, EPI, PRO>(p, s);
-        } else {
-            if (fits32) return launch_cfg<DT, DT_OUT, AROWS, 2, 16, 1, 16, EPI, PRO>(p, s);
-            if (fits48) return launch_cfg<DT, DT_OUT, AROWS, 3, 16, 1, 16, EPI, PRO>(p, s);
-            if constexpr (AROWS == 16) return launch_cfg<DT, DT_OUT, 16, 2, 8, 1, 16, EPI, PRO>(p, s);
-            else return launch_cfg<DT, DT_OUT, 8, 2, 16, 1, 16, EPI, PRO>(p, s);
-        }
+    // each (every line of a 1024-wide K in flight at once); on wider W the
+    // configuration whose busiest CU streams the fewest W rows, then the one
+    // that needs the fewest rounds of resident workgroups, then the fewest
+    // workgroups (see pick_rows).  A grid one workgroup past a round pays
+    // for a second one.  Measured on MI355X (W streamed from HBM, bench.py
+    // --decode-sweep), M = 4 / 8 / 16 / 32: N = 8224 (257 workgroups of 32
+    // rows) 5.74 / 5.91 / 7.31 / 8.45 us with 32 rows throughout, 5.31 /
+    // 5.44 / 5.68 us with 48 rows and 7.43 us with 8-wave workgroups of 16
+    // rows three to a CU at M = 32; N = 16384, M = 16 / 32: 9.13 / 10.20
+    // against 8.04 / 8.95 us with 8-wave workgroups of 32 rows resident
+    // three / two to a CU.
+    if constexpr (EPI != EPI_SILU_MUL) {
+        if ((rows + 31) / 32 > kDecodeCus) return launch_picked<DT, DT_OUT, EPI, AROWS, PRO>(p, s, rows);
     }
     // 16 waves, one line each: every line of a 1024-wide K is in flight at
     // once.  With 32 rows of A and a prologue operand the copies need 192 KiB

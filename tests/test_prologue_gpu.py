@@ -85,20 +85,22 @@ def test_sigmoid_gate_kernel_vs_oracle(dtype, view):
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 32])
+@pytest.mark.parametrize("n", [1024, 9000])
 @pytest.mark.parametrize("dtype,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
                          ids=["bf16", "f16-f32"])
-def test_gemm_gated_fused_equals_gate_then_gemm(m, dtype, dout):
-    """Qwen3.5 o_proj (N = 1024, K = 8 heads x 256): the gate inside
-    splitk_decode (forced here at every M; the default fuses it up to M = 8)
-    gives the same bits as the gate kernel followed by splitk_decode, and so
-    does the default path; that meets the GEMM bound on the gated operand."""
-    gen = torch.Generator().manual_seed(100 + m)
-    heads, hd, n = 8, 256, 1024
+def test_gemm_gated_fused_equals_gate_then_gemm(m, n, dtype, dout):
+    """Qwen3.5 o_proj (N = 1024, K = 8 heads x 256), and a W wide enough
+    (9000 rows) for the wide-W configurations: the gate inside splitk_decode
+    (forced here at every M; the default fuses it up to M = 8) gives the same
+    bits as the gate kernel followed by splitk_decode, and so does the
+    default path; that meets the GEMM bound on the gated operand."""
+    gen = torch.Generator().manual_seed(100 + m + n)
+    heads, hd = 8, 256
     a = torch.randn((m, heads, hd), generator=gen).to(dtype).to(DEV)
     q_gate, _ = _qgate(m, heads, hd, dtype, gen)
     gate = q_gate.to(DEV).chunk(2, -1)[1]
     w = (torch.randn((n, heads * hd), generator=gen) * 0.02).to(dtype).to(DEV)
-    _say(f"gemm_gated fused M={m} {NAME[dtype]}->{NAME[dout]}")
+    _say(f"gemm_gated fused M={m} N={n} {NAME[dtype]}->{NAME[dout]}")
     fused = K.gemm_gated_with_kernel(a, gate, w, L.KERNEL_SPLITK_DECODE, dout)
     default = K.gemm_gated(a, gate, w, dout)
     operand = K.sigmoid_gate(a, gate)
@@ -192,7 +194,7 @@ def _check_add_norm(out, res_out, h, r, nw, w, eps, dtype, dout):
         assert stats["cancel_beyond"] <= orc.cancellation_cap(ok.size), stats
 
 
-NORM_SHAPES = [(6144, 1024), (1000, 1000), (1024, 3584), (3000, 3592)]
+NORM_SHAPES = [(6144, 1024), (1000, 1000), (1024, 3584), (3000, 3592), (9000, 1000)]
 
 
 @pytest.mark.parametrize("n,k", NORM_SHAPES, ids=[f"N{n}-K{k}" for n, k in NORM_SHAPES])
