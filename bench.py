@@ -217,7 +217,7 @@ def run_probes(torch) -> int:
     # With three 1 KiB fragment reads per copied KiB (about a GEMM K-tile's
     # mix): whether the LDS serves the copies' writes and the reads at once.
     out["copy"] = [P.copy_rate(torch, mode, workgroups=P.CUS, inflight=f, window=win, reads=r)
-                   for win in (16 << 10, 4 << 20) for mode in (0, 1, 2) for f in (8, 16) for r in (0, 3)
+                   for win in (16 << 10, 4 << 20) for mode in (0, 1, 2, 3) for f in (8, 16) for r in (0, 3)
                    if mode != 1 or r == 0]
     for r in out["copy"]:
         log(f"copy: {r}")

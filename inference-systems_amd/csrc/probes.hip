@@ -111,11 +111,8 @@ __global__ __launch_bounds__(512) void lds_read_kernel(int iters, uint32_t* sink
 // second 64 KiB region (the fragment reads a GEMM K-step makes next to its
 // copies), so the LDS serves both.
 template <int INFLIGHT, int READS>
-__global__ __launch_bounds__(512) void dma_kernel(const char* __restrict__ src, int64_t window, int iters,
-                                                  uint32_t* sink, uint64_t* clocks) {
-    __shared__ u32x4_t lds[2 * 64 * 1024 / 16];
-    stamp(clocks, 0);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+__device__ __forceinline__ u32x4_t dma_body(const char* __restrict__ src, int64_t window, int iters, u32x4_t* lds,
+                                            int wave, int lane) {
     const int64_t slots = window / 1024;
     int64_t slot = (int64_t(blockIdx.x) * 8 + wave) * 37 % slots;
     const uint32_t dst0 = __builtin_amdgcn_readfirstlane(lds_address(lds) + uint32_t(wave) * 8192u);
@@ -129,6 +126,16 @@ __global__ __launch_bounds__(512) void dma_kernel(const char* __restrict__ src, 
         wait_vmcnt<INFLIGHT - 1>();
     }
     wait_vmcnt<0>();
+    return acc;
+}
+
+template <int INFLIGHT, int READS>
+__global__ __launch_bounds__(512) void dma_kernel(const char* __restrict__ src, int64_t window, int iters,
+                                                  uint32_t* sink, uint64_t* clocks) {
+    __shared__ u32x4_t lds[2 * 64 * 1024 / 16];
+    stamp(clocks, 0);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const u32x4_t acc = dma_body<INFLIGHT, READS>(src, window, iters, lds, wave, lane);
     __syncthreads();
     sink_wave(sink, fold(lds[wave * 512 + lane] ^ acc));
     stamp(clocks, 1);
@@ -138,11 +145,8 @@ __global__ __launch_bounds__(512) void dma_kernel(const char* __restrict__ src, 
 // into a register; with STORE the loaded chunks are also written to LDS
 // with ds_write_b128 (the register-staged copy path); READS as above.
 template <int INFLIGHT, int STORE, int READS>
-__global__ __launch_bounds__(512) void vload_kernel(const char* __restrict__ src, int64_t window, int iters,
-                                                    uint32_t* sink, uint64_t* clocks) {
-    __shared__ u32x4_t lds[2 * 64 * 1024 / 16];
-    stamp(clocks, 0);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ u32x4_t vload_body(const char* __restrict__ src, int64_t window, int iters, u32x4_t* lds,
+                                              int wave, int lane) {
     const int64_t slots = window / 1024;
     int64_t slot = (int64_t(blockIdx.x) * 8 + wave) * 37 % slots;
     const u32x4_t* rd = lds + 4096 + wave * 512 + lane;
@@ -165,11 +169,38 @@ __global__ __launch_bounds__(512) void vload_kernel(const char* __restrict__ src
         // just because the next round overwrites the same LDS slots.
         asm volatile("" ::: "memory");
     }
+    return acc;
+}
+
+template <int INFLIGHT, int STORE, int READS>
+__global__ __launch_bounds__(512) void vload_kernel(const char* __restrict__ src, int64_t window, int iters,
+                                                    uint32_t* sink, uint64_t* clocks) {
+    __shared__ u32x4_t lds[2 * 64 * 1024 / 16];
+    stamp(clocks, 0);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    u32x4_t acc = vload_body<INFLIGHT, STORE, READS>(src, window, iters, lds, wave, lane);
     if constexpr (STORE) {
         __syncthreads();
         acc ^= lds[wave * 512 + lane];
     }
     sink_wave(sink, fold(acc));
+    stamp(clocks, 1);
+}
+
+// Both copy paths at once: waves 0-3 copy with global_load_lds_dwordx4,
+// waves 4-7 load into registers and write LDS with ds_write_b128 (the same
+// bytes per wave), to see whether the two paths add up.
+template <int INFLIGHT, int READS>
+__global__ __launch_bounds__(512) void hybrid_kernel(const char* __restrict__ src, int64_t window, int iters,
+                                                     uint32_t* sink, uint64_t* clocks) {
+    __shared__ u32x4_t lds[2 * 64 * 1024 / 16];
+    stamp(clocks, 0);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    u32x4_t acc;
+    if (wave < 4) acc = dma_body<INFLIGHT, READS>(src, window, iters, lds, wave, lane);
+    else acc = vload_body<INFLIGHT, 1, READS>(src, window, iters, lds, wave, lane);
+    __syncthreads();
+    sink_wave(sink, fold(lds[wave * 512 + lane] ^ acc));
     stamp(clocks, 1);
 }
 
@@ -259,10 +290,12 @@ int nvprobe_lds_read(int workgroups, int iters, uint32_t* sink, uint64_t* clocks
 
 // src holds `window` bytes, a positive multiple of 1024.  mode 0: copies to
 // LDS (global_load_lds_dwordx4); 1: loads to registers; 2: loads to
-// registers + ds_write_b128.  iters must be a positive multiple of inflight
-// (8 or 16); reads (0 or 3) ds_read_b128 accompany each copy.
+// registers + ds_write_b128; 3: modes 0 and 2 in half the waves each.
+// iters must be a positive multiple of inflight (8 or 16); reads (0 or 3)
+// ds_read_b128 accompany each copy.  src and sink must be device pointers.
 int nvprobe_copy(int mode, const void* src, int64_t window, int workgroups, int iters, int inflight, int reads,
                  uint32_t* sink, uint64_t* clocks, hipStream_t s) {
+    if (src == nullptr || sink == nullptr) return kErr;
     if (workgroups < 1 || iters < 1 || window < 1024 || window % 1024) return kErr;
     if ((inflight != 8 && inflight != 16) || (reads != 0 && reads != 3)) return kErr;
     if (iters % inflight) return kErr;
@@ -272,6 +305,7 @@ int nvprobe_copy(int mode, const void* src, int64_t window, int workgroups, int 
     if (mode == 0) hipLaunchKernelGGL((dma_kernel<F, R>), g, b, 0, s, p, window, iters, sink, clocks);   \
     else if (mode == 1) hipLaunchKernelGGL((vload_kernel<F, 0, R>), g, b, 0, s, p, window, iters, sink, clocks); \
     else if (mode == 2) hipLaunchKernelGGL((vload_kernel<F, 1, R>), g, b, 0, s, p, window, iters, sink, clocks); \
+    else if (mode == 3) hipLaunchKernelGGL((hybrid_kernel<F, R>), g, b, 0, s, p, window, iters, sink, clocks);   \
     else return kErr;
     if (inflight == 8 && reads == 0) { NVPROBE_COPY(8, 0) }
     else if (inflight == 8) { NVPROBE_COPY(8, 3) }

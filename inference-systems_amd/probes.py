@@ -147,7 +147,8 @@ def lds_read(torch, workgroups=CUS, iters=1024):
 
 
 COPY_MODES = {0: "global_load_lds_dwordx4 (to LDS)", 1: "global_load_dwordx4 (to VGPRs)",
-              2: "global_load_dwordx4 + ds_write_b128 (to LDS through VGPRs)"}
+              2: "global_load_dwordx4 + ds_write_b128 (to LDS through VGPRs)",
+              3: "half the waves each of modes 0 and 2 (to LDS)"}
 
 
 def copy_rate(torch, mode, workgroups=CUS, iters=512, inflight=8, window=4 << 20, reads=0):

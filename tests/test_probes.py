@@ -26,11 +26,14 @@ def test_probes_refuse_unsafe_sizes_before_launch():
     assert lib.nvprobe_lds_read(256, 12, None, None, None) == -1
     assert lib.nvprobe_lds_read(0, 16, None, None, None) == -1
     # copy window: a positive multiple of 1 KiB; in-flight 8 or 16; iterations a multiple of it
-    assert lib.nvprobe_copy(0, None, 1000, 256, 64, 8, 0, None, None, None) == -1
-    assert lib.nvprobe_copy(0, None, 4096, 256, 64, 4, 0, None, None, None) == -1
-    assert lib.nvprobe_copy(0, None, 4096, 256, 60, 8, 0, None, None, None) == -1
-    assert lib.nvprobe_copy(0, None, 4096, 256, 64, 8, 2, None, None, None) == -1
-    assert lib.nvprobe_copy(3, None, 4096, 256, 64, 8, 0, None, None, None) == -1
+    fake = 1 << 20   # never dereferenced: every call below is refused first
+    assert lib.nvprobe_copy(0, None, 4096, 256, 64, 8, 0, fake, None, None) == -1
+    assert lib.nvprobe_copy(0, fake, 4096, 256, 64, 8, 0, None, None, None) == -1
+    assert lib.nvprobe_copy(0, fake, 1000, 256, 64, 8, 0, fake, None, None) == -1
+    assert lib.nvprobe_copy(0, fake, 4096, 256, 64, 4, 0, fake, None, None) == -1
+    assert lib.nvprobe_copy(0, fake, 4096, 256, 60, 8, 0, fake, None, None) == -1
+    assert lib.nvprobe_copy(0, fake, 4096, 256, 64, 8, 2, fake, None, None) == -1
+    assert lib.nvprobe_copy(4, fake, 4096, 256, 64, 8, 0, fake, None, None) == -1
     assert lib.nvprobe_mfma(256, 16, 3, None, None, None) == -1
     # each 128-row tile writes 512 bytes per row: ld must cover tiles_n of them
     assert lib.nvprobe_write_tiles(None, 8192 - 16, 16, 16, 1, None, None) == -1
