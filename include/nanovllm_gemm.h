@@ -61,14 +61,17 @@ enum {
  *   MFMA_DIRECT    one wave per 32x32 C tile, operands straight from
  *                  global memory, any shape          (gemm_bench.cu:80-115, gemm_wmma.cu:56-104)
  *   MFMA_STAGED    LDS multi-buffered macro-tile MFMA kernel for
- *                  prefill-shaped problems on W[N,K], and for every M on
- *                  B[K,N] with N a multiple of 8 (B's k-rows copied to
- *                  LDS as they lie, read back transposed)
+ *                  prefill-shaped problems on W[N,K] and on B[K,N] with N a
+ *                  multiple of 8 (B's k-rows copied to LDS as they lie,
+ *                  read back transposed)
  *                                                    (gemm_bench.cu:117-196, gemm_wmma.cu:116-207)
  *   SPLITK_DECODE  split-K wavefront-reduction kernel for M <= 32 (the
  *                  plain GEMM and the fused SiLU-and-mul up to M = 64 below
- *                  65536 W rows) that streams W once, copied to LDS in
- *                  whole 128-byte lines; selected for 2 <= M <= 32, for
+ *                  65536 W rows; B[K,N] up to M = 64, 64 columns per
+ *                  workgroup, read back transposed) that streams W once,
+ *                  copied to LDS in whole 128-byte lines; selected for
+ *                  B[K,N] up to M = 32 (M = 64 on N <= 4096) and, on W[N,K],
+ *                  for 2 <= M <= 32, for
  *                  M == 1 when W is larger than 64 MiB (LM head), for
  *                  33 <= M <= 64 when N <= 4096 (or N <= 10240 with
  *                  K <= 1024), and for the fused SiLU-and-mul at every

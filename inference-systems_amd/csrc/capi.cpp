@@ -95,7 +95,8 @@ bool supports(int kernel_id, int64_t m, int64_t n, int64_t k, int64_t lda, int64
             return is_half(din) &&
                    (vector_ok(k, lda, ldb, b_layout, aligned16) || kn_vector_ok(n, k, lda, ldb, b_layout, aligned16));
         case NANOVLLM_GEMM_KERNEL_SPLITK_DECODE:
-            return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && splitk_plain_ok(m, n);
+            return is_half(din) && ((vector_ok(k, lda, ldb, b_layout, aligned16) && splitk_plain_ok(m, n)) ||
+                                    (kn_vector_ok(n, k, lda, ldb, b_layout, aligned16) && m <= kSplitkPlainMaxM));
         case NANOVLLM_GEMM_KERNEL_GEMV_DECODE:
             return is_half(din) && vector_ok(k, lda, ldb, b_layout, aligned16) && m == 1;
         default: return false;
@@ -121,11 +122,17 @@ int select(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_layo
             return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
         return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
     }
-    // B[K,N] (the reference bench's layout): the staged kernel at every M
-    // (the decode kernels read W[N,K] only; on the reference's B[K,N] shapes
-    // at M = 1 / 16 the staged rung ran 6.2-10.0 us against 9.3-18.4 us for
-    // the direct one).
-    if (kn_vector_ok(n, k, lda, ldb, b_layout, aligned16)) return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
+    // B[K,N] (the reference bench's layout): splitk_decode up to M = 32 and
+    // up to M = 64 on at most 4096 columns, the staged kernel above.  On the
+    // reference's shape matrix (bf16, fp32 out) splitk_decode took M = 1 / 16
+    // from 6.2-9.9 us (staged) to 3.7-4.6 us, and 64 x 1024 x 2048 / 3584
+    // from 10.0 / 15.8 to 8.1 / 10.8 us; at 64 x 6144 / 7168 (96 / 112
+    // workgroups of 64 columns) it ran 6.8 / 7.0 against 6.6 / 6.7 us.
+    if (kn_vector_ok(n, k, lda, ldb, b_layout, aligned16)) {
+        if (m <= kDecodeMaxM || (m <= kSplitkPlainMaxM && n <= kSplitkPlainNarrowN))
+            return NANOVLLM_GEMM_KERNEL_SPLITK_DECODE;
+        return NANOVLLM_GEMM_KERNEL_MFMA_STAGED;
+    }
     return NANOVLLM_GEMM_KERNEL_MFMA_DIRECT;
 }
 

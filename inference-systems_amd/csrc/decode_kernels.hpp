@@ -22,6 +22,13 @@ struct ProArgs {
     int64_t ldres;
 };
 
+// B[K,N] lines: position of column chunk c of k-row r is c ^ kn_line_swizzle(r).
+// A fragment read touches k-rows {0..3, 8..11, 16..19, 24..27} (+ 4) x 32
+// bytes; rows r and r + 2 share banks (128-byte rows), and flipping chunk
+// pairs by bits 1 and 3 of r puts the 8 rows of each parity on 4 distinct
+// 32-byte bank groups, two each: two clocks, the minimum for 512 bytes.
+__device__ __forceinline__ int kn_line_swizzle(int r) { return 2 * (((r >> 1) & 1) | ((r >> 2) & 2)); }
+
 // Whether a splitk_decode configuration builds: its LDS (the copy regions
 // and, with the norm prologue, the per-wave sums of squares) within the
 // 160 KiB of a CU, the partition tiles within a wave's region, the copies
@@ -43,7 +50,15 @@ constexpr bool decode_cfg_fits() {
 // (8, 16, 32 or 64: M rounded up), WAVES waves splitting K, LPB lines per wave
 // in flight at once, PARTS K partitions (a multiple of WAVES), PRO the
 // prologue on A.
-template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO>
+//
+// KN: B is given as B[K,N] (row stride ldb >= N, N a multiple of 8), the
+// reference bench's layout, with RG = 4: a workgroup takes 64 output
+// columns, and a line is 64 k-rows of B x those 64 columns (128 bytes of a
+// k-row), copied as they lie by 8 instructions of 8 k-rows.  k-row r holds
+// its 16-byte column chunks in position chunk ^ kn_line_swizzle(r), and the
+// W fragments (8 consecutive k of one column per lane) are read back with
+// gfx950's transposing LDS read, two ds_read_b64_tr_b16 of 4 k-rows each.
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO, int KN = 0>
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
@@ -56,6 +71,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     constexpr int IL = IW + IA + IP;
     static_assert(PRO == PRO_NONE || EPI == EPI_NONE || (PRO == PRO_ADD_NORM && EPI == EPI_SILU_MUL),
                   "prologues come with the plain store (and the norm also with SiLU-and-mul)");
+    static_assert(!KN || (RG == 4 && EPI == EPI_NONE && PRO == PRO_NONE), "B[K,N]: 64 columns, plain store");
     static_assert(LPB * IL < 64, "vmcnt range");
     static_assert(PARTS % WAVES == 0, "whole partitions per wave");
     constexpr int PW = PARTS / WAVES;                  // partitions per wave
@@ -92,10 +108,17 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     for (int h = 0; h < IW; ++h) {
         const int r = h >> 1;
         const int64_t rr = 8 * (h & 1) + r8;
-        if constexpr (EPI == EPI_SILU_MUL)
+        if constexpr (KN) {
+            // k-row 8 h + r8 of the line; column chunks past N read the last
+            // chunk (their outputs are not stored).
+            const int kr = 8 * h + r8;
+            const int64_t col = n0 + 8 * ((lane & 7) ^ kn_line_swizzle(kr));
+            wsrc[h] = w + int64_t(kr) * ldb + min_i64(col, n - 8);
+        } else if constexpr (EPI == EPI_SILU_MUL) {
             wsrc[h] = w + ((r & 1) ? n : 0) * ldb + min_i64(n0 + 16 * (r >> 1) + rr, n - 1) * ldb + chunk * 8;
-        else
+        } else {
             wsrc[h] = w + min_i64(n0 + 16 * r + rr, n - 1) * ldb + chunk * 8;
+        }
     }
     const uint16_t* asrc[IA];
 #pragma unroll
@@ -147,7 +170,17 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                     for (int st = 0; st < 2; ++st)
                         nwv[t][st] = load16(pro.norm_w + min_i64(koff + (4 * st + grp) * 8, k - 8));
                 }
-                if (koff + kLine <= k) {
+                if constexpr (KN) {
+                    // k-rows past K and A chunks past K copy zeros.
+                    const bool in_k = koff + chunk * 8 < k;
+#pragma unroll
+                    for (int h = 0; h < IW; ++h)
+                        dma16(koff + 8 * h + r8 < k ? static_cast<const void*>(wsrc[h] + koff * ldb) : zero,
+                              dst + 1024u * h);
+#pragma unroll
+                    for (int h = 0; h < IA; ++h)
+                        dma16(in_k ? static_cast<const void*>(asrc[h] + koff) : zero, dst + 1024u * (IW + h));
+                } else if (koff + kLine <= k) {
 #pragma unroll
                     for (int h = 0; h < IW; ++h) dma16(wsrc[h] + koff, dst + 1024u * h);
 #pragma unroll
@@ -200,8 +233,27 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                 for (int st = 0; st < 2; ++st) {
                     const int slot = st ? slot1 : slot0;
                     u32x4_t wf[RG], af[MG];
+                    if constexpr (KN) {
+                        // Lane 16 g + j of a read points at k-row 32 st + 8 g + j / 4
+                        // (+ 4 for the second) and columns 16 r + 4 (j % 4) .. + 3; lane
+                        // 16 g + i receives k = 32 st + 8 g .. + 7 of column 16 r + i.
+                        typedef short v4i16_t __attribute__((ext_vector_type(4)));
+                        typedef __attribute__((address_space(3))) v4i16_t* lds_v4;
+                        const int kr = 32 * st + 8 * grp + (i16 >> 2);
+                        const uint32_t rowb = lds_address(lb) + uint32_t(kr) * 128u + 8u * (i16 & 1);
 #pragma unroll
-                    for (int r = 0; r < RG; ++r) wf[r] = lb[(2 * r + hi) * 64 + slot];
+                        for (int r = 0; r < RG; ++r) {
+                            const int ch = (2 * r + ((i16 & 3) >> 1)) ^ kn_line_swizzle(kr);
+                            const uint32_t a0 = rowb + uint32_t(ch) * 16u;
+                            const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4)(uintptr_t)a0);
+                            const v4i16_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4)(uintptr_t)(a0 + 512u));
+                            const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi4);
+                            wf[r] = u32x4_t{l2[0], l2[1], h2[0], h2[1]};
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < RG; ++r) wf[r] = lb[(2 * r + hi) * 64 + slot];
+                    }
 #pragma unroll
                     for (int g = 0; g < MG; ++g) af[g] = lb[(IW + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot];
                     if constexpr (PRO == PRO_ADD_NORM) {
@@ -422,7 +474,8 @@ int launch_regs(const Problem& p, hipStream_t s) {
     return check_launch("splitk_decode");
 }
 
-template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO = PRO_NONE>
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO = PRO_NONE,
+          int KN = 0>
 int launch_cfg(const Problem& p, hipStream_t s) {
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;
     if (p.m > AROWS) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above the configuration's rows");
@@ -432,7 +485,7 @@ int launch_cfg(const Problem& p, hipStream_t s) {
     if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
     const ProArgs pro{static_cast<const uint16_t*>(p.a2), p.lda2, p.group, p.group_stride,
                       static_cast<const uint16_t*>(p.norm_w), p.eps, static_cast<uint16_t*>(p.res_out), p.ldres};
-    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI, PRO>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI, PRO, KN>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
                        p.lda, p.ldb, p.ldc, p.keys, pro, p.sample);
     return check_launch("splitk_decode");

@@ -213,9 +213,31 @@ int launch_argmax(const Problem& p, hipStream_t s) {
     return launch_epi<DT, NANOVLLM_GEMM_F32, EPI_ARGMAX>(p, s);
 }
 
+// B[K,N] (the reference bench's layout), plain store, M <= 64: 64 columns
+// per workgroup, K split over the waves by 64-k-row lines; 16 waves up to
+// M = 8 (144 KiB of LDS), 8 waves with 8 K partitions above.
+template <int DT, int DT_OUT>
+int launch_kn(const Problem& p, hipStream_t s) {
+    if (p.m <= 8) return launch_cfg<DT, DT_OUT, 8, 4, 16, 1, 16, EPI_NONE, PRO_NONE, 1>(p, s);
+    if (p.m <= 16) return launch_cfg<DT, DT_OUT, 16, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>(p, s);
+    if (p.m <= 32) return launch_cfg<DT, DT_OUT, 32, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>(p, s);
+    if (p.m <= 64) return launch_cfg<DT, DT_OUT, 64, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>(p, s);
+    return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: B[K,N] above M = 64");
+}
+
 }  // namespace
 
 int launch_splitk_decode(const Problem& p, hipStream_t s) {
+    if (p.b_layout == NANOVLLM_GEMM_B_KN) {
+        if (p.epi != EPI_NONE || p.pro != PRO_NONE)
+            return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: B[K,N] takes the plain GEMM only");
+        if (p.dtype_in == NANOVLLM_GEMM_BF16) {
+            if (p.dtype_out == NANOVLLM_GEMM_BF16) return launch_kn<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_BF16>(p, s);
+            return launch_kn<NANOVLLM_GEMM_BF16, NANOVLLM_GEMM_F32>(p, s);
+        }
+        if (p.dtype_out == NANOVLLM_GEMM_F16) return launch_kn<NANOVLLM_GEMM_F16, NANOVLLM_GEMM_F16>(p, s);
+        return launch_kn<NANOVLLM_GEMM_F16, NANOVLLM_GEMM_F32>(p, s);
+    }
     if (p.epi == EPI_ARGMAX) {
         if (p.dtype_in == NANOVLLM_GEMM_BF16) return launch_argmax<NANOVLLM_GEMM_BF16>(p, s);
         return launch_argmax<NANOVLLM_GEMM_F16>(p, s);

@@ -111,10 +111,11 @@ def _expected(m, n, k, lda, ldb, layout, din, aligned):
         if m <= 64 and (n <= 4096 or (n <= 10240 and k <= 1024)):
             return L.KERNEL_SPLITK_DECODE
         return L.KERNEL_MFMA_STAGED
-    # B[K,N] with whole 8-column chunks: the staged kernel
+    # B[K,N] with whole 8-column chunks: splitk_decode up to M = 32, and up to
+    # M = 64 on at most 4096 columns; the staged kernel above
     kn_vec = aligned and k % 8 == 0 and lda % 8 == 0 and ldb % 8 == 0 and n % 8 == 0 and layout == KN
     if kn_vec:
-        return L.KERNEL_MFMA_STAGED
+        return L.KERNEL_SPLITK_DECODE if m <= 32 or (m <= 64 and n <= 4096) else L.KERNEL_MFMA_STAGED
     return L.KERNEL_MFMA_DIRECT
 
 
@@ -158,9 +159,11 @@ def test_selection_on_workloads_and_qwen_shapes():
         kid = L.select(m, n, k, k, k, n, NK, BF16, BF16, 1)
         want_k = "gemv_decode" if m == 1 else ("splitk_decode" if m <= 64 else "mfma_staged")
         assert L.kernel_name(kid) == want_k, label
-        # the reference's B[K,N] layout of the same shapes: the staged rung
+        # the reference's B[K,N] layout of the same shapes: splitk_decode up to M = 32 (and
+        # M = 64 on N <= 4096), the staged rung above
         kid = L.select(m, n, k, k, n, n, KN, BF16, F32, 1)
-        assert L.kernel_name(kid) == "mfma_staged", label
+        want_kn = "splitk_decode" if m <= 32 or (m <= 64 and n <= 4096) else "mfma_staged"
+        assert L.kernel_name(kid) == want_kn, label
 
 
 def test_no_vendor_kernel_id():

@@ -269,7 +269,8 @@ def test_staged_kn_ragged(m, n, k, din, dout):
     gen = torch.Generator().manual_seed(m + 3 * n)
     a = torch.randn((m, k), generator=gen).to(din)
     b = (torch.randn((k, n), generator=gen) * 0.1).to(din)
-    assert L.select(m, n, k, k, n, n, L.B_KN, CODE[din], CODE[dout], True) == L.KERNEL_MFMA_STAGED
+    want = L.KERNEL_SPLITK_DECODE if m <= 32 or (m <= 64 and n <= 4096) else L.KERNEL_MFMA_STAGED
+    assert L.select(m, n, k, k, n, n, L.B_KN, CODE[din], CODE[dout], True) == want
     out = G.gemm_with_kernel(a.to(DEV), b.to(DEV), L.KERNEL_MFMA_STAGED, dout, L.B_KN)
     torch.cuda.synchronize()
     rows = np.unique(np.concatenate([np.linspace(0, m - 1, 48).astype(int), np.arange(max(m - 16, 0), m)]))
@@ -278,6 +279,36 @@ def test_staged_kn_ragged(m, n, k, din, dout):
     out_nk = G.gemm_with_kernel(a.to(DEV), b.t().contiguous().to(DEV), L.KERNEL_MFMA_STAGED, dout, L.B_NK)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), out_nk.cpu())
+
+
+SPLITK_KN_CASES = [(1, 6144, 1024), (5, 200, 136), (8, 8224, 1000), (16, 1024, 2048), (13, 520, 1000),
+                   (29, 4104, 520), (33, 1000, 72), (64, 7168, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLITK_KN_CASES, ids=[f"M{m}-N{n}-K{k}" for m, n, k in SPLITK_KN_CASES])
+@pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)],
+                         ids=["bf16", "f16-f32"])
+def test_splitk_kn_ragged(m, n, k, din, dout):
+    """splitk_decode on B[K,N] (the reference bench's layout) up to M = 64:
+    64 columns per workgroup, B's k-rows copied as they lie and read back
+    with the transposing LDS read; N a multiple of 8 but not of 64 (the last
+    workgroup's chunks past N read the last chunk and are not stored), K
+    ending in a partial 64-row line (zeros past K), every A-row count.  Up to
+    M = 8 both layouts use 16 K partitions in the same order, so the product
+    equals the W[N,K] splitk_decode result bit for bit."""
+    _say(f"splitk B[K,N] M={m} N={n} K={k} {NAME[din]}->{NAME[dout]}")
+    gen = torch.Generator().manual_seed(5 * m + n + k)
+    a = torch.randn((m, k), generator=gen).to(din)
+    b = (torch.randn((k, n), generator=gen) * 0.1).to(din)
+    want = L.KERNEL_SPLITK_DECODE if m <= 32 or n <= 4096 else L.KERNEL_MFMA_STAGED
+    assert L.select(m, n, k, k, n, n, L.B_KN, CODE[din], CODE[dout], True) == want
+    out = G.gemm_with_kernel(a.to(DEV), b.to(DEV), L.KERNEL_SPLITK_DECODE, dout, L.B_KN)
+    torch.cuda.synchronize()
+    _check_tolerance(out.cpu(), a, b, L.B_KN, dout)
+    if m <= 8:
+        out_nk = G.gemm_with_kernel(a.to(DEV), b.t().contiguous().to(DEV), L.KERNEL_SPLITK_DECODE, dout, L.B_NK)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), out_nk.cpu())
 
 
 @pytest.mark.parametrize("m", [1, 5, 13, 29])
@@ -995,5 +1026,6 @@ def test_reference_shape_matrix():
         assert r["status"] == "PASS", r
         for c in ("direct_max_abs", "staged_max_abs", "dispatch_max_abs", "staged_nk_max_abs", "dispatch_nk_max_abs"):
             assert float(r[c]) == 0.0, (r["label"], c)
-        # on B[K,N] the table takes the staged rung
-        assert r["dispatch"] == "mfma_staged", r["label"]
+        # on B[K,N] the table takes splitk_decode up to M = 32 (M = 64 on N <= 4096), the staged rung above
+        mm, nn = int(r["M"]), int(r["N"])
+        assert r["dispatch"] == ("splitk_decode" if mm <= 32 or (mm <= 64 and nn <= 4096) else "mfma_staged"), r["label"]
