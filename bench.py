@@ -257,6 +257,7 @@ def run_decode_sweep(torch, L) -> int:
         w0 = w_cpu.cuda()
         copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (n * k * 2)) + 1)
         ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        bs = [wt.t().contiguous() for wt in ws]    # the same matrices as B[K,N]
         for m in (1, 4, 8, 16, 32):
             a = torch.randn(m, k, generator=gen).bfloat16().cuda()
             ref = (a.float() @ w0.float().T)
@@ -266,24 +267,25 @@ def run_decode_sweep(torch, L) -> int:
             def product(wt):
                 args_ = (a.data_ptr(), wt.data_ptr(), c.data_ptr(), m, n, k, k, k, n, L.B_NK, L.BF16, L.BF16)
                 return lambda: L.gemm_raw(*args_, torch.cuda.current_stream().cuda_stream)
-            runs = [("selected " + L.kernel_name(kid), product)]
-            for idx, name, max_m in cfgs:
+            runs = [("selected " + L.kernel_name(kid), False, product)]
+            for idx, name, max_m, kn in cfgs:
                 if max_m >= m and max_m < 2 * max(m, 8):   # the configurations with the fewest rows of A that fit
-                    runs.append((name, lambda wt, idx=idx: P.sweep_launcher(torch, idx, a, wt, c)))
-            for name, make in runs:
+                    runs.append((name, kn, lambda wt, idx=idx: P.sweep_launcher(torch, idx, a, wt, c)))
+            for name, kn, make in runs:
+                mats = bs if kn else ws
                 c.zero_()
-                make(w0)()
+                make(mats[0])()
                 torch.cuda.synchronize()
                 err = float((c.float() - ref).abs().max())
                 tol = float(ref.abs().max()) * 2 ** -7 + 1e-3
-                t_ms = median_graph_ms(torch, [make(ws[i % copies]) for i in range(copies * 10)], trials=3)
+                t_ms = median_graph_ms(torch, [make(mats[i % copies]) for i in range(copies * 10)], trials=3)
                 gbs = (n * k + m * k + m * n) * 2 / (t_ms * 1e-3) / 1e9
                 row = {"n": n, "k": k, "m": m, "config": name, "us": round(t_ms * 1e3, 3), "GB/s": round(gbs, 1),
                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "max_abs_err": err, "ok": err <= tol}
                 out["rows"].append(row)
                 log(f"N={n} K={k} M={m:2d} {name:40s} {row['us']:7.2f} us  {gbs:6.0f} GB/s  "
                     f"err {err:.3g}{'' if row['ok'] else '  WRONG'}")
-        del ws, w0
+        del ws, bs, w0
         torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
     return 0 if all(r["ok"] for r in out["rows"]) else 1

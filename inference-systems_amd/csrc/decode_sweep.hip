@@ -7,6 +7,8 @@
 // same kernel templates as the GEMM library.
 //   lds   rows = rows of A per copy, rg = W rows per workgroup, waves, lpb =
 //         lines per wave copied together (16 K partitions)
+//   kn    the B[K,N] form of splitk_decode: rows of A per copy, 64 columns
+//         per workgroup, waves, lpb (16 partitions with 16 waves, 8 with 8)
 //   lines rows = rows of A loaded per line, rg = W rows per workgroup, waves,
 //         lpb = lines per wave loaded together (16 K partitions); the
 //         register-loading kernel below, which the GEMM library does not use
@@ -171,56 +173,61 @@ struct SweepConfig {
     int (*launch)(const Problem&, hipStream_t);
     const char* name;
     int max_m;
+    int kn;   // 1: B[K,N] (ldb = N), else W[N,K] (ldb = K)
 };
 
 #define DECODE_SWEEP_CONFIGS(X) \
-    X((launch_cfg<BF, BF, 8, 1, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=16 waves=16 lpb=1", 8) \
-    X((launch_cfg<BF, BF, 8, 2, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=32 waves=16 lpb=1", 8) \
-    X((launch_cfg<BF, BF, 8, 2, 8, 2, 16, EPI_NONE>), "lds rows=8 rg=32 waves=8 lpb=2", 8) \
-    X((launch_cfg<BF, BF, 16, 1, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=16 waves=16 lpb=1", 16) \
-    X((launch_cfg<BF, BF, 16, 2, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=32 waves=16 lpb=1", 16) \
-    X((launch_cfg<BF, BF, 16, 2, 8, 2, 16, EPI_NONE>), "lds rows=16 rg=32 waves=8 lpb=2", 16) \
-    X((launch_cfg<BF, BF, 32, 1, 16, 1, 16, EPI_NONE>), "lds rows=32 rg=16 waves=16 lpb=1", 32) \
-    X((launch_cfg<BF, BF, 32, 2, 16, 1, 16, EPI_NONE>), "lds rows=32 rg=32 waves=16 lpb=1", 32) \
-    X((launch_cfg<BF, BF, 32, 2, 8, 2, 16, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=2", 32) \
-    X((launch_cfg<BF, BF, 8, 2, 8, 1, 16, EPI_NONE>), "lds rows=8 rg=32 waves=8 lpb=1", 8) \
-    X((launch_cfg<BF, BF, 8, 3, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=48 waves=16 lpb=1", 8) \
-    X((launch_cfg<BF, BF, 8, 4, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=64 waves=16 lpb=1", 8) \
-    X((launch_cfg<BF, BF, 16, 2, 8, 1, 16, EPI_NONE>), "lds rows=16 rg=32 waves=8 lpb=1", 16) \
-    X((launch_cfg<BF, BF, 16, 3, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=48 waves=16 lpb=1", 16) \
-    X((launch_cfg<BF, BF, 32, 1, 8, 1, 16, EPI_NONE>), "lds rows=32 rg=16 waves=8 lpb=1", 32) \
-    X((launch_cfg<BF, BF, 32, 2, 8, 1, 16, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=1", 32) \
-    X((launch_lines<1, 1, 16, 1>), "lines rows=8 rg=8 waves=16 lpb=1", 8) \
-    X((launch_lines<1, 2, 16, 1>), "lines rows=8 rg=16 waves=16 lpb=1", 8) \
-    X((launch_lines<1, 4, 16, 1>), "lines rows=8 rg=32 waves=16 lpb=1", 8) \
-    X((launch_lines<1, 8, 16, 1>), "lines rows=8 rg=64 waves=16 lpb=1", 8) \
-    X((launch_lines<1, 1, 8, 2>), "lines rows=8 rg=8 waves=8 lpb=2", 8) \
-    X((launch_lines<1, 2, 8, 2>), "lines rows=8 rg=16 waves=8 lpb=2", 8) \
-    X((launch_lines<1, 4, 8, 2>), "lines rows=8 rg=32 waves=8 lpb=2", 8) \
-    X((launch_lines<1, 8, 8, 2>), "lines rows=8 rg=64 waves=8 lpb=2", 8) \
-    X((launch_lines<1, 1, 4, 4>), "lines rows=8 rg=8 waves=4 lpb=4", 8) \
-    X((launch_lines<1, 2, 4, 4>), "lines rows=8 rg=16 waves=4 lpb=4", 8) \
-    X((launch_lines<1, 4, 4, 4>), "lines rows=8 rg=32 waves=4 lpb=4", 8) \
-    X((launch_lines<2, 1, 16, 1>), "lines rows=16 rg=8 waves=16 lpb=1", 16) \
-    X((launch_lines<2, 2, 16, 1>), "lines rows=16 rg=16 waves=16 lpb=1", 16) \
-    X((launch_lines<2, 4, 16, 1>), "lines rows=16 rg=32 waves=16 lpb=1", 16) \
-    X((launch_lines<2, 1, 8, 2>), "lines rows=16 rg=8 waves=8 lpb=2", 16) \
-    X((launch_lines<2, 2, 8, 2>), "lines rows=16 rg=16 waves=8 lpb=2", 16) \
-    X((launch_lines<2, 4, 8, 2>), "lines rows=16 rg=32 waves=8 lpb=2", 16) \
-    X((launch_lines<2, 8, 8, 2>), "lines rows=16 rg=64 waves=8 lpb=2", 16) \
-    X((launch_lines<2, 1, 4, 4>), "lines rows=16 rg=8 waves=4 lpb=4", 16) \
-    X((launch_lines<2, 2, 4, 4>), "lines rows=16 rg=16 waves=4 lpb=4", 16) \
-    X((launch_lines<2, 4, 4, 4>), "lines rows=16 rg=32 waves=4 lpb=4", 16) \
-    X((launch_lines<4, 1, 16, 1>), "lines rows=32 rg=8 waves=16 lpb=1", 32) \
-    X((launch_lines<4, 2, 16, 1>), "lines rows=32 rg=16 waves=16 lpb=1", 32) \
-    X((launch_lines<4, 4, 16, 1>), "lines rows=32 rg=32 waves=16 lpb=1", 32) \
-    X((launch_lines<4, 1, 8, 2>), "lines rows=32 rg=8 waves=8 lpb=2", 32) \
-    X((launch_lines<4, 2, 8, 2>), "lines rows=32 rg=16 waves=8 lpb=2", 32) \
-    X((launch_lines<4, 4, 8, 2>), "lines rows=32 rg=32 waves=8 lpb=2", 32) \
-    X((launch_lines<4, 1, 4, 4>), "lines rows=32 rg=8 waves=4 lpb=4", 32) \
-    X((launch_lines<4, 2, 4, 4>), "lines rows=32 rg=16 waves=4 lpb=4", 32)
+    X((launch_cfg<BF, BF, 8, 1, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=16 waves=16 lpb=1", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=32 waves=16 lpb=1", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 8, 2, 16, EPI_NONE>), "lds rows=8 rg=32 waves=8 lpb=2", 8, 0) \
+    X((launch_cfg<BF, BF, 16, 1, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=16 waves=16 lpb=1", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 2, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=32 waves=16 lpb=1", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 2, 8, 2, 16, EPI_NONE>), "lds rows=16 rg=32 waves=8 lpb=2", 16, 0) \
+    X((launch_cfg<BF, BF, 32, 1, 16, 1, 16, EPI_NONE>), "lds rows=32 rg=16 waves=16 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 16, 1, 16, EPI_NONE>), "lds rows=32 rg=32 waves=16 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 8, 2, 16, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=2", 32, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 8, 1, 16, EPI_NONE>), "lds rows=8 rg=32 waves=8 lpb=1", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 3, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=48 waves=16 lpb=1", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 4, 16, 1, 16, EPI_NONE>), "lds rows=8 rg=64 waves=16 lpb=1", 8, 0) \
+    X((launch_cfg<BF, BF, 16, 2, 8, 1, 16, EPI_NONE>), "lds rows=16 rg=32 waves=8 lpb=1", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 3, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=48 waves=16 lpb=1", 16, 0) \
+    X((launch_cfg<BF, BF, 32, 1, 8, 1, 16, EPI_NONE>), "lds rows=32 rg=16 waves=8 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 8, 1, 16, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 8, 4, 16, 1, 16, EPI_NONE, PRO_NONE, 1>), "kn rows=8 cols=64 waves=16 lpb=1", 8, 1) \
+    X((launch_cfg<BF, BF, 8, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>), "kn rows=8 cols=64 waves=8 lpb=1", 8, 1) \
+    X((launch_cfg<BF, BF, 16, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>), "kn rows=16 cols=64 waves=8 lpb=1", 16, 1) \
+    X((launch_cfg<BF, BF, 32, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>), "kn rows=32 cols=64 waves=8 lpb=1", 32, 1) \
+    X((launch_lines<1, 1, 16, 1>), "lines rows=8 rg=8 waves=16 lpb=1", 8, 0) \
+    X((launch_lines<1, 2, 16, 1>), "lines rows=8 rg=16 waves=16 lpb=1", 8, 0) \
+    X((launch_lines<1, 4, 16, 1>), "lines rows=8 rg=32 waves=16 lpb=1", 8, 0) \
+    X((launch_lines<1, 8, 16, 1>), "lines rows=8 rg=64 waves=16 lpb=1", 8, 0) \
+    X((launch_lines<1, 1, 8, 2>), "lines rows=8 rg=8 waves=8 lpb=2", 8, 0) \
+    X((launch_lines<1, 2, 8, 2>), "lines rows=8 rg=16 waves=8 lpb=2", 8, 0) \
+    X((launch_lines<1, 4, 8, 2>), "lines rows=8 rg=32 waves=8 lpb=2", 8, 0) \
+    X((launch_lines<1, 8, 8, 2>), "lines rows=8 rg=64 waves=8 lpb=2", 8, 0) \
+    X((launch_lines<1, 1, 4, 4>), "lines rows=8 rg=8 waves=4 lpb=4", 8, 0) \
+    X((launch_lines<1, 2, 4, 4>), "lines rows=8 rg=16 waves=4 lpb=4", 8, 0) \
+    X((launch_lines<1, 4, 4, 4>), "lines rows=8 rg=32 waves=4 lpb=4", 8, 0) \
+    X((launch_lines<2, 1, 16, 1>), "lines rows=16 rg=8 waves=16 lpb=1", 16, 0) \
+    X((launch_lines<2, 2, 16, 1>), "lines rows=16 rg=16 waves=16 lpb=1", 16, 0) \
+    X((launch_lines<2, 4, 16, 1>), "lines rows=16 rg=32 waves=16 lpb=1", 16, 0) \
+    X((launch_lines<2, 1, 8, 2>), "lines rows=16 rg=8 waves=8 lpb=2", 16, 0) \
+    X((launch_lines<2, 2, 8, 2>), "lines rows=16 rg=16 waves=8 lpb=2", 16, 0) \
+    X((launch_lines<2, 4, 8, 2>), "lines rows=16 rg=32 waves=8 lpb=2", 16, 0) \
+    X((launch_lines<2, 8, 8, 2>), "lines rows=16 rg=64 waves=8 lpb=2", 16, 0) \
+    X((launch_lines<2, 1, 4, 4>), "lines rows=16 rg=8 waves=4 lpb=4", 16, 0) \
+    X((launch_lines<2, 2, 4, 4>), "lines rows=16 rg=16 waves=4 lpb=4", 16, 0) \
+    X((launch_lines<2, 4, 4, 4>), "lines rows=16 rg=32 waves=4 lpb=4", 16, 0) \
+    X((launch_lines<4, 1, 16, 1>), "lines rows=32 rg=8 waves=16 lpb=1", 32, 0) \
+    X((launch_lines<4, 2, 16, 1>), "lines rows=32 rg=16 waves=16 lpb=1", 32, 0) \
+    X((launch_lines<4, 4, 16, 1>), "lines rows=32 rg=32 waves=16 lpb=1", 32, 0) \
+    X((launch_lines<4, 1, 8, 2>), "lines rows=32 rg=8 waves=8 lpb=2", 32, 0) \
+    X((launch_lines<4, 2, 8, 2>), "lines rows=32 rg=16 waves=8 lpb=2", 32, 0) \
+    X((launch_lines<4, 4, 8, 2>), "lines rows=32 rg=32 waves=8 lpb=2", 32, 0) \
+    X((launch_lines<4, 1, 4, 4>), "lines rows=32 rg=8 waves=4 lpb=4", 32, 0) \
+    X((launch_lines<4, 2, 4, 4>), "lines rows=32 rg=16 waves=4 lpb=4", 32, 0)
 
-#define X(fn, name, rows) {fn, name, rows},
+#define X(fn, name, rows, kn) {fn, name, rows, kn},
 const SweepConfig kConfigs[] = {DECODE_SWEEP_CONFIGS(X)};
 #undef X
 constexpr int kCount = int(sizeof(kConfigs) / sizeof(kConfigs[0]));
@@ -236,13 +243,19 @@ const char* nvsweep_decode_name(int cfg) { return cfg >= 0 && cfg < nvg::kCount 
 
 int nvsweep_decode_max_m(int cfg) { return cfg >= 0 && cfg < nvg::kCount ? nvg::kConfigs[cfg].max_m : 0; }
 
-// C[M,N] = A[M,K] W[N,K]^T in bf16 on configuration `cfg`; -1 for a bad
-// configuration or sizes it cannot run (M above its rows, K not a multiple
-// of 8, null pointers).
+// 1 when configuration `cfg` takes B[K,N] (ldb = N), 0 for W[N,K], -1 for a bad index.
+int nvsweep_decode_kn(int cfg) { return cfg >= 0 && cfg < nvg::kCount ? nvg::kConfigs[cfg].kn : -1; }
+
+// C[M,N] = A[M,K] W[N,K]^T (or A B with B[K,N] for a B[K,N] configuration)
+// in bf16 on configuration `cfg`; -1 for a bad configuration or sizes it
+// cannot run (M above its rows, K not a multiple of 8, N not a multiple of
+// 8 on B[K,N], null pointers).
 int nvsweep_decode(int cfg, const void* a, const void* w, void* c, int64_t m, int64_t n, int64_t k, void* stream) {
     if (cfg < 0 || cfg >= nvg::kCount) return -1;
     if (a == nullptr || w == nullptr || c == nullptr) return -1;
     if (m < 1 || m > nvg::kConfigs[cfg].max_m || n < 1 || k < 8 || k % 8 != 0) return -1;
+    const bool kn = nvg::kConfigs[cfg].kn != 0;
+    if (kn && (n < 8 || n % 8 != 0)) return -1;
     nvg::Problem p{};
     p.a = a;
     p.b = w;
@@ -251,9 +264,9 @@ int nvsweep_decode(int cfg, const void* a, const void* w, void* c, int64_t m, in
     p.n = n;
     p.k = k;
     p.lda = k;
-    p.ldb = k;
+    p.ldb = kn ? n : k;
     p.ldc = n;
-    p.b_layout = NANOVLLM_GEMM_B_NK;
+    p.b_layout = kn ? NANOVLLM_GEMM_B_KN : NANOVLLM_GEMM_B_NK;
     p.dtype_in = NANOVLLM_GEMM_BF16;
     p.dtype_out = NANOVLLM_GEMM_BF16;
     return nvg::kConfigs[cfg].launch(p, static_cast<hipStream_t>(stream)) == NANOVLLM_GEMM_OK ? 0 : -1;

@@ -226,6 +226,8 @@ def load_sweep():
         lib.nvsweep_decode_name.argtypes = [_INT]
         lib.nvsweep_decode_max_m.restype = _INT
         lib.nvsweep_decode_max_m.argtypes = [_INT]
+        lib.nvsweep_decode_kn.restype = _INT
+        lib.nvsweep_decode_kn.argtypes = [_INT]
         lib.nvsweep_decode.restype = _INT
         lib.nvsweep_decode.argtypes = [_INT, _VP, _VP, _VP, _I64, _I64, _I64, _VP]
         _sweep = lib
@@ -233,17 +235,18 @@ def load_sweep():
 
 
 def sweep_configs():
-    """(index, name, max M) of every decode configuration in the sweep library."""
+    """(index, name, max M, B[K,N]?) of every decode configuration in the sweep library."""
     lib = load_sweep()
-    return [(i, lib.nvsweep_decode_name(i).decode(), lib.nvsweep_decode_max_m(i))
+    return [(i, lib.nvsweep_decode_name(i).decode(), lib.nvsweep_decode_max_m(i), lib.nvsweep_decode_kn(i) == 1)
             for i in range(lib.nvsweep_decode_count())]
 
 
 def sweep_launcher(torch, cfg, a, w, c):
-    """A no-argument launch of configuration `cfg` on bf16 a[M,K], w[N,K] into c[M,N]."""
+    """A no-argument launch of configuration `cfg` on bf16 a[M,K] and w (W[N,K],
+    or B[K,N] for a B[K,N] configuration) into c[M,N]."""
     lib = load_sweep()
     m, k = a.shape
-    n = w.shape[0]
+    n = c.shape[1]
     args = (cfg, a.data_ptr(), w.data_ptr(), c.data_ptr(), m, n, k)
 
     def f():

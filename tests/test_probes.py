@@ -47,17 +47,21 @@ def test_decode_sweep_library_lists_and_refuses():
     anything is launched."""
     cfgs = P.sweep_configs()
     assert len(cfgs) >= 10
-    names = [name for _, name, _ in cfgs]
+    names = [name for _, name, _, _ in cfgs]
     assert len(set(names)) == len(names)
-    assert all(name.split()[0] in ("lds", "lines") for name in names)
-    assert {rows for _, _, rows in cfgs} == {8, 16, 32}
+    assert all(name.split()[0] in ("lds", "lines", "kn") for name in names)
+    assert all(kn == (name.split()[0] == "kn") for _, name, _, kn in cfgs)
+    assert {rows for _, _, rows, _ in cfgs} == {8, 16, 32}
     lib = P.load_sweep()
     fake = 1 << 20   # never dereferenced: every call below is refused first
     assert lib.nvsweep_decode(-1, fake, fake, fake, 1, 64, 64, None) == -1
     assert lib.nvsweep_decode(len(cfgs), fake, fake, fake, 1, 64, 64, None) == -1
     assert lib.nvsweep_decode(0, None, fake, fake, 1, 64, 64, None) == -1
-    idx8 = next(i for i, _, rows in cfgs if rows == 8)
+    idx8 = next(i for i, _, rows, kn in cfgs if rows == 8 and not kn)
+    idx_kn = next(i for i, _, rows, kn in cfgs if rows == 8 and kn)
+    assert lib.nvsweep_decode(idx_kn, fake, fake, fake, 1, 60, 64, None) == -1   # N not a multiple of 8
     assert lib.nvsweep_decode(idx8, fake, fake, fake, 9, 64, 64, None) == -1
     assert lib.nvsweep_decode(idx8, fake, fake, fake, 1, 64, 60, None) == -1
     assert lib.nvsweep_decode(idx8, fake, fake, fake, 0, 64, 64, None) == -1
     assert lib.nvsweep_decode_name(len(cfgs)) == b""
+    assert lib.nvsweep_decode_kn(len(cfgs)) == -1
