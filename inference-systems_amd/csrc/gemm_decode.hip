@@ -80,6 +80,9 @@ constexpr int64_t kDecodeCus = 256;
 
 // Workgroups of a configuration resident on one CU at once (LDS, waves and
 // registers), from the runtime's occupancy query, once per configuration.
+// The query enqueues nothing (it may run under graph capture); should it
+// fail, one workgroup per CU is assumed and the error is cleared so the
+// launch that follows does not report it.
 template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int EPI, int PRO>
 int64_t resident_per_cu() {
     static const int64_t per_cu = [] {
@@ -87,6 +90,7 @@ int64_t resident_per_cu() {
         const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &blocks, reinterpret_cast<const void*>(&splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, 1, 16, EPI, PRO>),
             WAVES * 64, 0);
+        if (e != hipSuccess) (void)hipGetLastError();
         return int64_t(e == hipSuccess && blocks > 0 ? blocks : 1);
     }();
     return per_cu;

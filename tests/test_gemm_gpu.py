@@ -483,6 +483,33 @@ def test_graph_capture_replay(m):
         assert torch.equal(out_static, eager), f"replay {step} differs"
 
 
+def test_graph_capture_first_call_wide_w():
+    """A wide-W splitk_decode configuration whose first call is inside graph
+    capture (bf16 -> fp32, M = 12, 12000 rows: the configuration is chosen
+    with the runtime's occupancy query, which enqueues nothing): the
+    captured launch equals eager on every replay."""
+    gen = torch.Generator().manual_seed(12)
+    m, n, k = 12, 12000, 512
+    a_static = torch.randn(m, k, generator=gen).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=gen) * 0.05).bfloat16().to(DEV)
+    _say(f"graph capture, first call M={m} N={n} K={k} bf16->f32")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph):
+            out_static = G.gemm(a_static, w, torch.float32)
+    torch.cuda.current_stream().wait_stream(side)
+    for step in range(3):
+        new_a = torch.randn(m, k, generator=gen).bfloat16().to(DEV)
+        a_static.copy_(new_a)
+        graph.replay()
+        eager = G.gemm(new_a, w, torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(out_static, eager), f"replay {step} differs"
+
+
 def test_torch_compile_fullgraph():
     gen = torch.Generator().manual_seed(12)
     a = torch.randn(40, 256, generator=gen).bfloat16().to(DEV)
