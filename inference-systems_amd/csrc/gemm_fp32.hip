@@ -4,14 +4,16 @@
 //                 reference ladder: cuda_kernels/gemm/src/gemm.cu:7-15,
 //                 gemm_tiled.cu:36-51).
 //   fp32_tiled  — 64x64 output tile per 512-thread workgroup, K-tiles of 64
-//                 staged in LDS (double buffered, one barrier per K-tile,
-//                 fragments read with ds_read_b128 in a K-permuted order),
-//                 products on the fp32 matrix cores with
-//                 v_mfma_f32_32x32x2_f32 (full fp32 precision; gfx950 has no
-//                 reduced-precision fp32 MFMA).  Replaces the shared-memory and
-//                 register-tiled rungs (gemm_tiled.cu:56-202), including their
-//                 zero-filled edge tiles, so any M, N, K and either B layout
-//                 runs.
+//                 staged in LDS (one barrier per K-tile), products on the
+//                 fp32 matrix cores with v_mfma_f32_32x32x2_f32 (full fp32
+//                 precision; gfx950 has no reduced-precision fp32 MFMA).
+//                 Replaces the shared-memory and register-tiled rungs
+//                 (gemm_tiled.cu:56-202), including their zero-filled edge
+//                 tiles, so any M, N, K and either B layout runs.  Problems
+//                 whose rows are whole 16-byte chunks take fp32_staged_kernel
+//                 (copies straight into a 3-deep LDS ring); the rest take
+//                 fp32_tiled_kernel (scalar loads staged through registers
+//                 into a double-buffered LDS tile).
 #include <type_traits>
 
 #include "gemm_common.hpp"
@@ -54,13 +56,10 @@ constexpr int kT32BK = 64;
 constexpr int kT32Pitch = kT32BK + 4;   // 68 floats: 16-lane ds_read_b128 groups hit 64 distinct banks
 constexpr int kT32Cpr = kT32BK / 4;     // 16-byte chunks per row of an A / W tile
 constexpr int kT32Threads = 512;        // 8 waves: two groups of 4 (2 x 2 over the tile)
-constexpr int kT32VecLoads = kT32BM * kT32Cpr / kT32Threads;     // 16-byte loads per operand per thread
 constexpr int kT32ScalarLoads = kT32BM * kT32BK / kT32Threads;   // 4-byte loads per operand per thread
 static_assert(kT32BM == 64 && kT32BN == 64, "B[K,N] tiles are read as rows of 64 floats");
-static_assert(kT32VecLoads == 2 && kT32Threads == 512, "B[K,N]: one 2 x 4 block of the 64 x 64 tile per thread");
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-template <int BL, int VEC>
+template <int BL>
 __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
@@ -71,10 +70,8 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     // k = 16 (l/32) + s, so lane l needs 16 consecutive k of one row of each
     // tile and reads them with four ds_read_b128.
     //
-    // Loads are staged through two register sets, two K-tiles ahead of the
-    // multiply (see `step` below).  VEC: 16-byte loads (2 per operand per
-    // thread; needs 16-byte aligned rows), else 8 scalar loads per operand
-    // per thread.
+    // Loads (8 scalar loads per operand per thread) are staged through two
+    // register sets, two K-tiles ahead of the multiply (see `step` below).
     __shared__ __attribute__((aligned(16))) float As[2][kT32BM][kT32Pitch];
     __shared__ __attribute__((aligned(16))) float Bs[2][kT32BN][kT32Pitch];
 
@@ -96,8 +93,7 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     const int64_t n0 = int64_t(tn) * kT32BN;
 
     // Two register sets of staged loads, used by even and odd K-tiles.
-    f32x4_t va[2][VEC ? kT32VecLoads : 1], vb[2][VEC ? kT32VecLoads : 1];
-    float ra[2][VEC ? 1 : kT32ScalarLoads], rb[2][VEC ? 1 : kT32ScalarLoads];
+    float ra[2][kT32ScalarLoads], rb[2][kT32ScalarLoads];
 
     // Every load is issued unconditionally from an address clamped into the
     // matrix; values outside the matrix are zeroed only when the tile is
@@ -107,71 +103,29 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     // wait for it at once).
     auto load_tile = [&](int64_t k0, auto set_c) {
         constexpr int S = decltype(set_c)::value;
-        if constexpr (VEC) {
 #pragma unroll
-            for (int r = 0; r < kT32VecLoads; ++r) {
-                const int e = tid + kT32Threads * r;     // 16-byte chunks of the operand tile
-                const int64_t gm = m0 + e / kT32Cpr, gka = k0 + 4 * (e % kT32Cpr);   // A: chunks of 4 k per row
-                va[S][r] = *reinterpret_cast<const f32x4_t*>(a + min_i64(gm, m - 1) * lda + min_i64(gka, k - 4));
-                if constexpr (BL == NANOVLLM_GEMM_B_NK) {
-                    const int64_t gn = n0 + e / kT32Cpr, gk = k0 + 4 * (e % kT32Cpr);
-                    vb[S][r] = *reinterpret_cast<const f32x4_t*>(b + min_i64(gn, n - 1) * ldb + min_i64(gk, k - 4));
-                } else {
-                    // B[K,N]: thread t takes 4 columns (t % 16) of rows 2 (t / 16) and 2 (t / 16) + 1.
-                    const int64_t gn = n0 + 4 * (tid & 15), gk = k0 + 2 * (tid >> 4) + r;
-                    vb[S][r] = *reinterpret_cast<const f32x4_t*>(b + min_i64(gk, k - 1) * ldb + min_i64(gn, n - 4));
-                }
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < kT32ScalarLoads; ++r) {
-                const int e = tid + kT32Threads * r;
-                ra[S][r] = a[min_i64(m0 + e / kT32BK, m - 1) * lda + min_i64(k0 + e % kT32BK, k - 1)];
-                if constexpr (BL == NANOVLLM_GEMM_B_NK)
-                    rb[S][r] = b[min_i64(n0 + e / kT32BK, n - 1) * ldb + min_i64(k0 + e % kT32BK, k - 1)];
-                else
-                    rb[S][r] = b[min_i64(k0 + (e >> 6), k - 1) * ldb + min_i64(n0 + (e & 63), n - 1)];
-            }
+        for (int r = 0; r < kT32ScalarLoads; ++r) {
+            const int e = tid + kT32Threads * r;
+            ra[S][r] = a[min_i64(m0 + e / kT32BK, m - 1) * lda + min_i64(k0 + e % kT32BK, k - 1)];
+            if constexpr (BL == NANOVLLM_GEMM_B_NK)
+                rb[S][r] = b[min_i64(n0 + e / kT32BK, n - 1) * ldb + min_i64(k0 + e % kT32BK, k - 1)];
+            else
+                rb[S][r] = b[min_i64(k0 + (e >> 6), k - 1) * ldb + min_i64(n0 + (e & 63), n - 1)];
         }
     };
     // Writes the K-tile starting at k0 (staged in register set S) to LDS
     // buffer `buf`, zeroing elements outside the matrix.
     auto store_tile = [&](int buf, int64_t k0, auto set_c) {
         constexpr int S = decltype(set_c)::value;
-        const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (VEC) {
 #pragma unroll
-            for (int r = 0; r < kT32VecLoads; ++r) {
-                const int e = tid + kT32Threads * r;
-                const int row = e / kT32Cpr, kq = e % kT32Cpr;
-                const bool in_a = m0 + row < m && k0 + 4 * kq < k;
-                *reinterpret_cast<f32x4_t*>(&As[buf][row][4 * kq]) = in_a ? va[S][r] : z4;
-                if constexpr (BL == NANOVLLM_GEMM_B_NK) {
-                    const bool in_b = n0 + row < n && k0 + 4 * kq < k;
-                    *reinterpret_cast<f32x4_t*>(&Bs[buf][row][4 * kq]) = in_b ? vb[S][r] : z4;
-                } else if (r == 1) {
-                    // The thread's 2 x 4 block of B[K,N], transposed into 4
-                    // pairs of consecutive k (one 8-byte write each).
-                    const int nq = tid & 15, kp = tid >> 4;
-                    const bool in_n = n0 + 4 * nq < n;
-                    const bool in0 = in_n && k0 + 2 * kp < k, in1 = in_n && k0 + 2 * kp + 1 < k;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        *reinterpret_cast<f32x2_t*>(&Bs[buf][4 * nq + q][2 * kp]) =
-                            f32x2_t{in0 ? vb[S][0][q] : 0.0f, in1 ? vb[S][1][q] : 0.0f};
-                }
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < kT32ScalarLoads; ++r) {
-                const int e = tid + kT32Threads * r;
-                const int row = e / kT32BK, kk = e % kT32BK;
-                As[buf][row][kk] = (m0 + row < m && k0 + kk < k) ? ra[S][r] : 0.0f;
-                if constexpr (BL == NANOVLLM_GEMM_B_NK)
-                    Bs[buf][row][kk] = (n0 + row < n && k0 + kk < k) ? rb[S][r] : 0.0f;
-                else
-                    Bs[buf][e & 63][e >> 6] = (n0 + (e & 63) < n && k0 + (e >> 6) < k) ? rb[S][r] : 0.0f;
-            }
+        for (int r = 0; r < kT32ScalarLoads; ++r) {
+            const int e = tid + kT32Threads * r;
+            const int row = e / kT32BK, kk = e % kT32BK;
+            As[buf][row][kk] = (m0 + row < m && k0 + kk < k) ? ra[S][r] : 0.0f;
+            if constexpr (BL == NANOVLLM_GEMM_B_NK)
+                Bs[buf][row][kk] = (n0 + row < n && k0 + kk < k) ? rb[S][r] : 0.0f;
+            else
+                Bs[buf][e & 63][e >> 6] = (n0 + (e & 63) < n && k0 + (e >> 6) < k) ? rb[S][r] : 0.0f;
         }
     };
 
@@ -247,6 +201,216 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     }
 }
 
+// fp32_staged: the fp32_tiled rung for problems whose rows are whole 16-byte
+// chunks (16-byte aligned bases and leading dimensions, K % 4 == 0, and N %
+// 4 == 0 for B[K,N]).  Same 64 x 64 tile, same two K-groups of four waves
+// and the same MFMA, but the operands move global -> LDS with
+// global_load_lds_dwordx4 into a 3-deep ring, with no register staging and
+// no LDS writes from the waves, and the copies of K-tile t + 2 are spread
+// between the MFMAs of K-tile t.  Each wave reads its fragments a quarter
+// K-tile ahead of its MFMAs and waits for the next K-tile before its last
+// quarter, so the matrix cores stay busy across the one barrier per K-tile.
+//
+// LDS stage (32 KiB): the A tile (64 rows x 16 chunks of 4 k), then the B
+// tile: W[N,K] rows like A; B[K,N] as 64 k-rows x 16 chunks of 4 columns,
+// copied as they lie in memory and read back one float per lane.
+//   A / W: chunk c of row r at position c ^ (r % 16): a ds_read_b128 of 16
+//     consecutive rows at one chunk then touches 16 distinct positions, all
+//     64 banks.
+//   B[K,N]: chunk c of k-row r at position c ^ (8 ((r / 16) % 2)): the b32
+//     read of one MFMA step takes 32 columns of k-rows r and r + 16, which
+//     then sit in opposite halves of the banks.
+constexpr int kF32StageChunks = 2 * kT32BM * kT32Cpr;   // 2048 16-byte chunks
+constexpr int kF32Ipw = kF32StageChunks / (64 * (kT32Threads / 64));   // copies per wave per K-tile
+static_assert(kF32Ipw == 4, "32 KiB per stage over 8 waves");
+constexpr int kF32Stages = 3;   // ring depth (4 stages measured the same at 1024^3 and 2048^3)
+
+// Source of the K-tail chunks: 16 zero bytes in global memory.
+__device__ u32x4_t g_f32_zero = {0u, 0u, 0u, 0u};
+
+template <int BL, int STAGES>
+__global__ __launch_bounds__(kT32Threads) void fp32_staged_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c,
+    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n) {
+    constexpr int AHEAD = STAGES - 1;   // K-tiles in flight beyond the one multiplied
+    static_assert(AHEAD >= 2 && AHEAD <= 3, "ring depth");
+    __shared__ u32x4_t ring[STAGES * kF32StageChunks];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;
+    const int wm = (wave >> 1) & 1;
+    const int wn = wave & 1;
+    const int half = lane >> 5;
+    const int r32 = lane & 31;
+
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
+    const int64_t m0 = int64_t(tm) * kT32BM;
+    const int64_t n0 = int64_t(tn) * kT32BN;
+
+    // Copy instruction j of this wave fills stage chunks 64 i .. 64 i + 63,
+    // i = 4 wave + j: i < 16 rows 4 i .. 4 i + 3 of A, else rows (k-rows for
+    // B[K,N]) 4 (i - 16) .. of B.  Lane L takes row 4 i' + L / 16, position
+    // L % 16.  kpos[j]: the k (element of a row, or k-row of B[K,N]) its
+    // chunk starts at within the K-tile.
+    const float* src[kF32Ipw];
+    int kpos[kF32Ipw];
+    const int rin = lane >> 4, pos = lane & 15;
+#pragma unroll
+    for (int j = 0; j < kF32Ipw; ++j) {
+        const int i = wave * kF32Ipw + j;
+        if (i < 16) {
+            const int row = 4 * i + rin;
+            const int lc = pos ^ (row & 15);
+            src[j] = a + min_i64(m0 + row, m - 1) * lda + 4 * lc;
+            kpos[j] = 4 * lc;
+        } else if constexpr (BL == NANOVLLM_GEMM_B_NK) {
+            const int row = 4 * (i - 16) + rin;
+            const int lc = pos ^ (row & 15);
+            src[j] = b + min_i64(n0 + row, n - 1) * ldb + 4 * lc;
+            kpos[j] = 4 * lc;
+        } else {
+            const int kr = 4 * (i - 16) + rin;
+            const int lc = pos ^ (8 * ((kr >> 4) & 1));
+            src[j] = b + int64_t(kr) * ldb + min_i64(n0 + 4 * lc, n - 4);
+            kpos[j] = kr;
+        }
+    }
+    const void* zero = &g_f32_zero;
+    asm volatile("" : "+s"(zero));
+    const int ktiles = static_cast<int>((k + kT32BK - 1) / kT32BK);
+    const uint32_t ring_lds = lds_address(ring);
+    auto issue_one = [&](int t, int stage, int j) {
+        const int64_t k0 = int64_t(t) * kT32BK;
+        const bool kn_row = BL == NANOVLLM_GEMM_B_KN && wave * kF32Ipw + j >= 16;
+        const void* s = k0 + kpos[j] < k ? static_cast<const void*>(src[j] + (kn_row ? k0 * ldb : k0)) : zero;
+        dma16(s, ring_lds + uint32_t(stage * kF32StageChunks + 64 * (wave * kF32Ipw + j)) * 16u);
+    };
+    auto issue = [&](int t, int stage) {
+#pragma unroll
+        for (int j = 0; j < kF32Ipw; ++j) issue_one(t, stage, j);
+    };
+
+    // Lane l takes k = 32 grp + 16 half + s of the K-tile in MFMA step s
+    // (0..15); quarter q holds steps 4 q .. 4 q + 3, one 16-byte chunk of an
+    // A (or W) row.
+    const int ai = wm * 32 + r32;
+    const int bj = wn * 32 + r32;
+    struct Frag {
+        f32x4_t a, b;
+    };
+    auto read_frag = [&](const u32x4_t* tile, int q) -> Frag {
+        const int lc = 8 * grp + 4 * half + q;
+        Frag f;
+        f.a = __builtin_bit_cast(f32x4_t, tile[ai * kT32Cpr + (lc ^ (ai & 15))]);
+        if constexpr (BL == NANOVLLM_GEMM_B_NK) {
+            f.b = __builtin_bit_cast(f32x4_t, tile[kT32BM * kT32Cpr + bj * kT32Cpr + (lc ^ (bj & 15))]);
+        } else {
+            const float* bt = reinterpret_cast<const float*>(tile + kT32BM * kT32Cpr);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int kr = 4 * lc + s;
+                f.b[s] = bt[(kr * kT32Cpr + ((bj >> 2) ^ (8 * ((kr >> 4) & 1)))) * 4 + (bj & 3)];
+            }
+        }
+        return f;
+    };
+    f32x16_t acc = {};
+    auto mfma4 = [&](const Frag& f) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[s], f.b[s], acc, 0, 0, 0);
+    };
+    // The 4 MFMAs of a quarter with copies J0 .. J0 + CNT - 1 of tile tt
+    // after its first CNT MFMAs.
+    auto mfma4_copy = [&](const Frag& f, int tt, int stage, int j0, int cnt) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[s], f.b[s], acc, 0, 0, 0);
+            if (s < cnt) {
+                __builtin_amdgcn_sched_barrier(0);
+                issue_one(tt, stage, j0 + s);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    // Tile u has landed in this wave's part of its stage once at most
+    // `later` tiles issued after it are still in flight.
+    auto wait_tiles_after = [&](int later) {
+        if (AHEAD >= 3 && later >= 2) wait_vmcnt<2 * kF32Ipw>();
+        else if (later >= 1) wait_vmcnt<kF32Ipw>();
+        else wait_vmcnt<0>();
+    };
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u)
+        if (u < ktiles) issue(u, u);
+    wait_tiles_after((ktiles < AHEAD ? ktiles : AHEAD) - 1);
+    lds_barrier();
+    Frag f0 = read_frag(ring, 0), f1;
+    int cur = 0;
+    // K-tile t: quarters 0-2 carry copies 2 / 1 / 1 of tile t + AHEAD into
+    // the stage tile t - 1 used (free since the barrier that opened tile t);
+    // the MFMAs run at raised wave priority, dropped before the wait for
+    // tile t + 1.  COPY (whether tile t + AHEAD exists) is a compile-time
+    // choice, and the tiles with and without copies run in two loops: a
+    // branch between the two forms inside one loop body gives the
+    // accumulator different registers on each path, and the copies that
+    // join them wait for the MFMA chain.
+    auto k_tile = [&](int t, auto copy_c) {
+        constexpr bool COPY = decltype(copy_c)::value;
+        const u32x4_t* tile = ring + cur * kF32StageChunks;
+        const int refill = cur == 0 ? STAGES - 1 : cur - 1;
+        const int next = cur + 1 == STAGES ? 0 : cur + 1;
+        __builtin_amdgcn_s_setprio(3);
+        f1 = read_frag(tile, 1);
+        if constexpr (COPY) mfma4_copy(f0, t + AHEAD, refill, 0, 2);
+        else mfma4(f0);
+        f0 = read_frag(tile, 2);
+        if constexpr (COPY) mfma4_copy(f1, t + AHEAD, refill, 2, 1);
+        else mfma4(f1);
+        f1 = read_frag(tile, 3);
+        if constexpr (COPY) mfma4_copy(f0, t + AHEAD, refill, 3, 1);
+        else mfma4(f0);
+        __builtin_amdgcn_s_setprio(0);
+        if (t + 1 < ktiles) {
+            if constexpr (COPY) {
+                if constexpr (AHEAD >= 3) wait_vmcnt<2 * kF32Ipw>();
+                else wait_vmcnt<kF32Ipw>();
+            } else {
+                wait_tiles_after(ktiles - 2 - t);
+            }
+            lds_barrier();
+            f0 = read_frag(ring + next * kF32StageChunks, 0);
+        }
+        cur = next;
+        mfma4(f1);
+    };
+    int t = 0;
+    for (; t + AHEAD < ktiles; ++t) k_tile(t, std::true_type{});
+    for (; t < ktiles; ++t) k_tile(t, std::false_type{});
+
+    // Group 1's partial tile to group 0 through LDS, once every wave is done
+    // reading the last K-tile.
+    lds_barrier();
+    float* xch = reinterpret_cast<float*>(ring);
+    if (grp == 1) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) xch[((wave & 3) * 16 + v) * 64 + lane] = acc[v];
+    }
+    lds_barrier();
+    if (grp == 1) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] += xch[((wave & 3) * 16 + v) * 64 + lane];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int64_t row = m0 + wm * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        const int64_t col = n0 + bj;
+        if (row < m && col < n) __builtin_nontemporal_store(acc[v], c + row * ldc + col);
+    }
+}
+
 }  // namespace
 
 int launch_fp32_naive(const Problem& p, hipStream_t s) {
@@ -272,25 +436,26 @@ int launch_fp32_tiled(const Problem& p, hipStream_t s) {
     const float* a = static_cast<const float*>(p.a);
     const float* b = static_cast<const float*>(p.b);
     float* c = static_cast<float*>(p.c);
-    // 16-byte loads need aligned bases and leading dims (and, for A and W,
-    // K-chunks of 4 that do not straddle K: K % 4 == 0; for B[K,N], N % 4).
+    // The 16-byte copies of fp32_staged need aligned bases and leading dims
+    // and chunks of 4 that do not straddle a row end: K % 4 == 0 (A and
+    // W[N,K] rows), N % 4 == 0 (B[K,N] rows).
     const bool aligned = reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 &&
                          p.lda % 4 == 0 && p.ldb % 4 == 0 && p.k % 4 == 0;
-    const bool vec = aligned && (p.b_layout == NANOVLLM_GEMM_B_NK || p.n % 4 == 0);
+    const bool staged = aligned && (p.b_layout == NANOVLLM_GEMM_B_NK || p.n % 4 == 0);
     const int ti = int(tiles_m), tj = int(tiles_n);
     if (p.b_layout == NANOVLLM_GEMM_B_NK) {
-        if (vec)
-            hipLaunchKernelGGL((fp32_tiled_kernel<NANOVLLM_GEMM_B_NK, 1>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
+        if (staged)
+            hipLaunchKernelGGL((fp32_staged_kernel<NANOVLLM_GEMM_B_NK, kF32Stages>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
                                p.lda, p.ldb, p.ldc, ti, tj);
         else
-            hipLaunchKernelGGL((fp32_tiled_kernel<NANOVLLM_GEMM_B_NK, 0>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
+            hipLaunchKernelGGL(fp32_tiled_kernel<NANOVLLM_GEMM_B_NK>, grid, block, 0, s, a, b, c, p.m, p.n, p.k,
                                p.lda, p.ldb, p.ldc, ti, tj);
     } else {
-        if (vec)
-            hipLaunchKernelGGL((fp32_tiled_kernel<NANOVLLM_GEMM_B_KN, 1>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
+        if (staged)
+            hipLaunchKernelGGL((fp32_staged_kernel<NANOVLLM_GEMM_B_KN, kF32Stages>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
                                p.lda, p.ldb, p.ldc, ti, tj);
         else
-            hipLaunchKernelGGL((fp32_tiled_kernel<NANOVLLM_GEMM_B_KN, 0>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
+            hipLaunchKernelGGL(fp32_tiled_kernel<NANOVLLM_GEMM_B_KN>, grid, block, 0, s, a, b, c, p.m, p.n, p.k,
                                p.lda, p.ldb, p.ldc, ti, tj);
     }
     return check_launch("fp32_tiled");

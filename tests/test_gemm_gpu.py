@@ -163,6 +163,30 @@ def test_fp32_reference_known_answer(kernel, layout):
     assert orc.rel_frobenius(out.cpu().numpy(), ref) <= 1e-5
 
 
+FP32_STAGED_SHAPES = [(1, 4, 4), (3, 8, 60), (64, 64, 64), (65, 68, 68), (130, 196, 132), (127, 192, 260),
+                      (200, 256, 1028), (257, 132, 192)]
+
+
+@pytest.mark.parametrize("layout", [L.B_KN, L.B_NK], ids=["kn", "nk"])
+def test_fp32_staged_ragged(layout):
+    """fp32_tiled on 16-byte rows (K % 4 == 0, N % 4 == 0 for B[K,N]): the
+    copy-into-LDS form, on edge tiles in M and N and K tails that are not a
+    multiple of the 64-wide K-tile; check_result against the float64 product
+    and relative Frobenius <= 1e-5."""
+    gen = torch.Generator().manual_seed(21)
+    for m, n, k in FP32_STAGED_SHAPES:
+        _say(f"fp32 staged {LAYOUT[layout]} M={m} N={n} K={k}")
+        a = torch.rand((m, k), generator=gen) * 2 - 1
+        b = torch.rand((n, k) if layout == L.B_NK else (k, n), generator=gen) * 2 - 1
+        out = G.gemm_with_kernel(a.to(DEV), b.to(DEV), L.KERNEL_FP32_TILED, torch.float32, layout)
+        torch.cuda.synchronize()
+        ref = (a.double() @ (b.double().T if layout == L.B_NK else b.double())).numpy()
+        got = out.cpu().numpy()
+        chk = orc.check_result(got, ref.astype(np.float32))
+        assert chk["correct"], (m, n, k, chk)
+        assert orc.rel_frobenius(got, ref) <= 1e-5, (m, n, k)
+
+
 # ---------------------------------------------------------------------------
 # Known-answer inputs: bit-exact on every kernel that takes the shape
 # ---------------------------------------------------------------------------
