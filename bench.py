@@ -33,6 +33,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 from pathlib import Path
 
@@ -74,6 +75,10 @@ def parse_args():
     p.add_argument("--matrix", action="store_true",
                    help="only run the reference's shape matrix (fp16 and bf16 over its Qwen3.5 shapes) and print "
                         "it as CSV")
+    p.add_argument("--vendor-tuned", action="store_true",
+                   help="only time torch's GPU GEMM with every hipBLASLt / rocBLAS solution searched (TunableOp) "
+                        "beside its default choice and the selected kernel here, on the workloads that fit one "
+                        "torch call, and print them as one JSON line")
     return p.parse_args()
 
 
@@ -233,6 +238,88 @@ def run_probes(torch) -> int:
     out["stream_read_lm_head_w"] = P.stream_read(torch, head_w, 2, per_lane_list=(1, 4), reps_per_copy=2)
     log(f"stream read 311 MB: {out['stream_read_lm_head_w']}")
     print(json.dumps(out), flush=True)
+    return 0
+
+
+# Workloads with a single-call torch equivalent of the same output dtype:
+# F.linear for W[N,K], torch.matmul for B[K,N] (the fp32-logit LM head has
+# none: F.linear returns bf16).  Every input stays resident, ours included.
+VENDOR_TUNED_CASES = (("bf16_prefill_2048x4096x1024", 2048), ("fp16_down_4096x1024x3584", 4096),
+                      ("fp32_square_1024", 1024), ("bf16_decode_n6144_k1024", 1), ("bf16_decode_n6144_k1024", 8),
+                      ("bf16_decode_n6144_k1024", 32))
+VENDOR_TUNING_MS = 5          # TunableOp: time budget per candidate solution
+VENDOR_TUNING_ITERATIONS = 20
+
+
+def run_vendor_tuned(torch, L, W) -> int:
+    """torch's GPU GEMM on each workload of VENDOR_TUNED_CASES with its
+    default hipBLASLt / rocBLAS choice, then with the fastest solution
+    TunableOp finds among all of them, beside the kernel selected here; each
+    timed as 200 graph-replayed launches after a clock ramp."""
+    import tempfile
+
+    F = torch.nn.functional
+    dev = torch.device("cuda:0")
+    code = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16}
+    cases = []
+    for name, m in VENDOR_TUNED_CASES:
+        wl = W.WORKLOADS[name]
+        a, b = W.make_inputs(name, m, device=dev)
+        c = torch.empty((m, wl.n), dtype=wl.dtype_out, device=dev)
+        ldb = wl.k if wl.b_layout == L.B_NK else wl.n
+        raw = (a.data_ptr(), b.data_ptr(), c.data_ptr(), m, wl.n, wl.k, wl.k, ldb, wl.n, wl.b_layout,
+               code[wl.dtype_in], code[wl.dtype_out])
+
+        def ours(raw=raw):
+            L.gemm_raw(*raw, torch.cuda.current_stream().cuda_stream)
+
+        def vendor(a=a, b=b, nk=wl.b_layout == L.B_NK):
+            if nk:
+                F.linear(a, b)
+            else:
+                torch.matmul(a, b)
+        cases.append((name, m, wl, ours, vendor))
+
+    rows = []
+    for name, m, wl, ours, vendor in cases:
+        rows.append({"workload": name, "m": m, "n": wl.n, "k": wl.k, "flops": W.problem_flops(m, wl.n, wl.k),
+                     "ours_us": median_graph_ms(torch, [ours] * 200) * 1e3,
+                     "torch_default_us": median_graph_ms(torch, [vendor] * 200) * 1e3})
+    T = torch.cuda.tunable
+    results = Path(tempfile.mkdtemp()) / "tunableop_results.csv"
+    T.set_filename(str(results))
+    T.set_max_tuning_duration(VENDOR_TUNING_MS)
+    T.set_max_tuning_iterations(VENDOR_TUNING_ITERATIONS)
+    T.enable(True)
+    T.tuning_enable(True)
+    for (name, m, wl, ours, vendor), row in zip(cases, rows):
+        vendor()                 # the search runs on the first call of a shape, outside any graph
+        torch.cuda.synchronize()
+        row["torch_tuned_us"] = median_graph_ms(torch, [vendor] * 200) * 1e3
+    tuned = [list(r) for r in T.get_results()]
+    T.tuning_enable(False)
+    T.enable(False)
+    for row in rows:
+        # The entry whose parameter signature carries this GEMM's three sizes
+        # (in TunableOp's m, n, k order, which follows the column-major call).
+        want = sorted((row["m"], row["n"], row["k"]))
+        for _, params, solution, _ in tuned:
+            nums = [int(x) for x in re.findall(r"\d+", params)]
+            if any(sorted(nums[i:i + 3]) == want for i in range(max(len(nums) - 2, 0))):
+                row["torch_tuned_solution"] = solution
+                break
+        for key in ("ours_us", "torch_default_us", "torch_tuned_us"):
+            row[key] = round(row[key], 3)
+        row["ours_vs_tuned"] = round(row["torch_tuned_us"] / row["ours_us"], 3)
+        tf = row.pop("flops")
+        row["ours_TFLOP/s"] = round(tf / (row["ours_us"] * 1e-6) / 1e12, 2)
+        log(f"{row['workload']} M={row['m']}: ours {row['ours_us']:.2f} us, torch default "
+            f"{row['torch_default_us']:.2f} us, torch tuned {row['torch_tuned_us']:.2f} us "
+            f"({row.get('torch_tuned_solution', '?')})")
+    print(json.dumps({"vendor_tuned": "torch GPU GEMM, default and TunableOp-searched hipBLASLt / rocBLAS solution, "
+                                      "against the selected kernel; inputs resident; 200 graph-replayed launches",
+                      "tuning_ms_per_solution": VENDOR_TUNING_MS, "rows": rows, "tunableop_results": tuned}),
+          flush=True)
     return 0
 
 
@@ -431,6 +518,9 @@ def main() -> int:
     if args.decode_sweep:
         torch.cuda.set_device(0)
         return run_decode_sweep(torch, L)
+    if args.vendor_tuned:
+        torch.cuda.set_device(0)
+        return run_vendor_tuned(torch, L, W)
     if args.matrix:
         torch.cuda.set_device(0)
         rows = reference_matrix(torch, L, W, emit=lambda line: print(line, flush=True))

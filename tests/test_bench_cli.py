@@ -33,3 +33,16 @@ def test_matrix_inputs_are_the_reference_generators():
         # exact in both half formats
         for dt in (torch.float16, torch.bfloat16):
             assert torch.equal(a.to(dt).float(), a) and torch.equal(b.to(dt).float(), b)
+
+
+def test_vendor_tuned_cases_are_workloads():
+    """Every row of `bench.py --vendor-tuned` is a workload of the table at one
+    of its M values, with a single-call torch equivalent of the same output
+    dtype (the fp32-logit LM head has none)."""
+    W = bench.__dict__.get("VENDOR_TUNED_CASES")
+    import __graft_entry__
+    wl = __graft_entry__.load_package().workloads.WORKLOADS
+    assert W
+    for name, m in W:
+        assert name in wl and m in wl[name].ms
+        assert wl[name].dtype_out == wl[name].dtype_in
