@@ -11,6 +11,14 @@ constexpr int kLine = 64;   // K elements per line: 128 bytes = 8 chunks of 16 b
 // Source of the K-tail chunks: 16 zero bytes in global memory.
 __device__ u32x4_t g_decode_zero = {0u, 0u, 0u, 0u};
 
+// 16-byte load through a global-address-space pointer (a generic pointer that
+// may also hold the zero chunk's address would otherwise make it a flat load,
+// which also counts on the LDS counter).
+__device__ __forceinline__ u32x4_t load16_global(const void* p) {
+    typedef const __attribute__((address_space(1))) u32x4_t* gptr;
+    return *reinterpret_cast<gptr>(reinterpret_cast<uintptr_t>(p));
+}
+
 // Operands of the prologues (PRO_GATE, PRO_ADD_NORM; see gemm_common.hpp).
 struct ProArgs {
     const uint16_t* a2;      // gate or residual, leading dimension lda2
@@ -58,7 +66,8 @@ constexpr bool decode_cfg_fits() {
 // its 16-byte column chunks in position chunk ^ kn_line_swizzle(r), and the
 // W fragments (8 consecutive k of one column per lane) are read back with
 // gfx950's transposing LDS read, two ds_read_b64_tr_b16 of 4 k-rows each.
-template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO, int KN = 0>
+template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO, int KN = 0,
+          int AREG = 0>
 __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
@@ -66,7 +75,10 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     static_assert(AROWS == 8 || AROWS == 16 || AROWS == 32 || AROWS == 64, "rows of A per line");
     constexpr int MG = AROWS == 8 ? 1 : AROWS / 16;   // 16-row groups of A in the MFMA
     constexpr int IW = 2 * RG;                 // W copies per line (8 rows each)
-    constexpr int IA = AROWS / 8;              // A copies per line
+    // AREG: A's fragments are loaded from global memory straight into
+    // registers (with the line's W copies), so only W passes through LDS.
+    static_assert(!AREG || (PRO == PRO_NONE && !KN), "register A: plain A, W[N,K]");
+    constexpr int IA = AREG ? 0 : AROWS / 8;   // A copies per line
     constexpr int IP = PRO == PRO_NONE ? 0 : IA;   // gate or residual copies per line
     constexpr int IL = IW + IA + IP;
     static_assert(PRO == PRO_NONE || EPI == EPI_NONE || (PRO == PRO_ADD_NORM && EPI == EPI_SILU_MUL),
@@ -120,9 +132,15 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
             wsrc[h] = w + min_i64(n0 + 16 * r + rr, n - 1) * ldb + chunk * 8;
         }
     }
-    const uint16_t* asrc[IA];
+    const uint16_t* asrc[IA > 0 ? IA : 1];
 #pragma unroll
     for (int h = 0; h < IA; ++h) asrc[h] = a + min_i64(8 * h + r8, m - 1) * lda + chunk * 8;
+    // AREG: lane l's A fragment of group g is row 16 g + l % 16 (rows 0-7
+    // twice at AROWS = 8), 8 elements at chunk l / 16 of each 32-wide K-step.
+    const uint16_t* afrag[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g)
+        afrag[g] = a + min_i64(AROWS == 8 ? (lane & 7) : 16 * g + (lane & 15), m - 1) * lda + 8 * (lane >> 4);
     const uint16_t* psrc[IP > 0 ? IP : 1];
 #pragma unroll
     for (int h = 0; h < IP; ++h) psrc[h] = pro.a2 + min_i64(8 * h + r8, m - 1) * pro.lda2 + chunk * 8;
@@ -156,6 +174,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
         for (int bt = 0; bt < ROUND / LPB; ++bt) {
             if (l0 + int64_t(WAVES) * (bt * LPB) >= lines) break;
             u32x4_t nwv[LPB][2];   // PRO_ADD_NORM: the norm weight at the lane's two fragment chunks
+            u32x4_t areg[LPB][2][MG];   // AREG: the lane's A fragments of each K-step
 #pragma unroll
             for (int t = 0; t < LPB; ++t) {
                 const int64_t line = l0 + int64_t(WAVES) * (bt * LPB + t);
@@ -199,6 +218,25 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
 #pragma unroll
                     for (int h = 0; h < IP; ++h)
                         dma16(in_k ? static_cast<const void*>(psrc[h] + pk) : zero, dst + 1024u * (IW + IA + h));
+                }
+                if constexpr (AREG) {
+                    if (koff + kLine <= k) {
+#pragma unroll
+                        for (int st = 0; st < 2; ++st)
+#pragma unroll
+                            for (int g = 0; g < MG; ++g) areg[t][st][g] = load16_global(afrag[g] + koff + 32 * st);
+                    } else {
+                        // K tail: chunks past K load the zero chunk (a
+                        // pointer select, so no wait is tied to the value).
+#pragma unroll
+                        for (int st = 0; st < 2; ++st) {
+                            const bool in_k = koff + (4 * st + grp) * 8 < k;
+#pragma unroll
+                            for (int g = 0; g < MG; ++g)
+                                areg[t][st][g] =
+                                    load16_global(in_k ? static_cast<const void*>(afrag[g] + koff + 32 * st) : zero);
+                        }
+                    }
                 }
             }
             wait_vmcnt<0>();
@@ -255,7 +293,8 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                         for (int r = 0; r < RG; ++r) wf[r] = lb[(2 * r + hi) * 64 + slot];
                     }
 #pragma unroll
-                    for (int g = 0; g < MG; ++g) af[g] = lb[(IW + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot];
+                    for (int g = 0; g < MG; ++g)
+                        af[g] = AREG ? areg[t][st][g] : lb[(IW + (AROWS == 8 ? 0 : 2 * g + hi)) * 64 + slot];
                     if constexpr (PRO == PRO_ADD_NORM) {
                         // Element k of this fragment chunk; chunks past K are zero in h and r.
                         const int64_t kc = line * kLine + (4 * st + grp) * 8;
@@ -475,7 +514,7 @@ int launch_regs(const Problem& p, hipStream_t s) {
 }
 
 template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO = PRO_NONE,
-          int KN = 0>
+          int KN = 0, int AREG = 0>
 int launch_cfg(const Problem& p, hipStream_t s) {
     constexpr int OG = EPI == EPI_SILU_MUL ? RG / 2 : RG;
     if (p.m > AROWS) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above the configuration's rows");
@@ -485,7 +524,7 @@ int launch_cfg(const Problem& p, hipStream_t s) {
     if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
     const ProArgs pro{static_cast<const uint16_t*>(p.a2), p.lda2, p.group, p.group_stride,
                       static_cast<const uint16_t*>(p.norm_w), p.eps, static_cast<uint16_t*>(p.res_out), p.ldres};
-    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI, PRO, KN>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitk_decode_kernel<DT, DT_OUT, AROWS, RG, WAVES, LPB, PARTS, EPI, PRO, KN, AREG>), grid, block, 0, s,
                        static_cast<const uint16_t*>(p.a), static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k,
                        p.lda, p.ldb, p.ldc, p.keys, pro, p.sample);
     return check_launch("splitk_decode");

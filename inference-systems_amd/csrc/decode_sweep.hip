@@ -7,6 +7,8 @@
 // same kernel templates as the GEMM library.
 //   lds   rows = rows of A per copy, rg = W rows per workgroup, waves, lpb =
 //         lines per wave copied together (16 K partitions)
+//   areg  splitk_decode with A's fragments loaded from global memory straight
+//         into registers (only W copied into LDS): rows of A, rg, waves, lpb
 //   kn    the B[K,N] form of splitk_decode: rows of A per copy, 64 columns
 //         per workgroup, waves, lpb (16 partitions with 16 waves, 8 with 8)
 //   lines rows = rows of A loaded per line, rg = W rows per workgroup, waves,
@@ -193,6 +195,13 @@ struct SweepConfig {
     X((launch_cfg<BF, BF, 16, 3, 16, 1, 16, EPI_NONE>), "lds rows=16 rg=48 waves=16 lpb=1", 16, 0) \
     X((launch_cfg<BF, BF, 32, 1, 8, 1, 16, EPI_NONE>), "lds rows=32 rg=16 waves=8 lpb=1", 32, 0) \
     X((launch_cfg<BF, BF, 32, 2, 8, 1, 16, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 16, 1, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=8 rg=32 waves=16 lpb=1", 8, 0) \
+    X((launch_cfg<BF, BF, 16, 2, 16, 1, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=16 rg=32 waves=16 lpb=1", 16, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 16, 1, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=32 rg=32 waves=16 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 1, 16, 1, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=32 rg=16 waves=16 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 3, 16, 1, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=32 rg=48 waves=16 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 4, 16, 1, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=32 rg=64 waves=16 lpb=1", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 8, 2, 16, EPI_NONE, PRO_NONE, 0, 1>), "areg rows=32 rg=32 waves=8 lpb=2", 32, 0) \
     X((launch_cfg<BF, BF, 8, 4, 16, 1, 16, EPI_NONE, PRO_NONE, 1>), "kn rows=8 cols=64 waves=16 lpb=1", 8, 1) \
     X((launch_cfg<BF, BF, 8, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>), "kn rows=8 cols=64 waves=8 lpb=1", 8, 1) \
     X((launch_cfg<BF, BF, 16, 4, 8, 1, 8, EPI_NONE, PRO_NONE, 1>), "kn rows=16 cols=64 waves=8 lpb=1", 16, 1) \

@@ -49,7 +49,7 @@ def test_decode_sweep_library_lists_and_refuses():
     assert len(cfgs) >= 10
     names = [name for _, name, _, _ in cfgs]
     assert len(set(names)) == len(names)
-    assert all(name.split()[0] in ("lds", "lines", "kn") for name in names)
+    assert all(name.split()[0] in ("lds", "areg", "lines", "kn") for name in names)
     assert all(kn == (name.split()[0] == "kn") for _, name, _, kn in cfgs)
     assert {rows for _, _, rows, _ in cfgs} == {8, 16, 32}
     lib = P.load_sweep()
