@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
 torch op, the selection table) imports or calls this module; only tests/,
 ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may use it,
-and only as the checker.
+and only to check results.
 
 It restates, in numpy, what the reference computes on the CPU for this
 path (paths relative to the reference repo):

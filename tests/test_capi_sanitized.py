@@ -6,7 +6,7 @@ temporary directory, and the CPU tests of the C ABI (tests/test_capi.py) run
 against that copy in a child process with the sanitizer runtime preloaded.
 The reference ran its kernels under compute-sanitizer memcheck / racecheck
 (cuda_kernels/gemm/README.md:157-169); the host-side counterpart here is
-what the GPU pool allows (no GPU sanitizer runs).  No kernel is launched.
+the part a sanitizer can cover without a GPU-instrumented build.  No kernel is launched.
 """
 from __future__ import annotations
 
