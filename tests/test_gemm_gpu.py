@@ -274,6 +274,32 @@ def test_staged_ring_depths_ragged(m, n, k, din, dout):
     _check_tolerance(out.cpu(), a, w, L.B_NK, dout, rows=rows)
 
 
+@pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_staged_tile_choices_same_bits(din):
+    """Every tile choice of mfma_staged sums K in the same order, so a row's
+    output does not depend on how many rows share the launch: with N = 4104
+    and K = 1000, M = 100 / 600 / 1000 / 2100 select 64 x 64 tiles, 128 x 128
+    on the spread 3-deep ring, 128 x 256, and 128 x 128 on the 2-deep burst
+    ring, and the first 100 rows (fp32 outputs, so any reordering of the K
+    sum would show) are bit-identical across all four."""
+    n, k, rows = 4104, 1000, 100
+    gen = torch.Generator().manual_seed(4104)
+    a = torch.randn((2100, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    a_d, w_d = a.to(DEV), w.to(DEV)
+    first = None
+    for m in (100, 600, 1000, 2100):
+        _say(f"staged tile choice M={m} N={n} K={k} {NAME[din]}->f32")
+        out = G.gemm_with_kernel(a_d[:m], w_d, L.KERNEL_MFMA_STAGED, torch.float32, L.B_NK)
+        torch.cuda.synchronize()
+        head = out[:rows].cpu()
+        if first is None:
+            first = head
+            _check_tolerance(head, a[:rows], w, L.B_NK, torch.float32)
+        else:
+            assert torch.equal(head, first), f"M={m}: {int((head != first).sum())} of the first {rows} rows' outputs differ"
+
+
 STAGED_GRIDS_KN = [(600, 1000, 1000), (1100, 2000, 1000), (2100, 2000, 1000), (2100, 4104, 1000),
                    (2100, 7000, 1000), (40, 520, 72), (2048, 4096, 1024), (1, 6144, 1024), (5, 200, 136)]
 
