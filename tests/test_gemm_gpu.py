@@ -401,6 +401,31 @@ def test_splitk_configs_ragged(n, k, m, din, dout):
     _check_tolerance(out.cpu(), a, w, L.B_NK, dout)
 
 
+@pytest.mark.parametrize("n", [6144, 1000], ids=["N6144", "N1000"])
+def test_splitk_rows_same_bits_across_m(n):
+    """splitk_decode adds its 16 K partitions in the same order whatever the
+    number of A rows (8, 16 or 32 copied per line), so a row's output does not
+    depend on M from 2 to 32: the first two rows (fp32 outputs) are
+    bit-identical at M = 2, 8, 13, 16, 32, on the decode width and on a
+    narrow W (16-row workgroups)."""
+    k = 1024
+    gen = torch.Generator().manual_seed(n)
+    a = torch.randn((32, k), generator=gen).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(torch.bfloat16)
+    a_d, w_d = a.to(DEV), w.to(DEV)
+    first = None
+    for m in (2, 8, 13, 16, 32):
+        _say(f"splitk rows across M: M={m} N={n} K={k} bf16->f32")
+        out = G.gemm_with_kernel(a_d[:m], w_d, L.KERNEL_SPLITK_DECODE, torch.float32, L.B_NK)
+        torch.cuda.synchronize()
+        head = out[:2].cpu()
+        if first is None:
+            first = head
+            _check_tolerance(head, a[:2], w, L.B_NK, torch.float32)
+        else:
+            assert torch.equal(head, first), f"M={m}: {int((head != first).sum())} of the first two rows' outputs differ"
+
+
 SPLITK64_CASES = [(1000, 3592, 64), (4096, 1000, 33), (5000, 1000, 47), (9000, 1000, 64), (20000, 264, 40)]
 
 
