@@ -213,8 +213,14 @@ def run_probes(torch) -> int:
         P.mfma_rate(torch, iters=512)
     out["launch_floor"] = P.launch_floor(torch)
     log(f"launch floor: {out['launch_floor']}")
-    out["mfma_bf16_32x32x16"] = [P.mfma_rate(torch, workgroups=w) for w in (P.CUS, 2 * P.CUS)]
+    out["mfma_bf16_32x32x16"] = [P.mfma_rate(torch, workgroups=w, chains=c) for w in (P.CUS, 2 * P.CUS)
+                                 for c in (4, 8)]
     log(f"mfma: {out['mfma_bf16_32x32x16']}")
+    # The 16 x 16 x 32 instruction: a quarter of the flops per instruction,
+    # so 4, 8 and 16 independent accumulators per wave.
+    out["mfma_bf16_16x16x32"] = [P.mfma_rate(torch, workgroups=w, chains=c, shape="16x16x32")
+                                 for w in (P.CUS, 2 * P.CUS) for c in (4, 8, 16)]
+    log(f"mfma 16x16x32: {out['mfma_bf16_16x16x32']}")
     out["lds_read_b128"] = [P.lds_read(torch, workgroups=w) for w in (P.CUS, 2 * P.CUS)]
     log(f"lds reads: {out['lds_read_b128']}")
     # Copies from a window small enough for the vector L1 (16 KiB), for L2

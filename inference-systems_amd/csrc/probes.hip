@@ -17,6 +17,7 @@ namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kErr = -1;
@@ -230,6 +231,32 @@ __global__ __launch_bounds__(512) void mfma_kernel(int iters, uint32_t* sink, ui
     stamp(clocks, 1);
 }
 
+// v_mfma_f32_16x16x32_bf16 back to back: CHAINS independent accumulators
+// per wave (each accumulator is 4 registers), `iters` rounds.
+template <int CHAINS>
+__global__ __launch_bounds__(512) void mfma16_kernel(int iters, uint32_t* sink, uint64_t* clocks) {
+    stamp(clocks, 0);
+    const int lane = threadIdx.x & 63;
+    const __bf16 one = static_cast<__bf16>(1.0f / 1024.0f);
+    const __bf16 x = static_cast<__bf16>(float(lane & 7) / 8.0f);
+    const bf16x8_t a = {one, one, one, one, one, one, one, one};
+    const bf16x8_t b = {x, x, x, x, x, x, x, x};
+    f32x4_t acc[CHAINS];
+#pragma unroll
+    for (int c = 0; c < CHAINS; ++c) acc[c] = f32x4_t{};
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int c = 0; c < CHAINS; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[c], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s += acc[c][v];
+    sink_wave(sink, __builtin_bit_cast(uint32_t, s));
+    stamp(clocks, 1);
+}
+
 // Output-tile writes: workgroup w writes rows [128 (w / tiles_n), +128) x
 // bytes [512 (w % tiles_n), +512) of a row-major matrix with `ld` bytes per
 // row (the C tiles of a 128 x 256 bf16 GEMM grid), 16 bytes per lane and
@@ -330,6 +357,17 @@ int nvprobe_mfma(int workgroups, int iters, int chains, uint32_t* sink, uint64_t
     if (workgroups < 1 || iters < 1) return kErr;
     if (chains == 4) hipLaunchKernelGGL(mfma_kernel<4>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
     else if (chains == 8) hipLaunchKernelGGL(mfma_kernel<8>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
+    else return kErr;
+    return launched(hipSuccess);
+}
+
+// The same with v_mfma_f32_16x16x32_bf16 (a quarter of the flops per
+// instruction); chains 4, 8 or 16.
+int nvprobe_mfma16(int workgroups, int iters, int chains, uint32_t* sink, uint64_t* clocks, hipStream_t s) {
+    if (workgroups < 1 || iters < 1) return kErr;
+    if (chains == 4) hipLaunchKernelGGL(mfma16_kernel<4>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
+    else if (chains == 8) hipLaunchKernelGGL(mfma16_kernel<8>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
+    else if (chains == 16) hipLaunchKernelGGL(mfma16_kernel<16>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
     else return kErr;
     return launched(hipSuccess);
 }

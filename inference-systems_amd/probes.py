@@ -27,6 +27,7 @@ _SIGS = {
     "nvprobe_lds_read": [_INT, _INT, _VP, _VP, _VP],
     "nvprobe_copy": [_INT, _VP, _I64, _INT, _INT, _INT, _INT, _VP, _VP, _VP],
     "nvprobe_mfma": [_INT, _INT, _INT, _VP, _VP, _VP],
+    "nvprobe_mfma16": [_INT, _INT, _INT, _VP, _VP, _VP],
     "nvprobe_write_tiles": [_VP, _I64, _INT, _INT, _INT, _VP, _VP],
 }
 _lib = None
@@ -168,15 +169,23 @@ def copy_rate(torch, mode, workgroups=CUS, iters=512, inflight=8, window=4 << 20
             "TB/s": round(nbytes / (ms * 1e-3) / 1e12, 2)}
 
 
-def mfma_rate(torch, workgroups=CUS, iters=2048, chains=4):
+def mfma_rate(torch, workgroups=CUS, iters=2048, chains=4, shape="32x32x16"):
+    """bf16 MFMA throughput: 8 waves per workgroup, `chains` independent
+    accumulators per wave, v_mfma_f32_32x32x16_bf16 or (shape "16x16x32")
+    v_mfma_f32_16x16x32_bf16, whose instruction has a quarter of the flops."""
     lib = load()
     ctx = _Ctx(torch, workgroups)
-    run = lambda: _check(lib.nvprobe_mfma(workgroups, iters, chains, ctx.sink.data_ptr(), ctx.clocks.data_ptr(),  # noqa
-                                          ctx.stream()), "mfma")
+    entry = lib.nvprobe_mfma if shape == "32x32x16" else lib.nvprobe_mfma16
+    if shape == "16x16x32":
+        iters *= 4   # the same flops per wave
+    run = lambda: _check(entry(workgroups, iters, chains, ctx.sink.data_ptr(), ctx.clocks.data_ptr(),  # noqa
+                               ctx.stream()), "mfma")
     ms = ctx.time_ms(run)
     ghz = ctx.clock_ghz()
-    flops = workgroups * 8 * iters * chains * 2.0 * 32 * 32 * 16
-    return {"workgroups": workgroups, "chains": chains, "us": round(ms * 1e3, 2), "clock_ghz": round(ghz, 3),
+    per_instr = 32 * 32 * 16 if shape == "32x32x16" else 16 * 16 * 32
+    flops = workgroups * 8 * iters * chains * 2.0 * per_instr
+    return {"shape": shape, "workgroups": workgroups, "chains": chains, "us": round(ms * 1e3, 2),
+            "clock_ghz": round(ghz, 3),
             "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
             "peak_at_clock_TFLOP/s": round(2500.0 * ghz / 2.4, 1)}
 

@@ -35,6 +35,8 @@ def test_probes_refuse_unsafe_sizes_before_launch():
     assert lib.nvprobe_copy(0, fake, 4096, 256, 64, 8, 2, fake, None, None) == -1
     assert lib.nvprobe_copy(4, fake, 4096, 256, 64, 8, 0, fake, None, None) == -1
     assert lib.nvprobe_mfma(256, 16, 3, None, None, None) == -1
+    assert lib.nvprobe_mfma16(256, 16, 2, None, None, None) == -1
+    assert lib.nvprobe_mfma16(0, 16, 4, None, None, None) == -1
     # each 128-row tile writes 512 bytes per row: ld must cover tiles_n of them
     assert lib.nvprobe_write_tiles(None, 8192 - 16, 16, 16, 1, None, None) == -1
     assert lib.nvprobe_write_tiles(None, 8192 + 8, 16, 16, 1, None, None) == -1
