@@ -10,8 +10,9 @@
 //                 Replaces the shared-memory and register-tiled rungs
 //                 (gemm_tiled.cu:56-202), including their zero-filled edge
 //                 tiles, so any M, N, K and either B layout runs.  Problems
-//                 whose rows are whole 16-byte chunks take fp32_staged_kernel
-//                 (copies straight into a 3-deep LDS ring); the rest take
+//                 whose rows are whole 16-byte chunks take fp32_buffered_kernel
+//                 (buffer loads through registers into a double-buffered LDS
+//                 tile, 32 x 32 or 64 x 64 tiles); the rest take
 //                 fp32_tiled_kernel (scalar loads staged through registers
 //                 into a double-buffered LDS tile).
 #include <type_traits>
@@ -54,7 +55,6 @@ constexpr int kT32BM = 64;
 constexpr int kT32BN = 64;
 constexpr int kT32BK = 64;
 constexpr int kT32Pitch = kT32BK + 4;   // 68 floats: 16-lane ds_read_b128 groups hit 64 distinct banks
-constexpr int kT32Cpr = kT32BK / 4;     // 16-byte chunks per row of an A / W tile
 constexpr int kT32Threads = 512;        // 8 waves: two groups of 4 (2 x 2 over the tile)
 constexpr int kT32ScalarLoads = kT32BM * kT32BK / kT32Threads;   // 4-byte loads per operand per thread
 static_assert(kT32BM == 64 && kT32BN == 64, "B[K,N] tiles are read as rows of 64 floats");
@@ -201,214 +201,316 @@ __global__ __launch_bounds__(kT32Threads) void fp32_tiled_kernel(
     }
 }
 
-// fp32_staged: the fp32_tiled rung for problems whose rows are whole 16-byte
-// chunks (16-byte aligned bases and leading dimensions, K % 4 == 0, and N %
-// 4 == 0 for B[K,N]).  Same 64 x 64 tile, same two K-groups of four waves
-// and the same MFMA, but the operands move global -> LDS with
-// global_load_lds_dwordx4 into a 3-deep ring, with no register staging and
-// no LDS writes from the waves, and the copies of K-tile t + 2 are spread
-// between the MFMAs of K-tile t.  Each wave reads its fragments a quarter
-// K-tile ahead of its MFMAs and waits for the next K-tile before its last
-// quarter, so the matrix cores stay busy across the one barrier per K-tile.
-//
-// LDS stage (32 KiB): the A tile (64 rows x 16 chunks of 4 k), then the B
-// tile: W[N,K] rows like A; B[K,N] as 64 k-rows x 16 chunks of 4 columns,
-// copied as they lie in memory and read back one float per lane.
-//   A / W: chunk c of row r at position c ^ (r % 16): a ds_read_b128 of 16
-//     consecutive rows at one chunk then touches 16 distinct positions, all
-//     64 banks.
-//   B[K,N]: chunk c of k-row r at position c ^ (8 ((r / 16) % 2)): the b32
-//     read of one MFMA step takes 32 columns of k-rows r and r + 16, which
-//     then sit in opposite halves of the banks.
-constexpr int kF32StageChunks = 2 * kT32BM * kT32Cpr;   // 2048 16-byte chunks
-constexpr int kF32Ipw = kF32StageChunks / (64 * (kT32Threads / 64));   // copies per wave per K-tile
-static_assert(kF32Ipw == 4, "32 KiB per stage over 8 waves");
-constexpr int kF32Stages = 3;   // ring depth (4 stages measured the same at 1024^3 and 2048^3)
+// fp32_buffered: the fp32_tiled rung for problems whose rows are whole
+// 16-byte chunks (16-byte aligned bases and leading dimensions, K % 4 == 0,
+// and N % 4 == 0 for B[K,N]).  A BM x BN tile per 4-wave workgroup (a 2 x 2
+// grid of BM/2 x BN/2 wave tiles), K-tiles of BK:
+//   * the operands are read with buffer loads into registers, one 16-byte
+//     chunk per lane and instruction, and written to a double-buffered LDS
+//     tile with ds_write_b128.  The buffer resources cover the tile's rows
+//     (A, W[N,K]) or B[K,N]'s K rows, so rows past M / N and K-rows past K
+//     read as zeros, and a chunk that starts at or past K is given an
+//     out-of-range offset so it reads as zeros too;
+//   * the loads of K-tile t + 3 are issued during K-tile t, into the register
+//     set K-tile t + 1 has just left for the LDS, so every load has two
+//     K-tiles of MFMAs to arrive (the loop is unrolled by two so both set
+//     indices are compile-time constants);
+//   * inside a K-tile the LDS writes of K-tile t + 1 ride on the first
+//     MFMAs, the loads on the next, then one barrier, then the next K-tile's
+//     fragments are read while the last quarter of this one's MFMAs runs;
+//     the loop's back edge is at a point with no LDS access outstanding;
+//   * LDS rows of A / W[N,K] hold chunk c of row r at c ^ swz(r) (16
+//     consecutive rows at one chunk touch 16 distinct bank groups); B[K,N]
+//     k-rows are copied as they lie, the column chunks of odd 16-k-row groups
+//     flipped by half a row, so the two K halves of a wave's b32 reads sit
+//     in opposite halves of the banks;
+//   * MFMA step s of a K-tile takes k = STEPS (l / LH) + s in lane l, LH the
+//     lanes per k group of the instruction, so a lane's A (and W[N,K])
+//     values of a K-tile are one run of contiguous floats (ds_read_b128).
+// Two configurations (measured on MI355X against the 8-wave copy-into-LDS
+// kernel this replaces, in one process, fp32, B[K,N] unless noted):
+//   * 64 x 32 tiles (wave tiles of 32 x 16: two 16 x 16 blocks, so two
+//     independent v_mfma_f32_16x16x4_f32 chains per wave), BK = 64, while
+//     the grid has fewer than 512 tiles of 64 x 64: two workgroups per CU
+//     on 1024^3, so one's barrier waits hide under the other's MFMAs
+//     (1024^3 21.7 -> 19.5 us; W[N,K] 21.5 -> 19.3 us);
+//   * 64 x 64 tiles, v_mfma_f32_32x32x2_f32 in two accumulator chains (odd
+//     steps in the second, added before the store), BK = 32, on larger grids
+//     (2048^3 156.7 -> 126.6 us, 4096^3 1208.6 -> 966.6 us).
+// Measured beside them: 64 x 64 tiles with one chain, BK = 32, 20.6 / 148.4
+// / 959.6 us; 32 x 32 tiles, BK = 64, 19.2-20.8 / 143 / 1107 us; one
+// K-tile of loads in flight more or less, half a K-tile of MFMAs after the
+// barrier instead of a quarter, or capping the waves per SIMD at 2-4, moved
+// 1024^3 by at most 1% (two waves per SIMD: 3% slower).  A v_mfma_f32_16x16x4_f32
+// chain alone sustains 111 TFLOP/s at one wave per SIMD, two chains 150, and
+// one v_mfma_f32_32x32x2_f32 chain 153 (157.3 peak).
+__device__ __forceinline__ int fp32_row_swizzle(int r, int chunks) { return chunks == 16 ? (r & 15) : ((r >> 1) & 7); }
 
-// Source of the K-tail chunks: 16 zero bytes in global memory.
-__device__ u32x4_t g_f32_zero = {0u, 0u, 0u, 0u};
-
-template <int BL, int STAGES>
-__global__ __launch_bounds__(kT32Threads) void fp32_staged_kernel(
+template <int BL, int BM, int BN, int BK, int MI, int CHN>
+__global__ __launch_bounds__(256) void fp32_buffered_kernel(
     const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c,
     int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n) {
-    constexpr int AHEAD = STAGES - 1;   // K-tiles in flight beyond the one multiplied
-    static_assert(AHEAD >= 2 && AHEAD <= 3, "ring depth");
-    __shared__ u32x4_t ring[STAGES * kF32StageChunks];
+    constexpr int NT = 256;
+    constexpr int WM = BM / 2, WN = BN / 2;             // wave tile
+    constexpr int NBA = WM / MI, NBB = WN / MI;          // MI x MI blocks of the wave tile
+    static_assert(NBA >= 1 && NBB >= 1 && WM % MI == 0 && WN % MI == 0, "wave tile");
+    constexpr int ACH = BK / 4;                          // 16-byte chunks per row of a K-tile (A, W[N,K])
+    constexpr int A_CH = BM * ACH;
+    constexpr int KCH = BN / 4;                          // B[K,N]: chunks per k-row of a K-tile
+    constexpr int STAGE = A_CH + BN * ACH;               // chunks per LDS stage
+    constexpr int LPT = STAGE / NT;                      // loads per thread per K-tile
+    constexpr int LA = A_CH / NT;                        // of which A
+    static_assert(LPT * NT == STAGE && LA * NT == A_CH, "whole loads per thread");
+    constexpr int STEPS = MI == 32 ? BK / 2 : BK / 4;    // MFMA K-steps per K-tile
+    constexpr int LH = MI == 32 ? 32 : 16;               // lanes per k group of the MFMA
+    __shared__ u32x4_t lds[2 * STAGE];
+    auto kswz = [](int kr) { return (KCH / 2) * ((kr >> 4) & 1); };
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave >> 2;
-    const int wm = (wave >> 1) & 1;
-    const int wn = wave & 1;
-    const int half = lane >> 5;
-    const int r32 = lane & 31;
-
+    const int wm = wave >> 1, wn = wave & 1;
     int tm, tn;
     grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    const int64_t m0 = int64_t(tm) * kT32BM;
-    const int64_t n0 = int64_t(tn) * kT32BN;
-
-    // Copy instruction j of this wave fills stage chunks 64 i .. 64 i + 63,
-    // i = 4 wave + j: i < 16 rows 4 i .. 4 i + 3 of A, else rows (k-rows for
-    // B[K,N]) 4 (i - 16) .. of B.  Lane L takes row 4 i' + L / 16, position
-    // L % 16.  kpos[j]: the k (element of a row, or k-row of B[K,N]) its
-    // chunk starts at within the K-tile.
-    const float* src[kF32Ipw];
-    int kpos[kF32Ipw];
-    const int rin = lane >> 4, pos = lane & 15;
+    const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+    // Byte ranges (the launcher checks they fit in 31 bits): the tile's rows
+    // of A and W[N,K], all K rows of B[K,N] from column n0.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a + m0 * lda), short(0), int(((min_i64(BM, m - m0) - 1) * lda + k) * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb =
+        BL == NANOVLLM_GEMM_B_KN
+            ? __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(b + n0), short(0), int(((k - 1) * ldb + (n - n0)) * 4),
+                                                0x00020000)
+            : __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(b + n0 * ldb), short(0),
+                                                int(((min_i64(BN, n - n0) - 1) * ldb + k) * 4), 0x00020000);
+    // Load j of a thread: chunk q = j NT + tid of the K-tile, A rows first.
+    // voff: byte offset in its resource at K-tile 0; kpos: the k (A, W[N,K]
+    // chunk) or k-row (B[K,N]) it starts at in the K-tile; dst: LDS chunk.
+    uint32_t voff[LPT], dst[LPT];
+    int kpos[LPT];
 #pragma unroll
-    for (int j = 0; j < kF32Ipw; ++j) {
-        const int i = wave * kF32Ipw + j;
-        if (i < 16) {
-            const int row = 4 * i + rin;
-            const int lc = pos ^ (row & 15);
-            src[j] = a + min_i64(m0 + row, m - 1) * lda + 4 * lc;
-            kpos[j] = 4 * lc;
-        } else if constexpr (BL == NANOVLLM_GEMM_B_NK) {
-            const int row = 4 * (i - 16) + rin;
-            const int lc = pos ^ (row & 15);
-            src[j] = b + min_i64(n0 + row, n - 1) * ldb + 4 * lc;
-            kpos[j] = 4 * lc;
+    for (int j = 0; j < LPT; ++j) {
+        const int q = (j < LA ? j : j - LA) * NT + tid;
+        if (j < LA || BL == NANOVLLM_GEMM_B_NK) {
+            const int r = q / ACH, ch = q % ACH;
+            voff[j] = uint32_t((r * (j < LA ? lda : ldb) + ch * 4) * 4);
+            dst[j] = uint32_t((j < LA ? 0 : A_CH) + r * ACH + (ch ^ fp32_row_swizzle(r, ACH)));
+            kpos[j] = 4 * ch;
         } else {
-            const int kr = 4 * (i - 16) + rin;
-            const int lc = pos ^ (8 * ((kr >> 4) & 1));
-            src[j] = b + int64_t(kr) * ldb + min_i64(n0 + 4 * lc, n - 4);
+            const int kr = q / KCH, ch = q % KCH;
+            voff[j] = uint32_t((kr * ldb + ch * 4) * 4);
+            dst[j] = uint32_t(A_CH + kr * KCH + (ch ^ kswz(kr)));
             kpos[j] = kr;
         }
     }
-    const void* zero = &g_f32_zero;
-    asm volatile("" : "+s"(zero));
-    const int ktiles = static_cast<int>((k + kT32BK - 1) / kT32BK);
-    const uint32_t ring_lds = lds_address(ring);
-    auto issue_one = [&](int t, int stage, int j) {
-        const int64_t k0 = int64_t(t) * kT32BK;
-        const bool kn_row = BL == NANOVLLM_GEMM_B_KN && wave * kF32Ipw + j >= 16;
-        const void* s = k0 + kpos[j] < k ? static_cast<const void*>(src[j] + (kn_row ? k0 * ldb : k0)) : zero;
-        dma16(s, ring_lds + uint32_t(stage * kF32StageChunks + 64 * (wave * kF32Ipw + j)) * 16u);
-    };
-    auto issue = [&](int t, int stage) {
-#pragma unroll
-        for (int j = 0; j < kF32Ipw; ++j) issue_one(t, stage, j);
-    };
-
-    // Lane l takes k = 32 grp + 16 half + s of the K-tile in MFMA step s
-    // (0..15); quarter q holds steps 4 q .. 4 q + 3, one 16-byte chunk of an
-    // A (or W) row.
-    const int ai = wm * 32 + r32;
-    const int bj = wn * 32 + r32;
-    struct Frag {
-        f32x4_t a, b;
-    };
-    auto read_frag = [&](const u32x4_t* tile, int q) -> Frag {
-        const int lc = 8 * grp + 4 * half + q;
-        Frag f;
-        f.a = __builtin_bit_cast(f32x4_t, tile[ai * kT32Cpr + (lc ^ (ai & 15))]);
-        if constexpr (BL == NANOVLLM_GEMM_B_NK) {
-            f.b = __builtin_bit_cast(f32x4_t, tile[kT32BM * kT32Cpr + bj * kT32Cpr + (lc ^ (bj & 15))]);
+    const int ktiles = static_cast<int>((k + BK - 1) / BK);
+    // Loads of K-tile t.  Before the last K-tile every chunk lies inside K
+    // and inside the allocation, and the K-tile's offset goes in the scalar
+    // offset.  The last K-tile (CHECKED) puts the whole offset in the lane's
+    // offset register, which the range check covers, and gives chunks that
+    // start at or past K an out-of-range offset, so they read as zeros.
+    auto load_one = [&](u32x4_t& r, int j, int t, auto checked_c) {
+        const int k0 = t * BK;
+        const bool kn_row = BL == NANOVLLM_GEMM_B_KN && j >= LA;
+        const uint32_t step = kn_row ? uint32_t(k0) * uint32_t(ldb) * 4u : uint32_t(k0) * 4u;
+        if constexpr (decltype(checked_c)::value) {
+            const uint32_t vo = k0 + kpos[j] < k ? voff[j] + step : 0x80000000u;
+            r = __builtin_amdgcn_raw_buffer_load_b128(j < LA ? ra : rb, vo, 0, 0);
         } else {
-            const float* bt = reinterpret_cast<const float*>(tile + kT32BM * kT32Cpr);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int kr = 4 * lc + s;
-                f.b[s] = bt[(kr * kT32Cpr + ((bj >> 2) ^ (8 * ((kr >> 4) & 1)))) * 4 + (bj & 3)];
-            }
-        }
-        return f;
-    };
-    f32x16_t acc = {};
-    auto mfma4 = [&](const Frag& f) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[s], f.b[s], acc, 0, 0, 0);
-    };
-    // The 4 MFMAs of a quarter with copies J0 .. J0 + CNT - 1 of tile tt
-    // after its first CNT MFMAs.
-    auto mfma4_copy = [&](const Frag& f, int tt, int stage, int j0, int cnt) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[s], f.b[s], acc, 0, 0, 0);
-            if (s < cnt) {
-                __builtin_amdgcn_sched_barrier(0);
-                issue_one(tt, stage, j0 + s);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            r = __builtin_amdgcn_raw_buffer_load_b128(j < LA ? ra : rb, voff[j], int(step), 0);
         }
     };
+    using Checked = std::true_type;
+    using Unchecked = std::false_type;
+    u32x4_t rs[2][LPT];
 
-    // Tile u has landed in this wave's part of its stage once at most
-    // `later` tiles issued after it are still in flight.
-    auto wait_tiles_after = [&](int later) {
-        if (AHEAD >= 3 && later >= 2) wait_vmcnt<2 * kF32Ipw>();
-        else if (later >= 1) wait_vmcnt<kF32Ipw>();
-        else wait_vmcnt<0>();
-    };
+    const int frow = lane % LH, fh = lane / LH;
+    struct Frag { f32x4_t q[STEPS / 4]; };   // a lane's STEPS values of one block
+    Frag fa0[NBA], fb0[NBB], fa1[NBA], fb1[NBB];
+    auto read_frags = [&](int st, Frag (&fa)[NBA], Frag (&fb)[NBB]) {
+        const u32x4_t* tile = lds + st * STAGE;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < AHEAD; ++u)
-        if (u < ktiles) issue(u, u);
-    wait_tiles_after((ktiles < AHEAD ? ktiles : AHEAD) - 1);
-    lds_barrier();
-    Frag f0 = read_frag(ring, 0), f1;
-    int cur = 0;
-    // K-tile t: quarters 0-2 carry copies 2 / 1 / 1 of tile t + AHEAD into
-    // the stage tile t - 1 used (free since the barrier that opened tile t);
-    // the MFMAs run at raised wave priority, dropped before the wait for
-    // tile t + 1.  COPY (whether tile t + AHEAD exists) is a compile-time
-    // choice, and the tiles with and without copies run in two loops: a
-    // branch between the two forms inside one loop body gives the
-    // accumulator different registers on each path, and the copies that
-    // join them wait for the MFMA chain.
-    auto k_tile = [&](int t, auto copy_c) {
-        constexpr bool COPY = decltype(copy_c)::value;
-        const u32x4_t* tile = ring + cur * kF32StageChunks;
-        const int refill = cur == 0 ? STAGES - 1 : cur - 1;
-        const int next = cur + 1 == STAGES ? 0 : cur + 1;
-        __builtin_amdgcn_s_setprio(3);
-        f1 = read_frag(tile, 1);
-        if constexpr (COPY) mfma4_copy(f0, t + AHEAD, refill, 0, 2);
-        else mfma4(f0);
-        f0 = read_frag(tile, 2);
-        if constexpr (COPY) mfma4_copy(f1, t + AHEAD, refill, 2, 1);
-        else mfma4(f1);
-        f1 = read_frag(tile, 3);
-        if constexpr (COPY) mfma4_copy(f0, t + AHEAD, refill, 3, 1);
-        else mfma4(f0);
-        __builtin_amdgcn_s_setprio(0);
-        if (t + 1 < ktiles) {
-            if constexpr (COPY) {
-                if constexpr (AHEAD >= 3) wait_vmcnt<2 * kF32Ipw>();
-                else wait_vmcnt<kF32Ipw>();
+        for (int i = 0; i < NBA; ++i) {
+            const int r = wm * WM + MI * i + frow;
+#pragma unroll
+            for (int q = 0; q < STEPS / 4; ++q) {
+                const int ch = (STEPS / 4) * fh + q;
+                fa[i].q[q] = __builtin_bit_cast(f32x4_t, tile[r * ACH + (ch ^ fp32_row_swizzle(r, ACH))]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBB; ++i) {
+            const int col = wn * WN + MI * i + frow;
+            if constexpr (BL == NANOVLLM_GEMM_B_KN) {
+                const float* bt = reinterpret_cast<const float*>(tile + A_CH);
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s) {
+                    const int kr = STEPS * fh + s;
+                    fb[i].q[s / 4][s % 4] = bt[kr * BN + (((col >> 2) ^ kswz(kr)) << 2) + (col & 3)];
+                }
             } else {
-                wait_tiles_after(ktiles - 2 - t);
+#pragma unroll
+                for (int q = 0; q < STEPS / 4; ++q) {
+                    const int ch = (STEPS / 4) * fh + q;
+                    fb[i].q[q] = __builtin_bit_cast(f32x4_t, tile[A_CH + col * ACH + (ch ^ fp32_row_swizzle(col, ACH))]);
+                }
             }
-            lds_barrier();
-            f0 = read_frag(ring + next * kF32StageChunks, 0);
         }
-        cur = next;
-        mfma4(f1);
+        __builtin_amdgcn_sched_barrier(0);
     };
-    int t = 0;
-    for (; t + AHEAD < ktiles; ++t) k_tile(t, std::true_type{});
-    for (; t < ktiles; ++t) k_tile(t, std::false_type{});
+    typedef std::conditional_t<MI == 32, f32x16_t, f32x4_t> acc_t;
+    acc_t acc[CHN][NBB][NBA];
+#pragma unroll
+    for (int h = 0; h < CHN; ++h)
+#pragma unroll
+        for (int i = 0; i < NBB; ++i)
+#pragma unroll
+            for (int j = 0; j < NBA; ++j) acc[h][i][j] = acc_t{};
+    // The MFMAs of steps [S0, S1) with CNT of the memory operations `fn`
+    // spread evenly between them (the scheduling barriers pin each one).
+    auto mfmas = [&](const Frag (&fa)[NBA], const Frag (&fb)[NBB], auto s0_c, auto s1_c, auto fn, auto cnt_c) {
+        constexpr int S0 = decltype(s0_c)::value, S1 = decltype(s1_c)::value, CNT = decltype(cnt_c)::value;
+        constexpr int PER = NBA * NBB, TOT = (S1 - S0) * PER;
+#pragma unroll
+        for (int x = 0; x < TOT; ++x) {
+            const int s = S0 + x / PER, i = (x / NBA) % NBB, j = x % NBA;
+            acc_t& d = acc[s % CHN][i][j];
+            // B's block (output columns) first: its rows are the rows of the product.
+            if constexpr (MI == 32)
+                d = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[i].q[s / 4][s % 4], fa[j].q[s / 4][s % 4], d, 0, 0, 0);
+            else
+                d = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[i].q[s / 4][s % 4], fa[j].q[s / 4][s % 4], d, 0, 0, 0);
+            const int from = x * CNT / TOT, to = (x + 1) * CNT / TOT;
+            if (to > from) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int y = from; y < to; ++y) fn(y);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    auto none = [](int) {};
+    using C0 = std::integral_constant<int, 0>;
+    using CL = std::integral_constant<int, LPT>;
+    using SMID = std::integral_constant<int, (STEPS - STEPS / 4) / 2>;
+    using STAIL = std::integral_constant<int, STEPS - STEPS / 4>;
+    using SEND = std::integral_constant<int, STEPS>;
 
-    // Group 1's partial tile to group 0 through LDS, once every wave is done
-    // reading the last K-tile.
-    lds_barrier();
-    float* xch = reinterpret_cast<float*>(ring);
-    if (grp == 1) {
+    // Prologue: K-tiles 0 and 1 into the register sets, K-tile 0 into stage
+    // 0, K-tile 2 into set 0.
 #pragma unroll
-        for (int v = 0; v < 16; ++v) xch[((wave & 3) * 16 + v) * 64 + lane] = acc[v];
+    for (int j = 0; j < LPT; ++j) load_one(rs[0][j], j, 0, Checked{});
+    if (ktiles > 1) {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) load_one(rs[1][j], j, 1, Checked{});
+    }
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) lds[dst[j]] = rs[0][j];
+    if (ktiles > 2) {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) load_one(rs[0][j], j, 2, Checked{});
     }
     lds_barrier();
-    if (grp == 1) return;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] += xch[((wave & 3) * 16 + v) * 64 + lane];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wm * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        const int64_t col = n0 + bj;
-        if (row < m && col < n) __builtin_nontemporal_store(acc[v], c + row * ldc + col);
+    read_frags(0, fa0, fb0);
+    // K-tile t, fragments in (fac, fbc): K-tile t + 1 from set SET into stage
+    // (t + 1) % 2 (when it exists), then K-tile t + 3 into SET (when it
+    // exists); the next K-tile's fragments go to (fan, fbn).
+    auto k_tile = [&](int t, auto set_c, Frag (&fac)[NBA], Frag (&fbc)[NBB], Frag (&fan)[NBA], Frag (&fbn)[NBB],
+                      bool load, bool write, auto checked_c) {
+        constexpr int SET = decltype(set_c)::value;
+        const int st = t & 1;
+        auto ld = [&](int j) { load_one(rs[SET][j], j, t + 3, checked_c); };
+        auto wr = [&](int j) { lds[(st ^ 1) * STAGE + dst[j]] = rs[SET][j]; };
+        // The MFMAs before the barrier run at raised wave priority, dropped
+        // before it: of the waves on a SIMD, those still multiplying issue
+        // ahead of those that have reached the barrier.
+        __builtin_amdgcn_s_setprio(3);
+        if (write) mfmas(fac, fbc, C0{}, SMID{}, wr, CL{});
+        else mfmas(fac, fbc, C0{}, SMID{}, none, C0{});
+        if (load) mfmas(fac, fbc, SMID{}, STAIL{}, ld, CL{});
+        else mfmas(fac, fbc, SMID{}, STAIL{}, none, C0{});
+        __builtin_amdgcn_s_setprio(0);
+        if (write) {
+            lds_barrier();
+            read_frags(st ^ 1, fan, fbn);
+        }
+        mfmas(fac, fbc, STAIL{}, SEND{}, none, C0{});
+    };
+    using Set0 = std::integral_constant<int, 0>;
+    using Set1 = std::integral_constant<int, 1>;
+    int t = 0;
+    // Two K-tiles per trip; every load and write of the trip exists, and the
+    // loads (of K-tiles t + 3, t + 4) precede the last K-tile.
+    for (; t + 5 < ktiles; t += 2) {
+        k_tile(t, Set1{}, fa0, fb0, fa1, fb1, true, true, Unchecked{});
+        k_tile(t + 1, Set0{}, fa1, fb1, fa0, fb0, true, true, Unchecked{});
     }
+    // The last (at most five) K-tiles as fixed sequences: t is even, so
+    // K-tile t + i uses set (i + 1) % 2 and fragment set i % 2; the only load
+    // into the last K-tile is the checked one.
+    auto tail = [&](int i, auto load_c, auto write_c, auto checked_c) {
+        constexpr bool LOAD = decltype(load_c)::value, WRITE = decltype(write_c)::value;
+        if (i % 2 == 0) k_tile(t + i, Set1{}, fa0, fb0, fa1, fb1, LOAD, WRITE, checked_c);
+        else k_tile(t + i, Set0{}, fa1, fb1, fa0, fb0, LOAD, WRITE, checked_c);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    switch (ktiles - t) {
+        case 5:
+            tail(0, T{}, T{}, Unchecked{});
+            tail(1, T{}, T{}, Checked{});
+            tail(2, F{}, T{}, Unchecked{});
+            tail(3, F{}, T{}, Unchecked{});
+            tail(4, F{}, F{}, Unchecked{});
+            break;
+        case 4:
+            tail(0, T{}, T{}, Checked{});
+            tail(1, F{}, T{}, Unchecked{});
+            tail(2, F{}, T{}, Unchecked{});
+            tail(3, F{}, F{}, Unchecked{});
+            break;
+        case 3:
+            tail(0, F{}, T{}, Unchecked{});
+            tail(1, F{}, T{}, Unchecked{});
+            tail(2, F{}, F{}, Unchecked{});
+            break;
+        case 2:
+            tail(0, F{}, T{}, Unchecked{});
+            tail(1, F{}, F{}, Unchecked{});
+            break;
+        default:
+            tail(0, F{}, F{}, Unchecked{});
+            break;
+    }
+    if constexpr (CHN == 2) {
+#pragma unroll
+        for (int i = 0; i < NBB; ++i)
+#pragma unroll
+            for (int j = 0; j < NBA; ++j) acc[0][i][j] += acc[1][i][j];
+    }
+    // acc[0][i][j][v]: MI = 32: D[n = 8 (v / 4) + 4 (l / 32) + v % 4][m = l % 32];
+    // MI = 16: D[n = 4 (l / 16) + v][m = l % 16] of block (i, j): 4 adjacent
+    // output columns of one row per quad.
+#pragma unroll
+    for (int i = 0; i < NBB; ++i)
+#pragma unroll
+        for (int j = 0; j < NBA; ++j) {
+            const int64_t row = m0 + wm * WM + MI * j + frow;
+#pragma unroll
+            for (int q = 0; q < MI * MI / 256; ++q) {
+                const int64_t col = n0 + wn * WN + MI * i + (MI == 32 ? 8 * q + 4 * fh : 4 * fh);
+                const acc_t& v = acc[0][i][j];
+                const f32x4_t o = f32x4_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                if (row >= m) continue;
+                if (col + 3 < n && ldc % 4 == 0) {
+                    __builtin_nontemporal_store(o, reinterpret_cast<f32x4_t*>(c + row * ldc + col));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < n) c[row * ldc + col + e] = o[e];
+                }
+            }
+        }
 }
 
 }  // namespace
@@ -429,31 +531,52 @@ int launch_fp32_naive(const Problem& p, hipStream_t s) {
     return check_launch("fp32_naive");
 }
 
+namespace {
+
+template <int BL, int BM, int BN, int BK, int MI, int CHN>
+void launch_buffered(const Problem& p, hipStream_t s) {
+    const int64_t tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
+    hipLaunchKernelGGL((fp32_buffered_kernel<BL, BM, BN, BK, MI, CHN>), dim3(static_cast<uint32_t>(tiles_m * tiles_n)),
+                       dim3(256), 0, s, static_cast<const float*>(p.a), static_cast<const float*>(p.b),
+                       static_cast<float*>(p.c), p.m, p.n, p.k, p.lda, p.ldb, p.ldc, int(tiles_m), int(tiles_n));
+}
+
+template <int BL>
+void launch_buffered_for(const Problem& p, hipStream_t s) {
+    const int64_t tiles64 = ((p.m + 63) / 64) * ((p.n + 63) / 64);
+    if (tiles64 < 512) launch_buffered<BL, 64, 32, 64, 16, 1>(p, s);
+    else launch_buffered<BL, 64, 64, 32, 32, 2>(p, s);
+}
+
+}  // namespace
+
 int launch_fp32_tiled(const Problem& p, hipStream_t s) {
     const int64_t tiles_m = (p.m + kT32BM - 1) / kT32BM, tiles_n = (p.n + kT32BN - 1) / kT32BN;
-    if (tiles_m * tiles_n > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "fp32_tiled: grid too large");
+    if (tiles_m * tiles_n > INT32_MAX / 4) return set_error(NANOVLLM_GEMM_EINVAL, "fp32_tiled: grid too large");
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n)), block(kT32Threads);
     const float* a = static_cast<const float*>(p.a);
     const float* b = static_cast<const float*>(p.b);
     float* c = static_cast<float*>(p.c);
-    // The 16-byte copies of fp32_staged need aligned bases and leading dims
+    // The 16-byte loads of fp32_buffered need aligned bases and leading dims
     // and chunks of 4 that do not straddle a row end: K % 4 == 0 (A and
-    // W[N,K] rows), N % 4 == 0 (B[K,N] rows).
+    // W[N,K] rows), N % 4 == 0 (B[K,N] rows); its buffer ranges are 31-bit
+    // byte counts: 64 rows of A or W[N,K], or all of B[K,N] from a column.
+    constexpr int64_t kRange = int64_t(1) << 31;
     const bool aligned = reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 &&
                          p.lda % 4 == 0 && p.ldb % 4 == 0 && p.k % 4 == 0;
-    const bool staged = aligned && (p.b_layout == NANOVLLM_GEMM_B_NK || p.n % 4 == 0);
+    const bool ranges = 64 * p.lda * 4 < kRange &&
+                        (p.b_layout == NANOVLLM_GEMM_B_NK ? 64 * p.ldb * 4 < kRange : p.k * p.ldb * 4 < kRange);
+    const bool buffered = aligned && ranges && (p.b_layout == NANOVLLM_GEMM_B_NK || p.n % 4 == 0);
     const int ti = int(tiles_m), tj = int(tiles_n);
     if (p.b_layout == NANOVLLM_GEMM_B_NK) {
-        if (staged)
-            hipLaunchKernelGGL((fp32_staged_kernel<NANOVLLM_GEMM_B_NK, kF32Stages>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
-                               p.lda, p.ldb, p.ldc, ti, tj);
+        if (buffered)
+            launch_buffered_for<NANOVLLM_GEMM_B_NK>(p, s);
         else
             hipLaunchKernelGGL(fp32_tiled_kernel<NANOVLLM_GEMM_B_NK>, grid, block, 0, s, a, b, c, p.m, p.n, p.k,
                                p.lda, p.ldb, p.ldc, ti, tj);
     } else {
-        if (staged)
-            hipLaunchKernelGGL((fp32_staged_kernel<NANOVLLM_GEMM_B_KN, kF32Stages>), grid, block, 0, s, a, b, c, p.m, p.n, p.k,
-                               p.lda, p.ldb, p.ldc, ti, tj);
+        if (buffered)
+            launch_buffered_for<NANOVLLM_GEMM_B_KN>(p, s);
         else
             hipLaunchKernelGGL(fp32_tiled_kernel<NANOVLLM_GEMM_B_KN>, grid, block, 0, s, a, b, c, p.m, p.n, p.k,
                                p.lda, p.ldb, p.ldc, ti, tj);

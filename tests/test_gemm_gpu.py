@@ -163,19 +163,21 @@ def test_fp32_reference_known_answer(kernel, layout):
     assert orc.rel_frobenius(out.cpu().numpy(), ref) <= 1e-5
 
 
-FP32_STAGED_SHAPES = [(1, 4, 4), (3, 8, 60), (64, 64, 64), (65, 68, 68), (130, 196, 132), (127, 192, 260),
-                      (200, 256, 1028), (257, 132, 192)]
+# The last two take the 64 x 64 tiles (at least 512 of them), the others the
+# 64 x 32 tiles.
+FP32_BUFFERED_SHAPES = [(1, 4, 4), (3, 8, 60), (64, 64, 64), (65, 68, 68), (130, 196, 132), (127, 192, 260),
+                        (200, 256, 1028), (257, 132, 192), (1500, 1400, 68), (1090, 1028, 100)]
 
 
 @pytest.mark.parametrize("layout", [L.B_KN, L.B_NK], ids=["kn", "nk"])
-def test_fp32_staged_ragged(layout):
+def test_fp32_buffered_ragged(layout):
     """fp32_tiled on 16-byte rows (K % 4 == 0, N % 4 == 0 for B[K,N]): the
-    copy-into-LDS form, on edge tiles in M and N and K tails that are not a
-    multiple of the 64-wide K-tile; check_result against the float64 product
-    and relative Frobenius <= 1e-5."""
+    buffered form, on edge tiles in M and N and K tails that are not a
+    multiple of the 32- or 64-wide K-tile, in both tile configurations;
+    check_result against the float64 product and relative Frobenius <= 1e-5."""
     gen = torch.Generator().manual_seed(21)
-    for m, n, k in FP32_STAGED_SHAPES:
-        _say(f"fp32 staged {LAYOUT[layout]} M={m} N={n} K={k}")
+    for m, n, k in FP32_BUFFERED_SHAPES:
+        _say(f"fp32 buffered {LAYOUT[layout]} M={m} N={n} K={k}")
         a = torch.rand((m, k), generator=gen) * 2 - 1
         b = torch.rand((n, k) if layout == L.B_NK else (k, n), generator=gen) * 2 - 1
         out = G.gemm_with_kernel(a.to(DEV), b.to(DEV), L.KERNEL_FP32_TILED, torch.float32, layout)
@@ -185,6 +187,36 @@ def test_fp32_staged_ragged(layout):
         chk = orc.check_result(got, ref.astype(np.float32))
         assert chk["correct"], (m, n, k, chk)
         assert orc.rel_frobenius(got, ref) <= 1e-5, (m, n, k)
+
+
+@pytest.mark.parametrize("layout", [L.B_KN, L.B_NK], ids=["kn", "nk"])
+@pytest.mark.parametrize("m,n,k", [(130, 196, 132), (1500, 1400, 68)], ids=["tiles64x32", "tiles64x64"])
+def test_fp32_buffered_padded_leading_dims(layout, m, n, k):
+    """The buffered fp32 form through the C ABI with lda > K and ldb past the
+    row length (K + 12 for W[N,K], N + 20 for B[K,N]): the padding holds NaN,
+    which must not reach any output; every output element checked."""
+    gen = torch.Generator().manual_seed(23 + m)
+    lda = k + 8
+    rows_b, cols_b = (n, k) if layout == L.B_NK else (k, n)
+    ldb = cols_b + (12 if layout == L.B_NK else 20)
+    a_full = torch.full((m, lda), float("nan"))
+    a_full[:, :k] = torch.rand((m, k), generator=gen) * 2 - 1
+    b_full = torch.full((rows_b, ldb), float("nan"))
+    b_full[:, :cols_b] = torch.rand((rows_b, cols_b), generator=gen) * 2 - 1
+    ad, bd = a_full.to(DEV), b_full.to(DEV)
+    c = torch.empty((m, n), device=DEV)
+    _say(f"fp32 buffered padded {LAYOUT[layout]} M={m} N={n} K={k} lda={lda} ldb={ldb}")
+    L.gemm_raw(ad.data_ptr(), bd.data_ptr(), c.data_ptr(), m, n, k, lda, ldb, n, layout, L.F32, L.F32,
+               torch.cuda.current_stream().cuda_stream, L.KERNEL_FP32_TILED)
+    torch.cuda.synchronize()
+    a64 = a_full[:, :k].double()
+    b64 = b_full[:, :cols_b].double()
+    ref = (a64 @ (b64.T if layout == L.B_NK else b64)).numpy()
+    got = c.cpu().numpy()
+    assert np.isfinite(got).all()
+    chk = orc.check_result(got, ref.astype(np.float32))
+    assert chk["correct"], chk
+    assert orc.rel_frobenius(got, ref) <= 1e-5
 
 
 # ---------------------------------------------------------------------------
