@@ -331,11 +331,16 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
     // A-row group g, in partition wave + WAVES q.  Each wave writes its
     // partition tiles to its own region (its last reads of it completed at
     // the wait above); partition p then sits in wave p % WAVES, slot
-    // p / WAVES.  Within a 16 x 16 tile, (n, m) is stored at 16 n + (m ^ n):
-    // the writes (16 lanes along m) and the reads below (16 lanes along n)
-    // both hit 16 distinct banks.
+    // p / WAVES.  Within a 16 x 16 tile, (n, m) is stored at
+    // 64 (n % 4) + 16 (n / 4) + (m ^ 4 (n % 4)), i.e. in bank
+    // 16 (n / 4) + (m ^ 4 (n % 4)) of the 64: one write instruction (fixed
+    // v, lanes over n / 4 and m) and the reads below (a wave's threads over
+    // 16 n and 4 consecutive m) each touch 64 distinct banks.  (With
+    // 16 n + (m ^ n) the writes touched 16 banks, four lanes each: the
+    // bank-conflict stalls the counters showed.)
     auto part = [&](int wv, int q, int r, int g, int nn, int mm) -> float& {
-        return reinterpret_cast<float*>(&buf[wv][0])[(((q * RG + r) * MG + g) * 16 + nn) * 16 + (mm ^ nn)];
+        return reinterpret_cast<float*>(&buf[wv][0])[((q * RG + r) * MG + g) * 256 + 64 * (nn & 3) + 16 * (nn >> 2) +
+                                                     (mm ^ (4 * (nn & 3)))];
     };
 #pragma unroll
     for (int q = 0; q < PW; ++q)
