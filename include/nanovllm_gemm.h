@@ -223,11 +223,15 @@ int nanovllm_gemm_argmax(const void* a, const void* w,
  * reference.  The partial keys go to a scratch array the library holds in
  * device memory: 8 MiB per device (1 << 23 bytes), enough for every
  * problem whose nanovllm_gemm_argmax_workspace_bytes() is at most that
- * (the 151936-entry vocabulary up to m = 512); larger problems return
- * NANOVLLM_GEMM_EINVAL before anything is launched.  Calls no allocator.
- * Every call on one device shares that device's array: calls that overlap
- * on one device (two streams, two threads) race and must be ordered by the
- * caller.  Same arguments and results as nanovllm_gemm_argmax otherwise.
+ * (the 151936-entry vocabulary up to m = 883: 1187 keys of 8 bytes per
+ * row); larger problems return NANOVLLM_GEMM_EINVAL before anything is
+ * launched.  Calls no allocator.  The first call with m >= 1 on a device
+ * resolves that device's copy of the array (hipGetSymbolAddress, with the
+ * stream's device made current for the call): make it before capturing a
+ * HIP graph that contains this entry point.  Every call on one device
+ * shares that device's array: calls that overlap on one device (two
+ * streams, two threads) race and must be ordered by the caller.  Same
+ * arguments and results as nanovllm_gemm_argmax otherwise.
  */
 int nanovllm_gemm_argmax_noalloc(const void* a, const void* w,
                                  int64_t* tokens, float* max_logits,

@@ -297,11 +297,13 @@ def test_argmax_noalloc_validates_before_launch(lib):
     assert rc == L.EUNSUPPORTED
     rc = lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, 4, 64, 16, 16, 16, BF16, F16, None)
     assert rc == L.EINVAL and "logit_dtype" in L.last_error()
-    # the Qwen vocabulary fits up to m = 512 on the staged head's 128 columns per key
-    assert L.argmax_workspace_bytes(512, 151936, 1024, 1024, 1024, BF16) <= 8 << 20
-    assert L.argmax_workspace_bytes(1024, 151936, 1024, 1024, 1024, BF16) > 8 << 20
-    rc = lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, 1024, 151936, 1024, 1024, 1024, BF16, BF16, None)
-    assert rc == L.EINVAL and "scratch" in L.last_error() and "nanovllm_gemm_argmax" in L.last_error()
+    # The Qwen vocabulary: 1187 keys of 8 bytes per row (128 columns per key),
+    # so the 8 MiB array holds m <= 883; m = 884 is refused before any device call.
+    assert L.argmax_workspace_bytes(883, 151936, 1024, 1024, 1024, BF16) <= 8 << 20
+    assert L.argmax_workspace_bytes(884, 151936, 1024, 1024, 1024, BF16) > 8 << 20
+    for m in (884, 1024):
+        rc = lib.nanovllm_gemm_argmax_noalloc(None, None, None, None, m, 151936, 1024, 1024, 1024, BF16, BF16, None)
+        assert rc == L.EINVAL and "scratch" in L.last_error() and "nanovllm_gemm_argmax" in L.last_error()
 
 
 def test_sample_validates_before_launch(lib):

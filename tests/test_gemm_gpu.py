@@ -91,17 +91,19 @@ def _check_tolerance(got: torch.Tensor, a: torch.Tensor, b: torch.Tensor, layout
         assert rel <= 1e-5, f"relative Frobenius error {rel:.3g}"
         return {"rel_frobenius": rel}
     stats = orc.narrow_parity(_to_np_out(got, dout), _fp32_reference(a, b, layout, dout, rows), r, s, NAME[dout])
-    _assert_narrow(stats)
+    _assert_narrow(stats, NAME[dout])
     del got_all
     return stats
 
 
-def _assert_narrow(stats):
+def _assert_narrow(stats, dtype: str):
     """Every non-cancellation element within 2 ulp of the fp32 reference,
     and at most oracle.cancellation_cap cancellation elements beyond it."""
     ok = stats.pop("ok")
+    _say(f"  narrow {dtype}: {ok.size} outputs, {stats['cancel_beyond']} cancellation elements beyond 2 ulp "
+         f"(cap {orc.cancellation_cap(ok.size, dtype)}), max ulp {stats['max_ulp_checked']}")
     assert ok.all(), f"{int((~ok).sum())} elements beyond 2 ulp of the fp32 reference ({stats})"
-    assert stats["cancel_beyond"] <= orc.cancellation_cap(ok.size), stats
+    assert stats["cancel_beyond"] <= orc.cancellation_cap(ok.size, dtype), stats
 
 
 # ---------------------------------------------------------------------------
@@ -274,7 +276,7 @@ def test_workload_parity(name, m):
         assert orc.check_result(got.numpy(), ref64.astype(np.float32))["correct"]
         return
     rows = None
-    if m * wl.n * wl.k > 2 ** 33:   # large LM head: check 64 rows spread over M, all N
+    if m * wl.n * wl.k > 2 ** 36:   # the LM head at M = 512: 64 rows spread over M, all N
         rows = np.unique(np.linspace(0, m - 1, 64).astype(int))
     stats = _check_tolerance(got, a, b, wl.b_layout, wl.dtype_out, rows=rows)
     _say(f"  {name} M={m}: {stats}")
@@ -376,8 +378,9 @@ def test_splitk_kn_ragged(m, n, k, din, dout):
     with the transposing LDS read; N a multiple of 8 but not of 64 (the last
     workgroup's chunks past N read the last chunk and are not stored), K
     ending in a partial 64-row line (zeros past K), every A-row count.  Up to
-    M = 8 both layouts use 16 K partitions in the same order, so the product
-    equals the W[N,K] splitk_decode result bit for bit."""
+    M = 8, and with N below 65536 (every case here), both layouts use 16 K
+    partitions in the same order, so the product equals the W[N,K]
+    splitk_decode result bit for bit."""
     _say(f"splitk B[K,N] M={m} N={n} K={k} {NAME[din]}->{NAME[dout]}")
     gen = torch.Generator().manual_seed(5 * m + n + k)
     a = torch.randn((m, k), generator=gen).to(din)
@@ -433,20 +436,31 @@ def test_splitk_configs_ragged(n, k, m, din, dout):
     _check_tolerance(out.cpu(), a, w, L.B_NK, dout)
 
 
-@pytest.mark.parametrize("n", [6144, 1000], ids=["N6144", "N1000"])
-def test_splitk_rows_same_bits_across_m(n):
-    """splitk_decode adds its 16 K partitions in the same order whatever the
-    number of A rows (8, 16 or 32 copied per line), so a row's output does not
-    depend on M from 2 to 32: the first two rows (fp32 outputs) are
-    bit-identical at M = 2, 8, 13, 16, 32, on the decode width and on a
-    narrow W (16-row workgroups)."""
+# (N, A-row counts that share one K-partition order).  Below 65536 W rows
+# every M from 2 to 32 uses 16 partitions; the LM-head width uses 8
+# partitions for M = 2-16 and 4 for M = 17-32 (M = 1 takes the
+# register-loading kernel, another order again).
+SPLITK_SAME_ORDER = [(6144, (2, 8, 13, 16, 32)), (1000, (2, 8, 13, 16, 32)), (151936, (2, 8, 13, 16)),
+                     (151936, (17, 24, 32))]
+
+
+@pytest.mark.parametrize("n,ms", SPLITK_SAME_ORDER, ids=["N6144", "N1000", "N151936-M2to16", "N151936-M17to32"])
+def test_splitk_rows_same_bits_across_m(n, ms):
+    """A row's output from splitk_decode depends only on the number of K
+    partitions, which the configurations fix per family (the partition of
+    64-element line L is L % PARTS, lines are added in increasing order
+    within a partition and partitions in order, whatever the waves, lines
+    per wave or W rows per workgroup): the first two rows (fp32 outputs) are
+    bit-identical across each listed set of A-row counts, on the decode
+    width, on a narrow W (16-row workgroups) and on the LM-head width in its
+    two partition families."""
     k = 1024
-    gen = torch.Generator().manual_seed(n)
+    gen = torch.Generator().manual_seed(n + ms[0])
     a = torch.randn((32, k), generator=gen).to(torch.bfloat16)
     w = (torch.randn((n, k), generator=gen) * 0.1).to(torch.bfloat16)
     a_d, w_d = a.to(DEV), w.to(DEV)
     first = None
-    for m in (2, 8, 13, 16, 32):
+    for m in ms:
         _say(f"splitk rows across M: M={m} N={n} K={k} bf16->f32")
         out = G.gemm_with_kernel(a_d[:m], w_d, L.KERNEL_SPLITK_DECODE, torch.float32, L.B_NK)
         torch.cuda.synchronize()
@@ -456,6 +470,30 @@ def test_splitk_rows_same_bits_across_m(n):
             _check_tolerance(head, a[:2], w, L.B_NK, torch.float32)
         else:
             assert torch.equal(head, first), f"M={m}: {int((head != first).sum())} of the first two rows' outputs differ"
+
+
+@pytest.mark.parametrize("n", [6144, 1000], ids=["N6144", "N1000"])
+def test_splitk_kn_rows_same_bits_across_m(n):
+    """splitk_decode on B[K,N] uses 16 K partitions up to M = 8 and 8 above:
+    the first two rows are bit-identical at M = 2, 5, 8 and again at M = 9,
+    16, 32."""
+    k = 1024
+    gen = torch.Generator().manual_seed(3 * n)
+    a = torch.randn((32, k), generator=gen).to(torch.bfloat16)
+    b = (torch.randn((k, n + 8 - n % 8), generator=gen) * 0.1).to(torch.bfloat16)
+    a_d, b_d = a.to(DEV), b.to(DEV)
+    for ms in ((2, 5, 8), (9, 16, 32)):
+        first = None
+        for m in ms:
+            _say(f"splitk B[K,N] rows across M: M={m} N={b.shape[1]} K={k}")
+            out = G.gemm_with_kernel(a_d[:m], b_d, L.KERNEL_SPLITK_DECODE, torch.float32, L.B_KN)
+            torch.cuda.synchronize()
+            head = out[:2].cpu()
+            if first is None:
+                first = head
+                _check_tolerance(head, a[:2], b, L.B_KN, torch.float32)
+            else:
+                assert torch.equal(head, first), f"M={m}: {int((head != first).sum())} outputs differ"
 
 
 SPLITK64_CASES = [(1000, 3592, 64), (4096, 1000, 33), (5000, 1000, 47), (9000, 1000, 64), (20000, 264, 40)]
@@ -723,7 +761,7 @@ def _check_silu_mul(got: torch.Tensor, a: torch.Tensor, w: torch.Tensor, dout: t
         # magnitude of the terms of silu(g) u: each sum's terms, weighted by
         # the other factor and the SiLU slope bound
         scale = orc.SILU_SLOPE_BOUND * sg * np.abs(u) + np.abs(orc.silu_f64(g)) * su
-        _assert_narrow(orc.narrow_parity(_to_np_out(got, dout), ref, r, scale, NAME[dout]))
+        _assert_narrow(orc.narrow_parity(_to_np_out(got, dout), ref, r, scale, NAME[dout]), NAME[dout])
 
 
 SILU_SHAPES = [(1, 1, 8), (1, 37, 64), (5, 7, 72), (16, 100, 136), (31, 65, 264), (33, 129, 520),

@@ -312,6 +312,30 @@ def test_narrow_parity_catches_what_the_fraction_rule_passed():
     assert not stats["ok"].all() or stats["cancel_beyond"] > orc.cancellation_cap(bad.size)
 
 
+def test_cancellation_cap_rejects_a_tenfold_rate():
+    """The per-dtype cap rejects a kernel whose cancellation elements go
+    beyond 2 ulp ten times as often as the library's (fp16: measured 1 in
+    10^4, planted 1 in 1500 of the outputs, all among the cancellation
+    elements), which the earlier flat cap of 1 in 1000 let through."""
+    a, w = _fp16_down_sample(m=256, n=192)
+    a64, w64 = a.astype(np.float64), w.astype(np.float64)
+    r = orc.gemm_f64(a64, w64)
+    s = orc.abs_products_f64(a64, w64)
+    ref = (torch.from_numpy(a).float() @ torch.from_numpy(w).float().T).to(torch.float16).numpy()
+    cancel = np.flatnonzero((np.abs(r) <= orc.CANCELLATION * s).reshape(-1))
+    planted = ref.size // 1500
+    assert cancel.size > 4 * planted
+    bad = ref.copy()
+    idx = np.random.default_rng(1).choice(cancel, size=planted, replace=False)
+    flat = bad.reshape(-1).view(np.uint16)
+    flat[idx] = flat[idx] ^ 0x8000       # sign flipped: far beyond 2 ulp unless the value is zero
+    stats = orc.narrow_parity(bad, ref, r, s, "f16")
+    assert stats["ok"].all()             # every planted element is a cancellation element
+    assert stats["cancel_beyond"] >= planted * 9 // 10
+    assert stats["cancel_beyond"] <= max(8, ref.size // 1000)            # the flat cap passes it
+    assert stats["cancel_beyond"] > orc.cancellation_cap(ref.size, "f16")  # the per-dtype cap does not
+
+
 def test_narrow_parity_exempts_only_cancellations():
     """An element whose exact value cancels (|r| under 2^-6 of the sum of
     its terms' magnitudes) may exceed 2 ulp (its low bits follow the
@@ -325,7 +349,8 @@ def test_narrow_parity_exempts_only_cancellations():
     assert stats["beyond"] == 2 and stats["cancel_beyond"] == 1
     np.testing.assert_array_equal(stats["ok"], [[True, False]])
     assert stats["max_ulp_checked"] == 3
-    assert orc.cancellation_cap(100) == 8 and orc.cancellation_cap(10 ** 6) == 1000
+    assert orc.cancellation_cap(100) == 8 and orc.cancellation_cap(10 ** 6) == 500
+    assert orc.cancellation_cap(10 ** 6, "bf16") == 33 and orc.cancellation_cap(8388608, "bf16") == 279
 
 
 def test_rel_frobenius_and_checks():
