@@ -79,6 +79,10 @@ def parse_args():
                    help="only time torch's GPU GEMM with every hipBLASLt / rocBLAS solution searched (TunableOp) "
                         "beside its default choice and the selected kernel here, on the workloads that fit one "
                         "torch call, and print them as one JSON line")
+    p.add_argument("--eager-overhead", action="store_true",
+                   help="only time the host cost of one eager call (nanovllm::gemm under the registration "
+                        "NANOVLLM_GEMM_OPS picks, the Linear path, the bare C ABI, F.linear) and print it as one "
+                        "JSON line")
     return p.parse_args()
 
 
@@ -329,6 +333,68 @@ def run_vendor_tuned(torch, L, W) -> int:
     return 0
 
 
+EAGER_CALLS = 2000
+EAGER_TRIALS = 7
+
+
+def eager_call_overhead(torch, pkg) -> dict:
+    """Host microseconds per eager call on the decode shape (bf16, M = 1,
+    W[6144, 1024]): `calls` launches issued back to back from Python, timed
+    on the host clock before the final synchronize ("host_us", what the
+    caller's thread spends per call) and after it ("wall_us").  The kernel
+    takes ~3 us of GPU time, so both are host-bound.  Median of the trials.
+    Under the op registration NANOVLLM_GEMM_OPS picks (kernels/gemm.py)."""
+    import statistics
+    import time
+
+    F = torch.nn.functional
+    G = sys.modules[pkg.__name__ + ".kernels.gemm"]
+    L = pkg._lib
+    dev = torch.device("cuda:0")
+    a, w = pkg.workloads.make_inputs("bf16_decode_n6144_k1024", 1, device=dev)
+    out = torch.empty(1, w.shape[0], dtype=torch.bfloat16, device=dev)
+    raw = (a.data_ptr(), w.data_ptr(), out.data_ptr(), 1, w.shape[0], w.shape[1], w.shape[1], w.shape[1],
+           w.shape[0], L.B_NK, L.BF16, L.BF16)
+    calls = {
+        "F.linear": lambda: F.linear(a, w),
+        "nanovllm::gemm": lambda: torch.ops.nanovllm.gemm(a, w, None),
+        "linear(backend=hip)": lambda: G.linear(a, w, None, backend="hip"),
+        "C ABI through ctypes, output preallocated": lambda: L.gemm_raw(
+            *raw, torch.cuda.current_stream().cuda_stream),
+    }
+    rows = {}
+    for label, fn in calls.items():
+        for _ in range(200):
+            fn()
+        torch.cuda.synchronize()
+        host, wall = [], []
+        for _ in range(EAGER_TRIALS):
+            t0 = time.perf_counter()
+            for _ in range(EAGER_CALLS):
+                fn()
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            host.append((t1 - t0) / EAGER_CALLS * 1e6)
+            wall.append((t2 - t0) / EAGER_CALLS * 1e6)
+        rows[label] = {"host_us": round(statistics.median(host), 3), "wall_us": round(statistics.median(wall), 3)}
+    return {"registration": G.REGISTRATION, "shape": "bf16 M=1 N=6144 K=1024, W[N,K]", "calls": EAGER_CALLS,
+            "trials": EAGER_TRIALS, "rows": rows}
+
+
+def eager_overhead_other_registration(registration: str) -> dict:
+    """eager_call_overhead under another op registration, in a child process
+    (an op name is registered once per process)."""
+    import subprocess
+
+    env = dict(os.environ, NANOVLLM_GEMM_OPS=registration)
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--eager-overhead"], env=env,
+                          capture_output=True, text=True, timeout=600)
+    if proc.returncode != 0:
+        return {"registration": registration, "error": proc.stderr.strip()[-300:]}
+    return json.loads(proc.stdout.strip().splitlines()[-1])["eager_call_overhead"]
+
+
 # (N, K): q/k/v, down, merged GDN input projection, o_proj / GDN out_proj, a wide W
 DECODE_SWEEP_SHAPES = ((6144, 1024), (1024, 3584), (8224, 1024), (1024, 2048), (16384, 1024))
 
@@ -527,6 +593,10 @@ def main() -> int:
     if args.vendor_tuned:
         torch.cuda.set_device(0)
         return run_vendor_tuned(torch, L, W)
+    if args.eager_overhead:
+        torch.cuda.set_device(0)
+        print(json.dumps({"eager_call_overhead": eager_call_overhead(torch, pkg)}), flush=True)
+        return 0
     if args.matrix:
         torch.cuda.set_device(0)
         rows = reference_matrix(torch, L, W, emit=lambda line: print(line, flush=True))
@@ -717,6 +787,21 @@ def main() -> int:
                 launches = [launcher(a_o, bs[i % nbuf], o_o, om, ow.n, ow.k, ow.b_layout, ow.dtype_in,
                                      ow.dtype_out) for i in range(reps)]
                 t_ms = median_graph_ms(torch, launches, trials=3)
+                # torch's GPU GEMM on the same operands (the same W rotation):
+                # F.linear on W[N,K], torch.matmul on B[K,N], and for fp32
+                # logits from bf16 torch.mm(a, w.t(), out_dtype=torch.float32).
+                if ow.b_layout != L.B_NK:
+                    v_call, v_fn = "torch.matmul(a, b)", (lambda aa, bb: torch.matmul(aa, bb))
+                elif ow.dtype_out != ow.dtype_in:
+                    v_call = "torch.mm(a, w.t(), out_dtype=torch.float32)"
+                    v_fn = (lambda aa, bb: torch.mm(aa, bb.t(), out_dtype=torch.float32))
+                else:
+                    v_call, v_fn = "F.linear(a, w)", (lambda aa, bb: torch.nn.functional.linear(aa, bb))
+                try:
+                    v_ms = median_graph_ms(torch, [(lambda bb=bs[i % nbuf], aa=a_o: v_fn(aa, bb))
+                                                   for i in range(reps)], trials=3)
+                except Exception as exc:  # comparison only; never fails the bench
+                    v_ms, v_call = float("nan"), f"{v_call}: {str(exc)[:120]}"
                 fl = W.problem_flops(om, ow.n, ow.k)
                 byts = W.problem_bytes(om, ow.n, ow.k, ow.dtype_in, ow.dtype_out)
                 tf = fl / (t_ms * 1e-3) / 1e12
@@ -727,9 +812,11 @@ def main() -> int:
                                             code[ow.dtype_out], True))
                 other.append({"workload": oname, "m": om, "us": round(t_ms * 1e3, 3), "TFLOP/s": round(tf, 2),
                               "frac_mfma": round(tf / pk, 4), "GB/s": round(gbs, 1),
-                              "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": ko})
+                              "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": ko,
+                              "torch_gpu_us": None if math.isnan(v_ms) else round(v_ms * 1e3, 3),
+                              "torch_gpu_call": v_call})
                 log(f"{oname} M={om}: {t_ms * 1e3:.1f} us  {tf:.1f} TFLOP/s ({100 * tf / pk:.1f}%)  "
-                    f"{gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)  [{ko}]")
+                    f"{gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)  [{ko}]; torch {v_ms * 1e3:.1f} us ({v_call})")
                 del bs, a_o, b_o, o_o
         extras["other_workloads"] = other
 
@@ -1005,6 +1092,19 @@ def main() -> int:
         log("reference shape matrix (bf16, fp32 out; B[K,N] / W[N,K]): " + ", ".join(
             f"{r['label']} {float(r['dispatch_ms']) * 1e3:.2f} / {float(r['dispatch_nk_ms']) * 1e3:.2f} us"
             for r in mrows))
+
+    # ------------------------------------- host cost of one eager call
+    if not args.no_extras:
+        eo = eager_call_overhead(torch, pkg)
+        other_reg = [r for r in sys.modules[pkg.__name__ + ".kernels.gemm"].REGISTRATIONS
+                     if r != eo["registration"]]
+        eo["other_registrations"] = [eager_overhead_other_registration(r) for r in other_reg]
+        extras["eager_call_overhead"] = eo
+        log("eager call host us (" + eo["registration"] + "): " + ", ".join(
+            f"{k} {v['host_us']:.2f}" for k, v in eo["rows"].items()))
+        for o in eo["other_registrations"]:
+            if "rows" in o:
+                log(f"  under {o['registration']}: nanovllm::gemm {o['rows']['nanovllm::gemm']['host_us']:.2f} us")
 
     # ------------------------------------------ vendor comparison (not used)
     if not args.no_vendor:

@@ -3,7 +3,9 @@
 Every HIP source under csrc/ is compiled to an object in a temporary
 directory, in parallel, and linked into ``libnanovllm_gemm.so`` next to this
 file.  The library is loaded with ctypes by ``_lib.py``; it has no
-dependency on torch.
+dependency on torch.  ``libnanovllm_torch_ops.so`` (csrc/torch_ops.cpp, host
+C++ against PyTorch's headers) registers nanovllm::gemm / gemm_kn from C++
+over that library.
 
 Usage: ``python inference-systems_amd/build.py`` or ``build()`` from Python.
 
@@ -63,6 +65,13 @@ PROBE_SOURCES = ["probes.hip"]
 PROBE_LIB_PATH = PKG_DIR / "libnanovllm_probes.so"
 SWEEP_SOURCES = ["decode_sweep.hip"]
 SWEEP_LIB_PATH = PKG_DIR / "libnanovllm_decode_sweep.so"
+
+# The C++ registration of nanovllm::gemm / gemm_kn (TORCH_LIBRARY over the
+# C ABI): host code only, built with the host compiler against PyTorch's
+# headers and linked to libnanovllm_gemm.so next to it.
+TORCH_OPS_SOURCE = "torch_ops.cpp"
+TORCH_OPS_LIB_PATH = PKG_DIR / "libnanovllm_torch_ops.so"
+INCLUDE_DIR = PKG_DIR.parent / "include"
 
 
 # Host-only sanitizers for capi.cpp: each -fsanitize= goes to the host pass
@@ -149,7 +158,38 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, sanitize:
         print(f"built {target}")
     if not sanitize and out is None:
         build_probes(verbose=verbose, extra_flags=extra)
+        build_torch_ops(verbose=verbose)
     return target
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """Compile csrc/torch_ops.cpp into libnanovllm_torch_ops.so (needs the
+    in-tree libnanovllm_gemm.so, found at run time through $ORIGIN)."""
+    import torch
+
+    if not LIB_PATH.is_file():
+        raise RuntimeError(f"{LIB_NAME} must be built before {TORCH_OPS_LIB_PATH.name}")
+    tdir = Path(torch.__file__).resolve().parent
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    with tempfile.TemporaryDirectory(prefix="nvgemm_tops_") as tmp:
+        out_tmp = Path(tmp) / TORCH_OPS_LIB_PATH.name
+        cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+               "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+               f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+               f"-I{rocm}/include", f"-I{INCLUDE_DIR}",
+               str(CSRC / TORCH_OPS_SOURCE), "-o", str(out_tmp),
+               f"-L{PKG_DIR}", "-lnanovllm_gemm", f"-L{tdir / 'lib'}", "-lc10", "-lc10_hip", "-ltorch",
+               "-ltorch_cpu", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tdir / 'lib'}"]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"building {TORCH_OPS_LIB_PATH.name} failed:\n{proc.stderr}")
+        final_tmp = TORCH_OPS_LIB_PATH.with_suffix(".so.tmp")
+        shutil.copyfile(out_tmp, final_tmp)
+        os.replace(final_tmp, TORCH_OPS_LIB_PATH)
+    if verbose:
+        print(f"built {TORCH_OPS_LIB_PATH}")
+    return TORCH_OPS_LIB_PATH
 
 
 def _build_aux(sources: list[str], lib_path: Path, verbose: bool, extra_flags: list[str] | None) -> Path:

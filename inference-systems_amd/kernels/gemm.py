@@ -30,6 +30,7 @@ could not be loaded.
 from __future__ import annotations
 
 import os
+from pathlib import Path
 from typing import Optional
 
 import torch
@@ -99,12 +100,43 @@ def _launch(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype], 
     return out
 
 
-@torch.library.custom_op("nanovllm::gemm", mutates_args=())
-def _gemm_op(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    return _launch(a, w, out_dtype, _lib.B_NK)
+# ---------------------------------------------------------------------------
+# Registration of nanovllm::gemm / nanovllm::gemm_kn
+# ---------------------------------------------------------------------------
+# Two registrations of the same schemas over the same C ABI:
+#   torch_library  csrc/torch_ops.cpp, a TORCH_LIBRARY fragment built into
+#                  libnanovllm_torch_ops.so (the nanovllm/csrc/ops.cpp:48-80
+#                  pattern); the dispatcher calls C++ directly.
+#   custom_op      torch.library.custom_op over the ctypes binding below.
+# The default is torch_library when that library is built (it costs less
+# host time per eager call) and custom_op otherwise; NANOVLLM_GEMM_OPS
+# picks one.  Both raise the same messages; neither has a CPU fallback.
+OPS_ENV = "NANOVLLM_GEMM_OPS"
+REGISTRATIONS = ("torch_library", "custom_op")
+TORCH_OPS_LIB = Path(_lib.__file__).resolve().parent / "libnanovllm_torch_ops.so"
 
 
-@_gemm_op.register_fake
+def _choose_registration() -> str:
+    asked = os.environ.get(OPS_ENV, "").strip().lower()
+    if asked and asked not in REGISTRATIONS:
+        raise ValueError(f"{OPS_ENV} must be one of {REGISTRATIONS}, got {asked!r}")
+    # The C++ registration links the in-tree libnanovllm_gemm.so; a library
+    # named by NANOVLLM_GEMM_LIB (a sanitized build) goes through ctypes.
+    usable = TORCH_OPS_LIB.is_file() and _lib.LIB_PATH.is_file() and _lib.library_path() == _lib.LIB_PATH
+    if asked == "torch_library":
+        if not usable:
+            raise _lib.GemmLibraryError(
+                f"{OPS_ENV}=torch_library needs {TORCH_OPS_LIB.name} and {_lib.LIB_PATH.name} built in "
+                f"{TORCH_OPS_LIB.parent} (and NANOVLLM_GEMM_LIB unset)")
+        return asked
+    if asked == "custom_op":
+        return asked
+    return "torch_library" if usable else "custom_op"
+
+
+REGISTRATION = _choose_registration()
+
+
 def _gemm_fake(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     torch._check(w.dim() == 2)
     torch._check(a.shape[-1] == w.shape[1])
@@ -113,18 +145,29 @@ def _gemm_fake(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype
     return a.new_empty((*a.shape[:-1], w.shape[0]), dtype=a.dtype if out_dtype is None else out_dtype)
 
 
-@torch.library.custom_op("nanovllm::gemm_kn", mutates_args=())
-def _gemm_kn_op(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    return _launch(a, b, out_dtype, _lib.B_KN)
-
-
-@_gemm_kn_op.register_fake
 def _gemm_kn_fake(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     torch._check(b.dim() == 2)
     torch._check(a.shape[-1] == b.shape[0])
     torch._check(a.dtype == b.dtype)
     torch._check(a.device == b.device)
     return a.new_empty((*a.shape[:-1], b.shape[1]), dtype=a.dtype if out_dtype is None else out_dtype)
+
+
+if REGISTRATION == "torch_library":
+    torch.ops.load_library(str(TORCH_OPS_LIB))
+    torch.library.register_fake("nanovllm::gemm")(_gemm_fake)
+    torch.library.register_fake("nanovllm::gemm_kn")(_gemm_kn_fake)
+else:
+    @torch.library.custom_op("nanovllm::gemm", mutates_args=())
+    def _gemm_op(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        return _launch(a, w, out_dtype, _lib.B_NK)
+
+    @torch.library.custom_op("nanovllm::gemm_kn", mutates_args=())
+    def _gemm_kn_op(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        return _launch(a, b, out_dtype, _lib.B_KN)
+
+    _gemm_op.register_fake(_gemm_fake)
+    _gemm_kn_op.register_fake(_gemm_kn_fake)
 
 
 def gemm(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:

@@ -62,7 +62,8 @@ def _check_tolerance(got: torch.Tensor, a: torch.Tensor, b: torch.Tensor, layout
     """Narrow outputs: every element within 2 ulp of the fp32-accumulated
     reference rounded once, except elements whose exact value lies within
     the fp32 accumulation bound of zero (oracle.narrow_parity: cancellation
-    elements, |R| <= 2^-6 sum |a w|, at most 1 in 10^3 of them beyond it),
+    elements, |R| <= 2^-6 sum |a w|, at most oracle.cancellation_cap of them
+    beyond it),
     and every element within 2 ulp of R plus that bound, R the float64
     product.
     fp32 outputs: the bound plus relative Frobenius <= 1e-5.  Returns the
@@ -665,6 +666,45 @@ def test_torch_compile_fullgraph():
 
     compiled = torch.compile(f, fullgraph=True)
     assert torch.equal(compiled(a, w), f(a, w))
+
+
+def test_cpp_registration_matches_ctypes_path():
+    """The C++ registration of nanovllm::gemm / gemm_kn (the default when
+    built) gives the ctypes path's bits on every dtype pair and both
+    layouts, and raises the Python contract's message for each violation."""
+    assert G.REGISTRATION == "torch_library"
+    gen = torch.Generator().manual_seed(41)
+    for din, dout in ((torch.float32, None), (torch.float16, None), (torch.float16, torch.float32),
+                      (torch.bfloat16, None), (torch.bfloat16, torch.float32)):
+        for m in (1, 7, 300):
+            a = torch.randn(2, m, 96, generator=gen).to(din).to(DEV)
+            w = (torch.randn(136, 96, generator=gen) * 0.1).to(din).to(DEV)
+            b = (torch.randn(96, 136, generator=gen) * 0.1).to(din).to(DEV)
+            assert torch.equal(torch.ops.nanovllm.gemm(a, w, dout), G._launch(a, w, dout, L.B_NK))
+            assert torch.equal(torch.ops.nanovllm.gemm_kn(a, b, dout), G._launch(a, b, dout, L.B_KN))
+    a = torch.randn(4, 64, device=DEV, dtype=torch.bfloat16)
+    w = torch.randn(8, 64, device=DEV, dtype=torch.bfloat16)
+    bad = [
+        (a, w.half(), None),
+        (a, torch.randn(64, 8, device=DEV, dtype=torch.bfloat16).T, None),
+        (a, torch.randn(8, 32, device=DEV, dtype=torch.bfloat16), None),
+        (a, w, torch.float16),
+        (a.int(), w.int(), None),
+        (a, w.reshape(2, 4, 64), None),
+        (a.T, torch.randn(8, 4, device=DEV, dtype=torch.bfloat16), None),
+        (torch.empty(4, 0, device=DEV, dtype=torch.bfloat16), torch.empty(8, 0, device=DEV, dtype=torch.bfloat16),
+         None),
+    ]
+    for x, y, od in bad:
+        reason = G.contract_reason(x, y, od)
+        assert reason is not None
+        with pytest.raises(RuntimeError) as err:
+            torch.ops.nanovllm.gemm(x, y, od)
+        assert str(err.value).splitlines()[0] == f"nanovllm::gemm: {reason}"
+    kn_reason = G.contract_reason(a, torch.randn(32, 8, device=DEV, dtype=torch.bfloat16), None, L.B_KN)
+    with pytest.raises(RuntimeError) as err:
+        torch.ops.nanovllm.gemm_kn(a, torch.randn(32, 8, device=DEV, dtype=torch.bfloat16))
+    assert str(err.value).splitlines()[0] == f"nanovllm::gemm: {kn_reason}"
 
 
 def test_contract_errors_on_gpu():

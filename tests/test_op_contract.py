@@ -34,6 +34,66 @@ def test_fake_impl_shapes_on_meta(out_dtype):
     assert out.shape == (7, 40) and out.dtype == torch.float32
 
 
+_REGISTRATION_PROBE = r"""
+import json, sys
+sys.path.insert(0, {root!r})
+import torch
+import __graft_entry__ as g
+g.load_package()
+import importlib
+G = importlib.import_module("inference_systems_amd.kernels.gemm")
+msgs = []
+for op in (torch.ops.nanovllm.gemm, torch.ops.nanovllm.gemm_kn):
+    try:
+        op(torch.randn(4, 8, dtype=torch.bfloat16), torch.randn(8, 8, dtype=torch.bfloat16))
+    except RuntimeError as exc:
+        msgs.append(str(exc).splitlines()[0])
+print(json.dumps({{"registration": G.REGISTRATION,
+                  "schemas": [str(torch.ops.nanovllm.gemm.default._schema),
+                              str(torch.ops.nanovllm.gemm_kn.default._schema)],
+                  "cpu_messages": msgs}}))
+"""
+
+
+def _registration_probe(choice):
+    import json
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    env = dict(os.environ)
+    env.pop("NANOVLLM_GEMM_LIB", None)
+    if choice is None:
+        env.pop(G.OPS_ENV, None)
+    else:
+        env[G.OPS_ENV] = choice
+    proc = subprocess.run([sys.executable, "-c", _REGISTRATION_PROBE.format(root=root)], env=env,
+                          capture_output=True, text=True, timeout=300)
+    return proc, (json.loads(proc.stdout.strip().splitlines()[-1]) if proc.returncode == 0 else None)
+
+
+def test_registrations_share_schema_and_messages():
+    """nanovllm::gemm / gemm_kn registered from C++ (TORCH_LIBRARY, the
+    default when built) and from Python (custom_op over ctypes) have the
+    same schemas and reject CPU operands with the same message; with the
+    C++ library built, it is the default."""
+    assert G.TORCH_OPS_LIB.is_file(), "libnanovllm_torch_ops.so is not built"
+    _, default = _registration_probe(None)
+    _, cpp = _registration_probe("torch_library")
+    _, py = _registration_probe("custom_op")
+    assert default["registration"] == "torch_library"
+    assert cpp["registration"] == "torch_library" and py["registration"] == "custom_op"
+    assert cpp["schemas"] == py["schemas"]
+    assert cpp["cpu_messages"] == py["cpu_messages"] == ["nanovllm::gemm: a and w must be CUDA (HIP) tensors"] * 2
+
+
+def test_registration_choice_is_validated():
+    proc, _ = _registration_probe("cuda_graphs")
+    assert proc.returncode != 0 and "NANOVLLM_GEMM_OPS must be one of" in proc.stderr
+
+
 def test_op_rejects_cpu_tensors():
     a = torch.randn(4, 8, dtype=torch.bfloat16)
     w = torch.randn(6, 8, dtype=torch.bfloat16)
