@@ -83,6 +83,10 @@ def parse_args():
                    help="only time the host cost of one eager call (nanovllm::gemm under the registration "
                         "NANOVLLM_GEMM_OPS picks, the Linear path, the bare C ABI, F.linear) and print it as one "
                         "JSON line")
+    p.add_argument("--stability", type=int, default=0, metavar="RUNS",
+                   help="only run the default bench (without the CPU baseline) RUNS times, each in a fresh child "
+                        "process (this process never touches the GPU), and print mean / std / min / max per "
+                        "workload and the ratio to torch's GPU GEMM as one JSON line")
     return p.parse_args()
 
 
@@ -333,6 +337,62 @@ def run_vendor_tuned(torch, L, W) -> int:
     return 0
 
 
+def _stability_cases(d: dict):
+    """(case, ours_us, torch_us or None) of one default bench line."""
+    yield (f"headline {d['config']['workload']}", d["ms_per_step"] * 1e3,
+           d.get("vendor_torch_linear", {}).get("us"))
+    if "headline_w_from_hbm" in d:
+        yield "headline, W rotated from HBM", d["headline_w_from_hbm"]["us"], None
+    for r in d.get("decode_bf16_n6144_k1024", []):
+        yield f"bf16_decode_n6144_k1024 M={r['m']}", r["us"], r.get("torch_gpu_us")
+    for r in d.get("other_workloads", []):
+        yield f"{r['workload']} M={r['m']}", r["us"], r.get("torch_gpu_us")
+    eo = d.get("eager_call_overhead")
+    if eo:
+        yield "eager call host time, nanovllm::gemm M=1", eo["rows"]["nanovllm::gemm"]["host_us"], \
+            eo["rows"]["F.linear"]["host_us"]
+
+
+def run_stability(runs: int) -> int:
+    """The default bench (no CPU baseline) in `runs` fresh child processes;
+    per case the mean, sample std, min and max of its microseconds, the same
+    for torch's GPU GEMM where the bench times it, and torch / ours of the
+    means.  This process imports neither torch nor the library."""
+    import statistics
+    import subprocess
+
+    samples: dict = {}
+    for i in range(runs):
+        proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--no-cpu"], capture_output=True, text=True,
+                              timeout=900)
+        if proc.returncode != 0:
+            print(proc.stderr[-2000:], file=sys.stderr)
+            return proc.returncode
+        d = json.loads(proc.stdout.strip().splitlines()[-1])
+        for case, ours, vendor in _stability_cases(d):
+            samples.setdefault(case, []).append((ours, vendor))
+        log(f"stability run {i + 1}/{runs}: headline {d['ms_per_step'] * 1e3:.2f} us")
+
+    def stats(xs):
+        return {"mean": round(statistics.fmean(xs), 3), "std": round(statistics.stdev(xs), 3) if len(xs) > 1 else 0.0,
+                "min": round(min(xs), 3), "max": round(max(xs), 3)}
+    rows = []
+    for case, vals in samples.items():
+        ours = [v[0] for v in vals]
+        row = {"case": case, "runs": len(ours), "us": stats(ours)}
+        vend = [v[1] for v in vals if v[1] is not None]
+        if len(vend) == len(ours):
+            row["torch_us"] = stats(vend)
+            row["torch_over_ours"] = round(statistics.fmean(vend) / statistics.fmean(ours), 3)
+        rows.append(row)
+        log(f"{case}: {row['us']['mean']:.2f} +- {row['us']['std']:.2f} us (min {row['us']['min']:.2f}, "
+            f"max {row['us']['max']:.2f})" + (f"; torch {row['torch_us']['mean']:.2f} +- {row['torch_us']['std']:.2f}"
+                                              f", torch/ours {row['torch_over_ours']:.3f}" if "torch_us" in row else ""))
+    print(json.dumps({"stability": {"runs": runs, "command": "python3 bench.py --no-cpu, one fresh process per run",
+                                    "rows": rows}}), flush=True)
+    return 0
+
+
 EAGER_CALLS = 2000
 EAGER_TRIALS = 7
 
@@ -576,6 +636,8 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
+    if args.stability:
+        return run_stability(args.stability)
 
     import torch
     import __graft_entry__
@@ -762,14 +824,18 @@ def main() -> int:
                         for i in range(copies * 10)]
             t_ms = median_graph_ms(torch, launches)
             t_plain = median_plain_ms(torch, launches)
+            # torch's GPU GEMM (F.linear) over the same W rotation
+            t_torch = median_graph_ms(torch, [(lambda bb=ws[i % copies], aa=a_d: torch.nn.functional.linear(aa, bb))
+                                              for i in range(copies * 10)])
             byts = W.problem_bytes(dm, dw.n, dw.k, dw.dtype_in, dw.dtype_out)
             gbs = byts / (t_ms * 1e-3) / 1e9
             kd = L.kernel_name(L.select(dm, dw.n, dw.k, dw.k, dw.k, dw.n, L.B_NK, L.BF16, L.BF16, True))
             rows.append({"m": dm, "us": round(t_ms * 1e3, 3), "GB/s": round(gbs, 1),
                          "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel": kd, "w_buffers": copies,
-                         "plain_launch_us": round(t_plain * 1e3, 3)})
+                         "plain_launch_us": round(t_plain * 1e3, 3), "torch_gpu_us": round(t_torch * 1e3, 3),
+                         "torch_gpu_call": "F.linear(a, w)"})
             log(f"decode M={dm:2d}: {t_ms * 1e3:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% of HBM ({kd}); "
-                f"plain stream launches {t_plain * 1e3:.2f} us")
+                f"plain stream launches {t_plain * 1e3:.2f} us; torch F.linear {t_torch * 1e3:.2f} us")
         extras["decode_bf16_n6144_k1024"] = rows
         del ws
 

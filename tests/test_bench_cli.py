@@ -46,3 +46,25 @@ def test_vendor_tuned_cases_are_workloads():
     for name, m in W:
         assert name in wl and m in wl[name].ms
         assert wl[name].dtype_out == wl[name].dtype_in
+
+
+def test_stability_cases_read_every_timed_row():
+    """`bench.py --stability` reads the headline, its W-from-HBM row, every
+    decode row, every other workload and the eager call of a bench line,
+    with torch's time where the line has one."""
+    line = {
+        "config": {"workload": "bf16_prefill_2048x4096x1024"}, "ms_per_step": 0.0175,
+        "vendor_torch_linear": {"us": 20.5}, "headline_w_from_hbm": {"us": 21.0},
+        "decode_bf16_n6144_k1024": [{"m": 1, "us": 3.8, "torch_gpu_us": 6.0}, {"m": 32, "us": 5.6}],
+        "other_workloads": [{"workload": "fp32_square_1024", "m": 1024, "us": 19.4, "torch_gpu_us": 18.5}],
+        "eager_call_overhead": {"rows": {"nanovllm::gemm": {"host_us": 5.3}, "F.linear": {"host_us": 19.5}}},
+    }
+    cases = list(bench._stability_cases(line))
+    assert cases == [
+        ("headline bf16_prefill_2048x4096x1024", 17.5, 20.5),
+        ("headline, W rotated from HBM", 21.0, None),
+        ("bf16_decode_n6144_k1024 M=1", 3.8, 6.0),
+        ("bf16_decode_n6144_k1024 M=32", 5.6, None),
+        ("fp32_square_1024 M=1024", 19.4, 18.5),
+        ("eager call host time, nanovllm::gemm M=1", 5.3, 19.5),
+    ]
