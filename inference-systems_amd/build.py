@@ -7,7 +7,11 @@ dependency on torch.  ``libnanovllm_torch_ops.so`` (csrc/torch_ops.cpp, host
 C++ against PyTorch's headers) registers nanovllm::gemm / gemm_kn from C++
 over that library.
 
-Usage: ``python inference-systems_amd/build.py`` or ``build()`` from Python.
+Usage: ``python inference-systems_amd/build.py`` or ``build()`` from Python;
+``build.py --resource-usage [KERNEL_STATS_CSV]`` prints every kernel's
+registers, LDS, spills and occupancy from the compiler's
+kernel-resource-usage remarks (with a rocprofv3 kernel-stats CSV: per family,
+and for each kernel that run launched).
 
 ``build(sanitize=True, out=path)`` (``build.py --sanitize PATH``) builds a
 copy whose host code in capi.cpp (argument validation, the selection table,
@@ -221,8 +225,119 @@ def build_probes(verbose: bool = False, extra_flags: list[str] | None = None) ->
     return PROBE_LIB_PATH
 
 
+_REMARK_KEYS = {"VGPRs": "vgpr", "AGPRs": "agpr", "TotalSGPRs": "sgpr", "ScratchSize [bytes/lane]": "scratch",
+                "Occupancy [waves/SIMD]": "occupancy", "SGPRs Spill": "sgpr_spill", "VGPRs Spill": "vgpr_spill",
+                "LDS Size [bytes/block]": "lds"}
+
+
+def resource_usage(sources: list[str] | None = None) -> list[dict]:
+    """Per kernel of the GEMM library: VGPRs, AGPRs, SGPRs, scratch, spills,
+    static LDS and the compiler's occupancy (waves per SIMD), from the gfx950
+    device pass's kernel-resource-usage remarks; kernel names demangled."""
+    import re
+
+    rows = []
+    for name in sources or [n for n in SOURCES if n.endswith(".hip")]:
+        cmd = [hipcc(), "-x", "hip", *HIP_FLAGS, "--offload-device-only", "-Rpass-analysis=kernel-resource-usage",
+               "-c", str(CSRC / name), "-o", os.devnull]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {name}:\n{proc.stderr[-2000:]}")
+        cur = None
+        for line in proc.stderr.splitlines():
+            m = re.search(r"remark: Function Name: (\S+)", line)
+            if m:
+                cur = {"source": name, "mangled": m.group(1)}
+                rows.append(cur)
+                continue
+            m = re.search(r"remark:\s+([^:]+): (\S+) \[-Rpass-analysis", line)
+            if m and cur is not None and m.group(1).strip() in _REMARK_KEYS:
+                val = m.group(2)
+                cur[_REMARK_KEYS[m.group(1).strip()]] = int(val) if val.lstrip("-").isdigit() else val
+    if rows:
+        demangled = subprocess.run(["c++filt"], input="\n".join(r["mangled"] for r in rows), capture_output=True,
+                                   text=True).stdout.splitlines()
+        for r, d in zip(rows, demangled):
+            r["kernel"] = re.sub(r"^(void )?nvg::\(anonymous namespace\)::", "", d).replace("(anonymous namespace)::", "")
+    return rows
+
+
+def resource_table(rows: list[dict]) -> str:
+    lines = ["| source | kernel | VGPR | AGPR | SGPR | LDS bytes | occupancy (waves/SIMD) | VGPR / SGPR spills | "
+             "scratch bytes/lane |", "|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        kern = r["kernel"].split("(")[0] if "(" in r["kernel"] else r["kernel"]
+        lines.append(f"| {r['source']} | `{kern}` | {r.get('vgpr')} | {r.get('agpr')} | {r.get('sgpr')} | "
+                     f"{r.get('lds')} | {r.get('occupancy')} | {r.get('vgpr_spill')} / {r.get('sgpr_spill')} | "
+                     f"{r.get('scratch')} |")
+    return "\n".join(lines)
+
+
+def _short_name(name: str) -> str:
+    """`mfma_staged_kernel<2, 2, 128, 256, ...>` from a demangled name with
+    namespace, return type and parameter list."""
+    import re
+
+    name = re.sub(r"^void ", "", name).replace("nvg::", "").replace("(anonymous namespace)::", "")
+    depth = 0
+    for i, ch in enumerate(name):
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def resource_report(rows: list[dict], stats_csv: Path | None = None) -> str:
+    """Markdown: per kernel family the number of instantiations and the range
+    of each resource; with a rocprofv3 kernel-stats CSV, one row per library
+    kernel that run launched (calls, average duration, resources)."""
+    import csv
+    from collections import defaultdict
+
+    fam = defaultdict(list)
+    for r in rows:
+        fam[_short_name(r["kernel"]).split("<")[0]].append(r)
+
+    def rng(v, key):
+        lo, hi = min(x.get(key, 0) for x in v), max(x.get(key, 0) for x in v)
+        return f"{lo}" if lo == hi else f"{lo}-{hi}"
+    out = ["| family | instantiations | VGPR | AGPR | LDS bytes | occupancy (waves/SIMD) | spills (VGPR / SGPR) | "
+           "scratch |", "|---|---|---|---|---|---|---|---|"]
+    for f, v in fam.items():
+        out.append(f"| `{f}` | {len(v)} | {rng(v, 'vgpr')} | {rng(v, 'agpr')} | {rng(v, 'lds')} | "
+                   f"{rng(v, 'occupancy')} | {rng(v, 'vgpr_spill')} / {rng(v, 'sgpr_spill')} | {rng(v, 'scratch')} |")
+    if stats_csv is not None:
+        by_name = {_short_name(r["kernel"]): r for r in rows}
+        traced = []
+        with open(stats_csv, newline="") as fh:
+            for st in csv.DictReader(fh):
+                key = _short_name(st["Name"])
+                if key in by_name:
+                    traced.append((key, int(st["Calls"]), float(st["AverageNs"]) / 1e3, by_name[key]))
+        traced.sort(key=lambda t: (t[0].split("<")[0], -t[1]))
+        out += ["", "| kernel (as launched) | calls | average us | VGPR | AGPR | SGPR | LDS bytes | "
+                    "workgroups per CU by LDS | occupancy (waves/SIMD) | spills |",
+                "|---|---|---|---|---|---|---|---|---|---|"]
+        for key, calls, avg, r in traced:
+            wg_lds = 163840 // r["lds"] if r.get("lds") else "-"
+            out.append(f"| `{key}` | {calls} | {avg:.2f} | {r.get('vgpr')} | {r.get('agpr')} | {r.get('sgpr')} | "
+                       f"{r.get('lds')} | {wg_lds} | {r.get('occupancy')} | "
+                       f"{r.get('vgpr_spill')} / {r.get('sgpr_spill')} |")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
     if len(sys.argv) == 3 and sys.argv[1] == "--sanitize":
         build(verbose=True, sanitize=True, out=Path(sys.argv[2]))
+    elif len(sys.argv) in (2, 3) and sys.argv[1] == "--resource-usage":
+        # --resource-usage [KERNEL_STATS_CSV]: every kernel's resources; with
+        # a rocprofv3 kernel-stats CSV, the summary per family and one row
+        # per kernel that run launched.
+        usage = resource_usage()
+        if len(sys.argv) == 3:
+            print(resource_report(usage, Path(sys.argv[2])))
+        else:
+            print(resource_table(usage))
     else:
         build(verbose=True)
