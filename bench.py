@@ -231,6 +231,8 @@ def run_probes(torch) -> int:
     log(f"mfma 16x16x32: {out['mfma_bf16_16x16x32']}")
     out["lds_read_b128"] = [P.lds_read(torch, workgroups=w) for w in (P.CUS, 2 * P.CUS)]
     log(f"lds reads: {out['lds_read_b128']}")
+    out["lds_lane_groups"] = P.lds_lane_groups(torch)
+    log(f"lds lane groups: {out['lds_lane_groups']}")
     # Copies from a window small enough for the vector L1 (16 KiB), for L2
     # (256 KiB and 4 MiB, read by every CU of an XCD), one workgroup per CU.
     # With three 1 KiB fragment reads per copied KiB (about a GEMM K-tile's

@@ -278,6 +278,76 @@ __global__ __launch_bounds__(512) void write_tiles_kernel(char* __restrict__ dst
     stamp(clocks, 1);
 }
 
+// LDS lane grouping: every wave of a 256-thread workgroup issues `iters`
+// LDS instructions of W bytes per lane (reads, or writes when WRITE), lane
+// L at byte offset map.off[L] of a 16 KiB region (each wave its own copy of
+// the region, so writes of different waves never meet), 8 in flight before
+// each wait.  Lane 0 of each workgroup's wave 0 writes the shader clocks
+// the loop took to cycles[blockIdx.x]; the host divides by 4 * iters for
+// the LDS cycles per instruction of the CU.  Which lanes the LDS serves in
+// the same clock shows as the maps with no extra cycles.
+struct LaneMap { uint32_t off[64]; };
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int W>
+__device__ __forceinline__ void lds_rd(uint32_t addr, u32x4_t& v) {
+    if constexpr (W == 16) {
+        asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    } else if constexpr (W == 8) {
+        uint64_t x;
+        asm volatile("ds_read_b64 %0, %1" : "=v"(x) : "v"(addr) : "memory");
+        v = u32x4_t{uint32_t(x), uint32_t(x >> 32), 0u, 0u};
+    } else {
+        uint32_t x;
+        asm volatile("ds_read_b32 %0, %1" : "=v"(x) : "v"(addr) : "memory");
+        v = u32x4_t{x, 0u, 0u, 0u};
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void lds_wr(uint32_t addr, u32x4_t v) {
+    if constexpr (W == 16) {
+        asm volatile("ds_write_b128 %0, %1" :: "v"(addr), "v"(v) : "memory");
+    } else if constexpr (W == 8) {
+        const uint64_t x = uint64_t(v[0]) | (uint64_t(v[1]) << 32);
+        asm volatile("ds_write_b64 %0, %1" :: "v"(addr), "v"(x) : "memory");
+    } else {
+        asm volatile("ds_write_b32 %0, %1" :: "v"(addr), "v"(v[0]) : "memory");
+    }
+}
+
+template <int W, bool WRITE>
+__global__ __launch_bounds__(256) void lds_map_kernel(LaneMap map, int iters, uint32_t* sink, uint64_t* cycles) {
+    __shared__ u32x4_t lds[4 * 16384 / 16];
+    for (int i = threadIdx.x; i < 4 * 1024; i += 256) lds[i] = u32x4_t{uint32_t(i), 0u, 0u, 0u};
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t addr = lds_address(lds) + uint32_t(wave) * 16384u + map.off[lane];
+    u32x4_t acc = {0u, 0u, 0u, uint32_t(lane)};
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    for (int i = 0; i < iters; i += 8) {
+        if constexpr (WRITE) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) lds_wr<W>(addr, acc);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            acc[0] += 1u;
+        } else {
+            u32x4_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) lds_rd<W>(addr, v[j]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc ^= v[j];
+        }
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    __syncthreads();
+    if (threadIdx.x == 0) cycles[blockIdx.x] = t1 - t0;
+    sink_wave(sink, fold(acc));
+}
+#pragma clang diagnostic pop
+
 int launched(hipError_t e) { return e == hipSuccess && hipGetLastError() == hipSuccess ? 0 : kErr; }
 
 }  // namespace
@@ -369,6 +439,34 @@ int nvprobe_mfma16(int workgroups, int iters, int chains, uint32_t* sink, uint64
     else if (chains == 8) hipLaunchKernelGGL(mfma16_kernel<8>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
     else if (chains == 16) hipLaunchKernelGGL(mfma16_kernel<16>, dim3(workgroups), dim3(512), 0, s, iters, sink, clocks);
     else return kErr;
+    return launched(hipSuccess);
+}
+
+// offsets: 64 byte offsets (host memory), each a multiple of width and at
+// most 16384 - width; width 4, 8 or 16; write 0 (reads) or 1 (writes);
+// iters a positive multiple of 8; cycles holds `workgroups` uint64.
+int nvprobe_lds_map(const uint32_t* offsets, int width, int write, int workgroups, int iters, uint32_t* sink,
+                    uint64_t* cycles, hipStream_t s) {
+    if (offsets == nullptr || sink == nullptr || cycles == nullptr) return kErr;
+    if (workgroups < 1 || iters < 8 || iters % 8 || (write != 0 && write != 1)) return kErr;
+    if (width != 4 && width != 8 && width != 16) return kErr;
+    LaneMap map;
+    for (int l = 0; l < 64; ++l) {
+        if (offsets[l] % uint32_t(width) || offsets[l] > uint32_t(16384 - width)) return kErr;
+        map.off[l] = offsets[l];
+    }
+#define NVPROBE_LDS_MAP(W, WR) \
+    hipLaunchKernelGGL((lds_map_kernel<W, WR>), dim3(workgroups), dim3(256), 0, s, map, iters, sink, cycles)
+    if (write) {
+        if (width == 16) NVPROBE_LDS_MAP(16, true);
+        else if (width == 8) NVPROBE_LDS_MAP(8, true);
+        else NVPROBE_LDS_MAP(4, true);
+    } else {
+        if (width == 16) NVPROBE_LDS_MAP(16, false);
+        else if (width == 8) NVPROBE_LDS_MAP(8, false);
+        else NVPROBE_LDS_MAP(4, false);
+    }
+#undef NVPROBE_LDS_MAP
     return launched(hipSuccess);
 }
 

@@ -29,6 +29,7 @@ _SIGS = {
     "nvprobe_mfma": [_INT, _INT, _INT, _VP, _VP, _VP],
     "nvprobe_mfma16": [_INT, _INT, _INT, _VP, _VP, _VP],
     "nvprobe_write_tiles": [_VP, _I64, _INT, _INT, _INT, _VP, _VP],
+    "nvprobe_lds_map": [_VP, _INT, _INT, _INT, _INT, _VP, _VP, _VP],
 }
 _lib = None
 
@@ -261,3 +262,52 @@ def sweep_launcher(torch, cfg, a, w, c):
     def f():
         _check(lib.nvsweep_decode(*args, torch.cuda.current_stream().cuda_stream), "decode sweep")
     return f
+
+
+def lds_map_cycles(torch, offsets, width, write=False, workgroups=CUS, iters=4096):
+    """LDS clocks per instruction of a CU when its four waves each issue
+    `iters` instructions of `width` bytes per lane, lane L at byte offset
+    offsets[L] (median over the workgroups, one per CU)."""
+    lib = load()
+    if len(offsets) != 64:
+        raise ValueError("one offset per lane")
+    arr = (ctypes.c_uint32 * 64)(*offsets)
+    sink = torch.zeros(8 * workgroups, dtype=torch.int32, device="cuda")
+    cycles = torch.zeros(workgroups, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(2):   # the first launch warms the clocks
+        _check(lib.nvprobe_lds_map(arr, width, int(write), workgroups, iters, sink.data_ptr(), cycles.data_ptr(),
+                                   stream), "lds_map")
+    torch.cuda.synchronize()
+    return statistics.median(cycles.cpu().tolist()) / (4 * iters)
+
+
+def _pack(lane, bits):
+    return sum(((lane >> b) & 1) << i for i, b in enumerate(bits))
+
+
+def lds_lane_groups(torch):
+    """Which lanes the LDS serves together.  Lane L owns 256-byte row L (so
+    every lane reads its own address) and picks its column from the lane
+    bits in `bits`: the maps whose chosen bits are exactly the bits that vary
+    inside the group the LDS serves per clock take the fewest clocks.  Also
+    all lanes on one column (the worst case) and, for 16-byte accesses, the
+    fragment-read map of the fp32 kernel (16 rows, lane group l / 16 at
+    chunk 4 (l / 16) ^ row)."""
+    from itertools import combinations
+
+    out = {}
+    for width, nbits in ((16, 4), (8, 5), (4, 6)):
+        rows = {}
+        for write in (False, True):
+            res = {}
+            for bits in combinations(range(6), nbits):
+                offs = [lane * 256 + _pack(lane, bits) * width for lane in range(64)]
+                res["bits " + "".join(str(b) for b in bits)] = lds_map_cycles(torch, offs, width, write)
+            res["one column"] = lds_map_cycles(torch, [lane * 256 for lane in range(64)], width, write)
+            if width == 16:
+                offs = [(lane % 16) * 256 + ((4 * (lane // 16)) ^ (lane % 16)) * 16 for lane in range(64)]
+                res["fp32 fragment map"] = lds_map_cycles(torch, offs, width, write)
+            rows["write" if write else "read"] = {k: round(v, 3) for k, v in res.items()}
+        out[f"b{8 * width}"] = rows
+    return out

@@ -37,6 +37,19 @@ def test_probes_refuse_unsafe_sizes_before_launch():
     assert lib.nvprobe_mfma(256, 16, 3, None, None, None) == -1
     assert lib.nvprobe_mfma16(256, 16, 2, None, None, None) == -1
     assert lib.nvprobe_mfma16(0, 16, 4, None, None, None) == -1
+    # LDS lane map: offsets inside the 16 KiB region and aligned to the width
+    import ctypes
+    fake_sink = 1 << 20
+    ok = (ctypes.c_uint32 * 64)(*[lane * 256 for lane in range(64)])
+    high = (ctypes.c_uint32 * 64)(*([lane * 256 for lane in range(63)] + [16384 - 8]))
+    odd = (ctypes.c_uint32 * 64)(*([4] + [lane * 256 for lane in range(1, 64)]))
+    assert lib.nvprobe_lds_map(high, 16, 0, 256, 64, fake_sink, fake_sink, None) == -1
+    assert lib.nvprobe_lds_map(odd, 8, 0, 256, 64, fake_sink, fake_sink, None) == -1
+    assert lib.nvprobe_lds_map(ok, 12, 0, 256, 64, fake_sink, fake_sink, None) == -1
+    assert lib.nvprobe_lds_map(ok, 16, 2, 256, 64, fake_sink, fake_sink, None) == -1
+    assert lib.nvprobe_lds_map(ok, 16, 0, 256, 60, fake_sink, fake_sink, None) == -1
+    assert lib.nvprobe_lds_map(ok, 16, 0, 0, 64, fake_sink, fake_sink, None) == -1
+    assert lib.nvprobe_lds_map(None, 16, 0, 256, 64, fake_sink, fake_sink, None) == -1
     # each 128-row tile writes 512 bytes per row: ld must cover tiles_n of them
     assert lib.nvprobe_write_tiles(None, 8192 - 16, 16, 16, 1, None, None) == -1
     assert lib.nvprobe_write_tiles(None, 8192 + 8, 16, 16, 1, None, None) == -1
