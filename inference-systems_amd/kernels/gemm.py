@@ -135,6 +135,19 @@ def _choose_registration() -> str:
 
 
 REGISTRATION = _choose_registration()
+if REGISTRATION == "torch_library":
+    try:
+        torch.ops.load_library(str(TORCH_OPS_LIB))
+    except (OSError, RuntimeError) as exc:
+        # Asked for by name: fail.  By default: the custom_op registration
+        # below reaches the same kernels through ctypes.
+        if os.environ.get(OPS_ENV, "").strip().lower() == "torch_library":
+            raise _lib.GemmLibraryError(f"failed to load {TORCH_OPS_LIB}: {exc}") from exc
+        import warnings
+
+        warnings.warn(f"{TORCH_OPS_LIB.name} did not load ({exc}); registering nanovllm::gemm through ctypes",
+                      RuntimeWarning, stacklevel=2)
+        REGISTRATION = "custom_op"
 
 
 def _gemm_fake(a: torch.Tensor, w: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
@@ -154,7 +167,6 @@ def _gemm_kn_fake(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dt
 
 
 if REGISTRATION == "torch_library":
-    torch.ops.load_library(str(TORCH_OPS_LIB))
     torch.library.register_fake("nanovllm::gemm")(_gemm_fake)
     torch.library.register_fake("nanovllm::gemm_kn")(_gemm_kn_fake)
 else:
