@@ -579,36 +579,6 @@ int launch_tile(const Problem& p, hipStream_t s) {
 //     128 x 128 choices only.
 constexpr int64_t kSmallGridTiles = kCus / 2;
 
-// Columns [c0, c0 + nc) of the problem as a problem of their own.
-inline Problem column_range(const Problem& p, int64_t c0, int64_t nc) {
-    const int in_bytes = 2, out_bytes = p.dtype_out == NANOVLLM_GEMM_F32 ? 4 : 2;
-    Problem q = p;
-    q.n = nc;
-    q.b = static_cast<const char*>(p.b) + (p.b_layout == NANOVLLM_GEMM_B_KN ? c0 : c0 * p.ldb) * in_bytes;
-    q.c = static_cast<char*>(p.c) + c0 * out_bytes;
-    return q;
-}
-
-// A grid of 128 x 256 tiles with more than one round on the CUs and a last
-// round at most half full runs the full rounds on a column range and the
-// remaining columns as 128 x 128 tiles in a second launch, one round: the
-// last round's CUs then each take half a tile instead of one while the
-// others idle (LM head, 512 x 151936 x 1024: 2376 tiles, 9 full rounds and
-// 72 tiles).  Every tile choice sums K in one order, so no bit changes.
-// Returns 1 when the grid does not qualify.
-template <int DT, int DT_OUT, int KN>
-int launch_split_tail(const Problem& p, hipStream_t s) {
-    const int64_t tiles_m = (p.m + 127) / 128;
-    const int64_t wide = tiles_m * ((p.n + 255) / 256);
-    const int64_t full = wide / kCus, rem = wide % kCus;
-    if (full < 1 || rem == 0 || rem > kCus / 2) return 1;
-    const int64_t cols = (full * kCus / tiles_m) * 256;
-    if (cols <= 0 || cols >= p.n || tiles_m * ((p.n - cols + 127) / 128) > kCus) return 1;
-    const int rc = launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI_NONE, 0, 1, KN>(column_range(p, 0, cols), s);
-    if (rc != NANOVLLM_GEMM_OK) return rc;
-    return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI_NONE, 0, 1, KN>(column_range(p, cols, p.n - cols), s);
-}
-
 template <int DT, int DT_OUT, int EPI, int RS = 0>
 int launch_epi(const Problem& p, hipStream_t s) {
     // A fused gate/up tile covers half its W rows in output columns.
@@ -628,13 +598,8 @@ int launch_epi(const Problem& p, hipStream_t s) {
     }
     if constexpr (EPI != EPI_ARGMAX) {
         const int64_t wide = ((p.m + 127) / 128) * ((n_tiles + 255) / 256);
-        if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2)) {
-            if constexpr (EPI == EPI_NONE && RS == 0) {
-                const int rc = launch_split_tail<DT, DT_OUT, 0>(p, s);
-                if (rc != 1) return rc;
-            }
+        if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2))
             return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI, RS, 1>(p, s);
-        }
     }
     if (tiles <= kCus) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI, RS, 1>(p, s);
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI, RS, 0>(p, s);
@@ -649,11 +614,8 @@ int launch_kn(const Problem& p, hipStream_t s) {
     const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
     if (tiles <= kSmallGridTiles) return launch_tile<DT, DT_OUT, 64, 64, 2, 2, 3, EPI_NONE, 0, 1, 1>(p, s);
     const int64_t wide = ((p.m + 127) / 128) * ((p.n + 255) / 256);
-    if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2)) {
-        const int rc = launch_split_tail<DT, DT_OUT, 1>(p, s);
-        if (rc != 1) return rc;
+    if (wide > kCus / 2 && (wide <= kCus || wide > 3 * kCus / 2))
         return launch_tile<DT, DT_OUT, 128, 256, 2, 4, 3, EPI_NONE, 0, 1, 1>(p, s);
-    }
     if (tiles <= kCus) return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 3, EPI_NONE, 0, 1, 1>(p, s);
     return launch_tile<DT, DT_OUT, 128, 128, 2, 2, 2, EPI_NONE, 0, 0, 1>(p, s);
 }

@@ -337,21 +337,17 @@ def test_staged_tile_choices_same_bits(din):
 
 @pytest.mark.parametrize("layout", [L.B_NK, L.B_KN], ids=["nk", "kn"])
 @pytest.mark.parametrize("dout", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-def test_staged_split_tail_same_bits(layout, dout):
-    """A 128 x 256 grid with a last round at most half full runs its full
-    rounds and then the remaining columns as 128 x 128 tiles in a second
-    launch: M = 512, N = 33000 is 4 x 129 = 516 wide tiles (two rounds of
-    256 and 4), so columns 0-32767 take 128 x 256 tiles and the ragged 232
-    columns after them 128 x 128.  The first 100 rows equal, bit for bit,
-    the same rows computed at M = 100 (one launch of 64 x 64 tiles), every
-    column including both sides of column 32768, and sampled rows meet the
-    tolerance."""
+def test_staged_multi_round_same_bits(layout, dout):
+    """A 128 x 256 grid of more than one round on the CUs (M = 512, N =
+    33000: 4 x 129 = 516 tiles, a ragged last column of tiles): the first
+    100 rows equal, bit for bit, the same rows computed at M = 100 (64 x 64
+    tiles), every column, and sampled rows meet the tolerance."""
     m, n, k, rows = 512, 33000, 256, 100
     gen = torch.Generator().manual_seed(33000)
     a = torch.randn((m, k), generator=gen).bfloat16()
     b = (torch.randn((n, k) if layout == L.B_NK else (k, n), generator=gen) * 0.1).bfloat16()
     a_d, b_d = a.to(DEV), b.to(DEV)
-    _say(f"staged split tail M={m} N={n} K={k} layout={layout} bf16->{NAME[dout]}")
+    _say(f"staged multi-round M={m} N={n} K={k} layout={layout} bf16->{NAME[dout]}")
     full = G.gemm_with_kernel(a_d, b_d, L.KERNEL_MFMA_STAGED, dout, layout)
     small = G.gemm_with_kernel(a_d[:rows], b_d, L.KERNEL_MFMA_STAGED, dout, layout)
     torch.cuda.synchronize()
