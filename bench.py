@@ -87,6 +87,10 @@ def parse_args():
                    help="only run the default bench (without the CPU baseline) RUNS times, each in a fresh child "
                         "process (this process never touches the GPU), and print mean / std / min / max per "
                         "workload and the ratio to torch's GPU GEMM as one JSON line")
+    p.add_argument("--data-patterns", action="store_true",
+                   help="only time the prefill headline and the fp16 down projection, ours and torch's GPU GEMM, "
+                        "on random, mantissa-free, constant and zero inputs (the MFMA-bound kernels run at the "
+                        "power limit, so their speed depends on the data) and print one JSON line")
     return p.parse_args()
 
 
@@ -395,6 +399,46 @@ def run_stability(runs: int) -> int:
     return 0
 
 
+def run_data_patterns(torch, pkg) -> int:
+    """Ours and torch's GPU GEMM (F.linear) on the same operands filled four
+    ways: seeded random values (the bench's inputs), the same values with
+    their mantissa bits cleared, constants, and zeros.  Graph replays of
+    launches after a clock ramp; the same number of MFMAs, LDS accesses and
+    bytes every time, only the bits differ."""
+    L = pkg._lib
+    W = pkg.workloads
+    F = torch.nn.functional
+    dev = torch.device("cuda:0")
+    code = {torch.float16: L.F16, torch.bfloat16: L.BF16}
+    x = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
+    for _ in range(200):
+        x @ x
+    rows = []
+    for name in ("bf16_prefill_2048x4096x1024", "fp16_down_4096x1024x3584"):
+        wl = W.WORKLOADS[name]
+        m = wl.ms[-1]
+        a, w = W.make_inputs(name, m, device=dev)
+        exp_mask = 0x7F80 if wl.dtype_in == torch.bfloat16 else 0x7C00
+        fills = {
+            "random": (a, w),
+            "random, mantissa cleared": ((a.view(torch.int16) & exp_mask).view(wl.dtype_in),
+                                         (w.view(torch.int16) & exp_mask).view(wl.dtype_in)),
+            "constant": (torch.ones_like(a), torch.full_like(w, 0.02)),
+            "zeros": (torch.zeros_like(a), torch.zeros_like(w)),
+        }
+        c = torch.empty(m, wl.n, dtype=wl.dtype_out, device=dev)
+        for fill, (aa, ww) in fills.items():
+            def ours(aa=aa, ww=ww):
+                L.gemm_raw(aa.data_ptr(), ww.data_ptr(), c.data_ptr(), m, wl.n, wl.k, wl.k, wl.k, wl.n, L.B_NK,
+                           code[wl.dtype_in], code[wl.dtype_out], torch.cuda.current_stream().cuda_stream)
+            us = median_graph_ms(torch, [ours] * 100) * 1e3
+            tus = median_graph_ms(torch, [(lambda aa=aa, ww=ww: F.linear(aa, ww))] * 100) * 1e3
+            rows.append({"workload": name, "inputs": fill, "us": round(us, 3), "torch_linear_us": round(tus, 3)})
+            log(f"{name} {fill}: ours {us:.2f} us, torch F.linear {tus:.2f} us")
+    print(json.dumps({"data_patterns": rows}), flush=True)
+    return 0
+
+
 EAGER_CALLS = 2000
 EAGER_TRIALS = 7
 
@@ -657,6 +701,9 @@ def main() -> int:
     if args.vendor_tuned:
         torch.cuda.set_device(0)
         return run_vendor_tuned(torch, L, W)
+    if args.data_patterns:
+        torch.cuda.set_device(0)
+        return run_data_patterns(torch, pkg)
     if args.eager_overhead:
         torch.cuda.set_device(0)
         print(json.dumps({"eager_call_overhead": eager_call_overhead(torch, pkg)}), flush=True)
