@@ -400,41 +400,57 @@ def run_stability(runs: int) -> int:
 
 
 def run_data_patterns(torch, pkg) -> int:
-    """Ours and torch's GPU GEMM (F.linear) on the same operands filled four
-    ways: seeded random values (the bench's inputs), the same values with
-    their mantissa bits cleared, constants, and zeros.  Graph replays of
-    launches after a clock ramp; the same number of MFMAs, LDS accesses and
-    bytes every time, only the bits differ."""
+    """Ours and torch's GPU GEMM on the same operands filled four ways:
+    seeded random values (the bench's inputs), the same values with their
+    mantissa bits cleared (sign and exponent kept), constants, and zeros.
+    Graph replays of launches after a clock ramp; the same number of MFMAs,
+    LDS accesses and bytes every time, only the bits differ.  torch's call
+    is F.linear, or torch.mm(a, w.t(), out_dtype=torch.float32) for the
+    LM head's fp32 logits."""
     L = pkg._lib
     W = pkg.workloads
     F = torch.nn.functional
     dev = torch.device("cuda:0")
-    code = {torch.float16: L.F16, torch.bfloat16: L.BF16}
+    code = {torch.float16: L.F16, torch.bfloat16: L.BF16, torch.float32: L.F32}
     x = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
     for _ in range(200):
         x @ x
     rows = []
-    for name in ("bf16_prefill_2048x4096x1024", "fp16_down_4096x1024x3584"):
+    for name, m, launches in (("bf16_prefill_2048x4096x1024", 2048, 100), ("fp16_down_4096x1024x3584", 4096, 100),
+                              ("bf16_lm_head_n151936_k1024", 512, 20)):
         wl = W.WORKLOADS[name]
-        m = wl.ms[-1]
         a, w = W.make_inputs(name, m, device=dev)
-        exp_mask = 0x7F80 if wl.dtype_in == torch.bfloat16 else 0x7C00
+        # sign and exponent bits, as the int16 view of the 16-bit pattern
+        keep = -128 if wl.dtype_in == torch.bfloat16 else -1024   # 0xFF80 / 0xFC00
         fills = {
             "random": (a, w),
-            "random, mantissa cleared": ((a.view(torch.int16) & exp_mask).view(wl.dtype_in),
-                                         (w.view(torch.int16) & exp_mask).view(wl.dtype_in)),
+            "random, mantissa cleared": ((a.view(torch.int16) & keep).view(wl.dtype_in),
+                                         (w.view(torch.int16) & keep).view(wl.dtype_in)),
             "constant": (torch.ones_like(a), torch.full_like(w, 0.02)),
             "zeros": (torch.zeros_like(a), torch.zeros_like(w)),
         }
         c = torch.empty(m, wl.n, dtype=wl.dtype_out, device=dev)
+        if wl.dtype_out == torch.float32:
+            torch_call = "torch.mm(a, w.t(), out_dtype=torch.float32)"
+        else:
+            torch_call = "F.linear(a, w)"
         for fill, (aa, ww) in fills.items():
             def ours(aa=aa, ww=ww):
                 L.gemm_raw(aa.data_ptr(), ww.data_ptr(), c.data_ptr(), m, wl.n, wl.k, wl.k, wl.k, wl.n, L.B_NK,
                            code[wl.dtype_in], code[wl.dtype_out], torch.cuda.current_stream().cuda_stream)
-            us = median_graph_ms(torch, [ours] * 100) * 1e3
-            tus = median_graph_ms(torch, [(lambda aa=aa, ww=ww: F.linear(aa, ww))] * 100) * 1e3
-            rows.append({"workload": name, "inputs": fill, "us": round(us, 3), "torch_linear_us": round(tus, 3)})
-            log(f"{name} {fill}: ours {us:.2f} us, torch F.linear {tus:.2f} us")
+
+            if wl.dtype_out == torch.float32:
+                def theirs(aa=aa, ww=ww):
+                    torch.mm(aa, ww.t(), out_dtype=torch.float32)
+            else:
+                def theirs(aa=aa, ww=ww):
+                    F.linear(aa, ww)
+            us = median_graph_ms(torch, [ours] * launches) * 1e3
+            tus = median_graph_ms(torch, [theirs] * launches) * 1e3
+            rows.append({"workload": name, "m": m, "inputs": fill, "us": round(us, 3), "torch_gpu_us": round(tus, 3),
+                         "torch_call": torch_call})
+            log(f"{name} M={m} {fill}: ours {us:.2f} us, torch {tus:.2f} us")
+        del a, w, fills, c
     print(json.dumps({"data_patterns": rows}), flush=True)
     return 0
 
