@@ -42,6 +42,7 @@ namespace {
 
 constexpr int kBK = 64;        // K elements per tile = 8 chunks of 16 bytes
 constexpr int kChunks = kBK / 8;
+constexpr int kLdsPerCu = 160 * 1024;   // LDS bytes of one CU (gfx950)
 
 // Source of the K-tail chunks: 16 zero bytes in global memory.
 __device__ u32x4_t g_zero_chunk = {0u, 0u, 0u, 0u};
@@ -98,11 +99,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int BNO = EPI == EPI_SILU_MUL ? BN / 2 : BN;   // output columns per tile
 
     // LDS: the ring of K-tile stages, reused after the K loop for the C tile.
+    // A C tile larger than a CU's LDS (256 x 256 with fp32 output) goes out
+    // in EPASS passes of EP_ROWS rows, one row of the wave grid per pass.
     constexpr int OB = DT_OUT == NANOVLLM_GEMM_F32 ? 4 : 2;     // output bytes
     constexpr int PITCH = BNO * OB + 16;                         // C-tile row pitch in LDS
     constexpr int STAGE_CHUNKS = ROWS * kChunks;
     constexpr int RING_BYTES = STAGES * STAGE_CHUNKS * 16;
-    constexpr int LDS_BYTES = RING_BYTES > BM * PITCH ? RING_BYTES : BM * PITCH;
+    constexpr int EP_ROWS = BM * PITCH <= kLdsPerCu ? BM : WM;
+    constexpr int EPASS = BM / EP_ROWS;
+    static_assert(EP_ROWS * PITCH <= kLdsPerCu && RING_BYTES <= kLdsPerCu, "LDS per CU");
+    static_assert(EPASS == 1 || EPI == EPI_NONE, "C-tile passes: plain store only");
+    constexpr int LDS_BYTES = RING_BYTES > EP_ROWS * PITCH ? RING_BYTES : EP_ROWS * PITCH;
     __shared__ u32x4_t ring[LDS_BYTES / 16];
 
     const int tid = threadIdx.x;
@@ -420,6 +427,67 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     constexpr int CPR = BNO * OB / 16;                           // 16-byte chunks per row
     static_assert(NT % CPR == 0, "rows per copy pass");
     char* ctile = reinterpret_cast<char*>(ring);
+    if constexpr (EPASS > 1) {
+        // Plain store of a C tile larger than LDS: one row of the wave grid
+        // (EP_ROWS = WM rows) per pass, staged and copied out as below.
+        constexpr int EPC = 16 / OB;
+        constexpr int ROWS_PER_PASS = NT / CPR;
+        static_assert(EP_ROWS % ROWS_PER_PASS == 0, "copy passes");
+        const int chunk = tid % CPR;
+        for (int ep = 0; ep < EPASS; ++ep) {
+            __syncthreads();   // the K loop's last reads, or the previous pass's stores, are done with LDS
+            if (wm == ep) {
+#pragma unroll
+                for (int j = 0; j < MJ; ++j) {
+#pragma unroll
+                    for (int i = 0; i < NI; ++i) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const f32x16_t& v = acc[i][j];
+                            char* dst = ctile + (32 * j + r32) * PITCH + (wn * WN + 32 * i + 8 * q + 4 * half) * OB;
+                            if constexpr (DT_OUT == NANOVLLM_GEMM_F32) {
+                                *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                            } else {
+                                *reinterpret_cast<u32x2_t*>(dst) =
+                                    u32x2_t{pack2<DT_OUT>(v[4 * q], v[4 * q + 1]), pack2<DT_OUT>(v[4 * q + 2], v[4 * q + 3])};
+                            }
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            const int64_t mp = m0 + int64_t(ep) * EP_ROWS;   // output row of C-tile row 0
+            if (c_vec && mp + EP_ROWS <= m && n0 + BNO <= n) {
+#pragma unroll
+                for (int pass = 0; pass < EP_ROWS / ROWS_PER_PASS; ++pass) {
+                    const int r = tid / CPR + pass * ROWS_PER_PASS;
+                    const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ctile + r * PITCH + chunk * 16);
+                    __builtin_nontemporal_store(
+                        val, reinterpret_cast<u32x4_t*>(static_cast<char*>(c) + ((mp + r) * ldc + n0 + chunk * EPC) * OB));
+                }
+                continue;
+            }
+            for (int r = tid / CPR; r < EP_ROWS; r += ROWS_PER_PASS) {
+                const int64_t grow = mp + r;
+                const int64_t gcol = n0 + chunk * EPC;
+                if (grow >= m || gcol >= n) continue;
+                const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ctile + r * PITCH + chunk * 16);
+                char* gdst = static_cast<char*>(c) + (grow * ldc + gcol) * OB;
+                if (c_vec && gcol + EPC <= n) {
+                    __builtin_nontemporal_store(val, reinterpret_cast<u32x4_t*>(gdst));
+                } else {
+                    const int valid = int(min_i64(EPC, n - gcol));
+                    if constexpr (OB == 4) {
+                        for (int e = 0; e < valid; ++e) reinterpret_cast<uint32_t*>(gdst)[e] = val[e];
+                    } else {
+                        for (int e = 0; e < valid; ++e)
+                            reinterpret_cast<uint16_t*>(gdst)[e] = uint16_t(val[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+            }
+        }
+        return;
+    }
     __syncthreads();   // every wave is done reading the last K-tile
     constexpr int NIO = EPI == EPI_SILU_MUL ? NI / 2 : NI;     // 32-column output groups per wave
 #pragma unroll
@@ -576,8 +644,29 @@ int launch_tile(const Problem& p, hipStream_t s) {
 //     spread copies, one workgroup per CU (4096 x 1024 x 3584, 256 tiles:
 //     40.0 -> 31.1 us against the burst schedule);
 //   * the greedy head, whose epilogue is written for 4 waves, takes the
-//     128 x 128 choices only.
+//     128 x 128 choices only;
+//   * fp32 outputs (logits) over a W larger than the Infinity Cache, with at
+//     least four rounds of 256 x 256 tiles and no more padded rows than
+//     128-row tiles: 256 x 256 tiles (8 waves of 128 x 64, 2-deep ring,
+//     burst copies; per flop two thirds of the bytes a 128 x 256 tile copies
+//     into LDS, and half the passes over W).  Against 128 x 256, four
+//     interleaved runs of each library in one process, bit-identical
+//     outputs: 512 x 151936 x 1024 212.1-213.0 -> 202.1-207.3 us, 1024 x
+//     151936 x 1024 404.0-405.0 -> 389.0-397.3 us; with a smaller W or bf16
+//     outputs it measured the same (2048 x 37984 fp32 183.8-184.8 against
+//     183.7-184.6, 512 x 151936 bf16 185.1-185.4 against 182.3-185.7, and
+//     bf16 2048 x 37984, 2048 x 8192, 4096 x 4096, 4096 x 8192 within 1-2%).
 constexpr int64_t kSmallGridTiles = kCus / 2;
+constexpr int64_t kInfinityCacheBytes = int64_t(256) << 20;
+
+// Whether an fp32-output plain GEMM takes 256 x 256 tiles (the rule above).
+bool square256_tiles(const Problem& p) {
+    const int64_t tiles_m128 = (p.m + 127) / 128;
+    if (tiles_m128 % 2 != 0) return false;   // 256-row tiles would pad 128 more rows
+    const int64_t tiles = tiles_m128 / 2 * ((p.n + 255) / 256);
+    if (tiles < 4 * kCus) return false;
+    return p.dtype_out == NANOVLLM_GEMM_F32 && p.n * p.k * 2 > kInfinityCacheBytes;
+}
 
 template <int DT, int DT_OUT, int EPI, int RS = 0>
 int launch_epi(const Problem& p, hipStream_t s) {
@@ -595,6 +684,9 @@ int launch_epi(const Problem& p, hipStream_t s) {
             // 15.7-17.0 -> 14.5-14.8 us at K = 2048 against the 3-deep one)
             return launch_tile<DT, DT_OUT, 64, 128, 2, 2, 3, EPI, RS, 1>(p, s);
         }
+    }
+    if constexpr (EPI == EPI_NONE && !RS && DT_OUT == NANOVLLM_GEMM_F32) {
+        if (square256_tiles(p)) return launch_tile<DT, DT_OUT, 256, 256, 2, 4, 2, EPI, RS, 0>(p, s);
     }
     if constexpr (EPI != EPI_ARGMAX) {
         const int64_t wide = ((p.m + 127) / 128) * ((n_tiles + 255) / 256);

@@ -357,6 +357,33 @@ def test_staged_multi_round_same_bits(layout, dout):
     _check_tolerance(full.cpu()[sample], a[sample], b, layout, dout)
 
 
+@pytest.mark.parametrize("din", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_staged_square256_same_bits(din):
+    """fp32 logits over a W larger than the Infinity Cache take 256 x 256
+    tiles whose C tile leaves LDS in two passes of 128 rows: M = 500, N =
+    140001, K = 1000 (W 280 MB; 2 x 547 tiles, a ragged last column, a
+    last tile row that ends inside its second pass, a K tail).  Rows 0-99
+    and 400-499 equal, bit for bit, the same rows computed alone (M = 100:
+    128 x 256 tiles), every column, and rows on both sides of each pass
+    boundary meet the tolerance."""
+    m, n, k = 500, 140001, 1000
+    gen = torch.Generator().manual_seed(140001)
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    a_d, w_d = a.to(DEV), w.to(DEV)
+    _say(f"staged 256x256 M={m} N={n} K={k} {NAME[din]}->f32")
+    full = G.gemm_with_kernel(a_d, w_d, L.KERNEL_MFMA_STAGED, torch.float32, L.B_NK)
+    torch.cuda.synchronize()
+    for r0 in (0, 400):
+        part = G.gemm_with_kernel(a_d[r0:r0 + 100], w_d, L.KERNEL_MFMA_STAGED, torch.float32, L.B_NK)
+        torch.cuda.synchronize()
+        head = full[r0:r0 + 100].cpu()
+        assert torch.equal(head, part.cpu()), f"rows {r0}-{r0 + 99}: {int((head != part.cpu()).sum())} outputs differ"
+    rows = np.array([0, 1, 127, 128, 129, 255, 256, 383, 384, 385, 498, 499])
+    _check_tolerance(full.cpu(), a, w, L.B_NK, torch.float32, rows=rows)
+    del full, w_d
+
+
 STAGED_GRIDS_KN = [(600, 1000, 1000), (1100, 2000, 1000), (2100, 2000, 1000), (2100, 4104, 1000),
                    (2100, 7000, 1000), (40, 520, 72), (2048, 4096, 1024), (1, 6144, 1024), (5, 200, 136)]
 
