@@ -88,9 +88,14 @@ def parse_args():
                         "process (this process never touches the GPU), and print mean / std / min / max per "
                         "workload and the ratio to torch's GPU GEMM as one JSON line")
     p.add_argument("--data-patterns", action="store_true",
-                   help="only time the prefill headline and the fp16 down projection, ours and torch's GPU GEMM, "
-                        "on random, mantissa-free, constant and zero inputs (the MFMA-bound kernels run at the "
-                        "power limit, so their speed depends on the data) and print one JSON line")
+                   help="only time the prefill headline, the fp16 down projection and the LM head at M = 512, "
+                        "ours and torch's GPU GEMM, on random, mantissa-free, constant and zero inputs (the "
+                        "MFMA-bound kernels run at the power limit, so their speed depends on the data) and print "
+                        "one JSON line")
+    p.add_argument("--counter-pair", type=int, default=0, metavar="CALLS",
+                   help="only call nanovllm::gemm and torch's equivalent GEMM on --workload / --m: one call of "
+                        "each compared, then two rounds of CALLS calls of ours followed by CALLS of torch's (a "
+                        "fixed dispatch sequence for rocprofv3 counter passes; no timing)")
     return p.parse_args()
 
 
@@ -455,6 +460,45 @@ def run_data_patterns(torch, pkg) -> int:
     return 0
 
 
+def run_counter_pair(torch, pkg, name: str, m, calls: int) -> int:
+    """nanovllm::gemm and torch's equivalent on a workload's seeded inputs:
+    one call of each compared, then two rounds of `calls` calls of ours and
+    `calls` of torch's, for profiler counter passes that read both
+    kernels on the same operands.  torch's call is F.linear (torch.matmul on
+    B[K,N]), or torch.mm(a, w.t(), out_dtype=torch.float32) for fp32 outputs
+    of 16-bit inputs."""
+    W = pkg.workloads
+    if name not in W.WORKLOADS:
+        print(f"unknown workload {name!r}; choose from {sorted(W.WORKLOADS)}", file=sys.stderr)
+        return 2
+    wl = W.WORKLOADS[name]
+    m = wl.ms[-1] if m is None else m
+    a, b = W.make_inputs(name, m, device="cuda")
+    nk = wl.b_layout == pkg._lib.B_NK
+    op = torch.ops.nanovllm.gemm if nk else torch.ops.nanovllm.gemm_kn
+
+    def ours():
+        return op(a, b, wl.dtype_out)
+
+    def theirs():
+        if not nk:
+            return torch.matmul(a, b)
+        if wl.dtype_out == torch.float32 and wl.dtype_in != torch.float32:
+            return torch.mm(a, b.t(), out_dtype=torch.float32)
+        return torch.nn.functional.linear(a, b)
+
+    diff = (ours().float() - theirs().float()).abs().max().item()
+    log(f"{name} M={m}: max |ours - torch| = {diff:.3g}")
+    for _ in range(2):
+        for f in (ours, theirs):
+            for _ in range(calls):
+                f()
+    torch.cuda.synchronize()
+    print(json.dumps({"counter_pair": {"workload": name, "m": m, "calls": 1 + 2 * calls, "max_abs_diff": diff}}),
+          flush=True)
+    return 0
+
+
 EAGER_CALLS = 2000
 EAGER_TRIALS = 7
 
@@ -717,6 +761,9 @@ def main() -> int:
     if args.vendor_tuned:
         torch.cuda.set_device(0)
         return run_vendor_tuned(torch, L, W)
+    if args.counter_pair:
+        torch.cuda.set_device(0)
+        return run_counter_pair(torch, pkg, args.workload or W.HEADLINE, args.m, args.counter_pair)
     if args.data_patterns:
         torch.cuda.set_device(0)
         return run_data_patterns(torch, pkg)
