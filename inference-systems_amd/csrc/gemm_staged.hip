@@ -8,7 +8,9 @@
 //     grid, 64 x 64 each), K-tiles of 64 elements; grids with enough
 //     128 x 256 tiles for every CU take those (8 waves in a 2x4 grid, 64 x
 //     64 each), grids of at most 128 tiles of 128 x 128 (half the CUs) take
-//     64 x 64 tiles (waves of 32 x 32);
+//     64 x 64 tiles (waves of 32 x 32), and fp32 logits over a W larger
+//     than the Infinity Cache take 256 x 256 tiles (8 waves of 128 x 64, the
+//     fp32 C tile leaving LDS in two passes of 128 rows);
 //   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging) into a ring of STAGES tile buffers; tiles t+1 .. t+STAGES-1
 //     are in flight while tile t is multiplied, and each wave waits on its
@@ -418,8 +420,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void mfma_staged_kernel(
     // is 4 consecutive columns of one output row.  The quads are converted
     // and written into a BM x BN tile in LDS (row pitch padded by 16 bytes so
     // the 32 rows one store instruction touches spread over the banks), then
-    // all 256 threads copy the tile out row by row, 16 bytes per lane, so
-    // every global store instruction writes whole 512-byte row segments.
+    // all the workgroup's threads copy the tile out row by row, 16 bytes per
+    // lane, so every global store instruction writes whole row segments.
     // The copy-out stores are non-temporal: C is written once and not read
     // back by this launch, so it is kept out of L2 where it would evict the
     // A and W tiles other workgroups still read (2048 x 4096 x 1024 bf16:
