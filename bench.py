@@ -72,6 +72,8 @@ def parse_args():
     p.add_argument("--decode-sweep", action="store_true",
                    help="only run every configuration of the decode kernels (rows of A and of W per workgroup, "
                         "waves, lines per wave) on the decode shapes and print them as one JSON line")
+    p.add_argument("--decode-sweep-shapes", default=None, metavar="NxK[,NxK...]",
+                   help="the W shapes of --decode-sweep (default: the Qwen3.5-0.8B decode shapes and 16384x1024)")
     p.add_argument("--matrix", action="store_true",
                    help="only run the reference's shape matrix (fp16 and bf16 over its Qwen3.5 shapes) and print "
                         "it as CSV")
@@ -565,7 +567,18 @@ def eager_overhead_other_registration(registration: str) -> dict:
 DECODE_SWEEP_SHAPES = ((6144, 1024), (1024, 3584), (8224, 1024), (1024, 2048), (16384, 1024))
 
 
-def run_decode_sweep(torch, L) -> int:
+def parse_shapes(text: str) -> tuple:
+    """'151936x1024,6144x1024' -> ((151936, 1024), (6144, 1024))."""
+    shapes = []
+    for item in text.split(","):
+        n, k = item.lower().split("x")
+        shapes.append((int(n), int(k)))
+        if shapes[-1][0] < 1 or shapes[-1][1] < 8 or shapes[-1][1] % 8:
+            raise ValueError(f"bad W shape {item!r}: N >= 1 and K a positive multiple of 8")
+    return tuple(shapes)
+
+
+def run_decode_sweep(torch, L, shapes=DECODE_SWEEP_SHAPES) -> int:
     """Every configuration of the LDS-staged and the register-loading decode
     kernels (inference-systems_amd/csrc/decode_sweep.hip) on the bf16 decode
     shapes, W rotated past the Infinity Cache, graph replays as for the
@@ -577,7 +590,7 @@ def run_decode_sweep(torch, L) -> int:
     cfgs = P.sweep_configs()
     out = {"decode_sweep": "bf16 in and out, W[N,K], W rotated past the Infinity Cache", "rows": []}
     gen = torch.Generator().manual_seed(2024)
-    for n, k in DECODE_SWEEP_SHAPES:
+    for n, k in shapes:
         w_cpu = (torch.randn(n, k, generator=gen) * 0.02).bfloat16()
         w0 = w_cpu.cuda()
         copies = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / (n * k * 2)) + 1)
@@ -757,7 +770,8 @@ def main() -> int:
         return run_probes(torch)
     if args.decode_sweep:
         torch.cuda.set_device(0)
-        return run_decode_sweep(torch, L)
+        shapes = parse_shapes(args.decode_sweep_shapes) if args.decode_sweep_shapes else DECODE_SWEEP_SHAPES
+        return run_decode_sweep(torch, L, shapes)
     if args.vendor_tuned:
         torch.cuda.set_device(0)
         return run_vendor_tuned(torch, L, W)

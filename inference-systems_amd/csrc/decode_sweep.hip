@@ -6,7 +6,8 @@
 // re-measured on the device.  A library of its own (libnanovllm_decode_sweep.so), built from the
 // same kernel templates as the GEMM library.
 //   lds   rows = rows of A per copy, rg = W rows per workgroup, waves, lpb =
-//         lines per wave copied together (16 K partitions)
+//         lines per wave copied together (16 K partitions; with `parts=P`,
+//         P partitions, the counts of the LM-head configurations)
 //   areg  splitk_decode with A's fragments loaded from global memory straight
 //         into registers (only W copied into LDS): rows of A, rg, waves, lpb
 //   kn    the B[K,N] form of splitk_decode: rows of A per copy, 64 columns
@@ -234,7 +235,31 @@ struct SweepConfig {
     X((launch_lines<4, 2, 8, 2>), "lines rows=32 rg=16 waves=8 lpb=2", 32, 0) \
     X((launch_lines<4, 4, 8, 2>), "lines rows=32 rg=32 waves=8 lpb=2", 32, 0) \
     X((launch_lines<4, 1, 4, 4>), "lines rows=32 rg=8 waves=4 lpb=4", 32, 0) \
-    X((launch_lines<4, 2, 4, 4>), "lines rows=32 rg=16 waves=4 lpb=4", 32, 0)
+    X((launch_lines<4, 2, 4, 4>), "lines rows=32 rg=16 waves=4 lpb=4", 32, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 8, 2, 8, EPI_NONE>), "lds rows=8 rg=32 waves=8 lpb=2 parts=8", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 8, 1, 8, EPI_NONE>), "lds rows=8 rg=32 waves=8 lpb=1 parts=8", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 4, 8, 1, 8, EPI_NONE>), "lds rows=8 rg=64 waves=8 lpb=1 parts=8", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 4, 4, 1, 4, EPI_NONE>), "lds rows=8 rg=64 waves=4 lpb=1 parts=4", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 8, 4, 1, 4, EPI_NONE>), "lds rows=8 rg=128 waves=4 lpb=1 parts=4", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 2, 4, 2, 4, EPI_NONE>), "lds rows=8 rg=32 waves=4 lpb=2 parts=4", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 4, 8, 2, 8, EPI_NONE>), "lds rows=8 rg=64 waves=8 lpb=2 parts=8", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 4, 4, 2, 4, EPI_NONE>), "lds rows=8 rg=64 waves=4 lpb=2 parts=4", 8, 0) \
+    X((launch_cfg<BF, BF, 8, 8, 4, 2, 4, EPI_NONE>), "lds rows=8 rg=128 waves=4 lpb=2 parts=4", 8, 0) \
+    X((launch_cfg<BF, BF, 16, 2, 8, 1, 8, EPI_NONE>), "lds rows=16 rg=32 waves=8 lpb=1 parts=8", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 4, 8, 1, 8, EPI_NONE>), "lds rows=16 rg=64 waves=8 lpb=1 parts=8", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 4, 4, 1, 4, EPI_NONE>), "lds rows=16 rg=64 waves=4 lpb=1 parts=4", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 8, 4, 1, 4, EPI_NONE>), "lds rows=16 rg=128 waves=4 lpb=1 parts=4", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 2, 8, 2, 8, EPI_NONE>), "lds rows=16 rg=32 waves=8 lpb=2 parts=8", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 4, 4, 2, 4, EPI_NONE>), "lds rows=16 rg=64 waves=4 lpb=2 parts=4", 16, 0) \
+    X((launch_cfg<BF, BF, 16, 8, 8, 1, 8, EPI_NONE>), "lds rows=16 rg=128 waves=8 lpb=1 parts=8", 16, 0) \
+    X((launch_cfg<BF, BF, 32, 8, 4, 1, 4, EPI_NONE>), "lds rows=32 rg=128 waves=4 lpb=1 parts=4", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 4, 4, 1, 4, EPI_NONE>), "lds rows=32 rg=64 waves=4 lpb=1 parts=4", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 4, 8, 1, 8, EPI_NONE>), "lds rows=32 rg=64 waves=8 lpb=1 parts=8", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 8, 1, 8, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=1 parts=8", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 4, 4, 2, 4, EPI_NONE>), "lds rows=32 rg=64 waves=4 lpb=2 parts=4", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 4, 2, 4, EPI_NONE>), "lds rows=32 rg=32 waves=4 lpb=2 parts=4", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 2, 8, 2, 8, EPI_NONE>), "lds rows=32 rg=32 waves=8 lpb=2 parts=8", 32, 0) \
+    X((launch_cfg<BF, BF, 32, 6, 4, 1, 4, EPI_NONE>), "lds rows=32 rg=96 waves=4 lpb=1 parts=4", 32, 0)
 
 #define X(fn, name, rows, kn) {fn, name, rows, kn},
 const SweepConfig kConfigs[] = {DECODE_SWEEP_CONFIGS(X)};
