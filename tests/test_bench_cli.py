@@ -68,3 +68,14 @@ def test_stability_cases_read_every_timed_row():
         ("fp32_square_1024 M=1024", 19.4, 18.5),
         ("eager call host time, nanovllm::gemm M=1", 5.3, 19.5),
     ]
+
+
+def test_decode_sweep_shapes_parse():
+    """`--decode-sweep-shapes` takes N x K pairs; K must be a positive
+    multiple of 8 (the decode kernels' 16-byte chunks)."""
+    assert bench.parse_shapes("151936x1024") == ((151936, 1024),)
+    assert bench.parse_shapes("6144x1024,1024X3584") == ((6144, 1024), (1024, 3584))
+    import pytest
+    for bad in ("6144x1000x2", "6144x1020", "0x1024", "6144"):
+        with pytest.raises(ValueError):
+            bench.parse_shapes(bad)
