@@ -384,6 +384,27 @@ def test_staged_square256_same_bits(din):
     del full, w_d
 
 
+def test_staged_square256_padded_ldc():
+    """The 256 x 256 tiles with a C row stride that is not a multiple of 16
+    bytes (ldc = N + 3 fp32): every tile of both 128-row passes takes the
+    element-wise store.  Equal, bit for bit, to the same product into a
+    dense C, and the 3 padding columns of every row keep their sentinel."""
+    m, n, k = 512, 140000, 1024
+    gen = torch.Generator().manual_seed(140000)
+    a = torch.randn((m, k), generator=gen).bfloat16().to(DEV)
+    w = (torch.randn((n, k), generator=gen) * 0.1).bfloat16().to(DEV)
+    _say(f"staged 256x256 padded ldc M={m} N={n} K={k}")
+    dense = G.gemm_with_kernel(a, w, L.KERNEL_MFMA_STAGED, torch.float32, L.B_NK)
+    ldc = n + 3
+    padded = torch.full((m, ldc), 7.0, dtype=torch.float32, device=DEV)
+    L.gemm_raw(a.data_ptr(), w.data_ptr(), padded.data_ptr(), m, n, k, k, k, ldc, L.B_NK, L.BF16, L.F32,
+               torch.cuda.current_stream().cuda_stream, kernel=L.KERNEL_MFMA_STAGED)
+    torch.cuda.synchronize()
+    assert torch.equal(padded[:, :n], dense), f"{int((padded[:, :n] != dense).sum())} outputs differ"
+    assert bool((padded[:, n:] == 7.0).all()), "a padding column was written"
+    del a, w, dense, padded
+
+
 STAGED_GRIDS_KN = [(600, 1000, 1000), (1100, 2000, 1000), (2100, 2000, 1000), (2100, 4104, 1000),
                    (2100, 7000, 1000), (40, 520, 72), (2048, 4096, 1024), (1, 6144, 1024), (5, 200, 136)]
 
