@@ -207,6 +207,61 @@ def test_selected_kernel_random_shapes(m, n, k, layout, din, dout):
         _check_tolerance(out.cpu(), a, b, layout, dout)
 
 
+def _random_stride_cases(count=32, seed=3031):
+    """Seeded random problems with padded leading dimensions: the shapes as
+    in _random_selection_cases (at most 5e8 multiply-adds), each of lda,
+    ldb and ldc padded by 0, 1, 3, 8 or 16 elements."""
+    rng = np.random.RandomState(seed)
+    pads = (0, 1, 3, 8, 16)
+    cases = []
+    while len(cases) < count:
+        m = int(np.exp(rng.uniform(0, np.log(2048))))
+        n, k = (int(np.exp(rng.uniform(0, np.log(hi)))) for hi in (8192, 4096))
+        n, k = (max(8, v // 8 * 8) if rng.uniform() < 0.75 else v for v in (n, k))
+        if m * n * k > 5e8:
+            continue
+        din, dout = PAIRS[rng.randint(len(PAIRS))]
+        layout = (L.B_NK, L.B_KN)[rng.randint(2)]
+        pa, pb, pc = (pads[rng.randint(len(pads))] for _ in range(3))
+        cases.append(pytest.param(m, n, k, layout, din, dout, pa, pb, pc,
+                                  id=f"M{m}-N{n}-K{k}-{LAYOUT[layout]}-{NAME[din]}-{NAME[dout]}-pad{pa}.{pb}.{pc}"))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,layout,din,dout,pa,pb,pc", _random_stride_cases())
+def test_selected_kernel_random_padded_strides(m, n, k, layout, din, dout, pa, pb, pc):
+    """nanovllm_gemm through the C ABI with lda = K + pa, ldb = (K or N) + pb
+    and ldc = N + pc (the selection then sees the leading dimensions' 16-byte
+    alignment as well as the shape): the same bars as the contiguous
+    problems, and no write into the padding of C."""
+    gen = torch.Generator().manual_seed(m * 104729 + n * 131 + k * 7 + pa + 5 * pb + 25 * pc)
+    a = torch.randn((m, k), generator=gen).to(din)
+    bshape = (n, k) if layout == L.B_NK else (k, n)
+    b = (torch.randn(bshape, generator=gen) * 0.1).to(din)
+    lda, ldb, ldc = k + pa, bshape[1] + pb, n + pc
+    a_full = torch.zeros((m, lda), dtype=din)
+    a_full[:, :k] = a
+    b_full = torch.zeros((bshape[0], ldb), dtype=din)
+    b_full[:, :bshape[1]] = b
+    ad, bd = a_full.to(DEV), b_full.to(DEV)
+    c = torch.full((m, ldc), 7.0, dtype=dout, device=DEV)
+    kid = L.select(m, n, k, lda, ldb, ldc, layout, CODE[din], CODE[dout],
+                   ad.data_ptr() % 16 == 0 and bd.data_ptr() % 16 == 0)
+    _say(f"selected {L.kernel_name(kid)} {NAME[din]}->{NAME[dout]} {LAYOUT[layout]} M={m} N={n} K={k} "
+         f"lda={lda} ldb={ldb} ldc={ldc}")
+    L.gemm_raw(ad.data_ptr(), bd.data_ptr(), c.data_ptr(), m, n, k, lda, ldb, ldc, layout, CODE[din], CODE[dout],
+               torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert bool((c[:, n:] == 7.0).all()), "a padding column of C was written"
+    out = c[:, :n].contiguous()
+    if din == torch.float32:
+        ref = a.double() @ (b.double().T if layout == L.B_NK else b.double())
+        chk = orc.check_result(out.cpu().numpy(), ref.numpy())
+        assert chk["correct"], chk
+    else:
+        _check_tolerance(out.cpu(), a, b, layout, dout)
+
+
 @pytest.mark.parametrize("kernel", [L.KERNEL_FP32_NAIVE, L.KERNEL_FP32_TILED], ids=lambda k: L.kernel_name(k))
 @pytest.mark.parametrize("layout", [L.B_KN, L.B_NK], ids=["kn", "nk"])
 def test_fp32_reference_known_answer(kernel, layout):
