@@ -1018,6 +1018,39 @@ def test_silu_mul_every_rung_small(kernel, din, dout):
     assert ran > 0
 
 
+def _silu_random_cases(count=16, seed=4047):
+    """Seeded random problems for the fused op's default selection: M
+    log-uniform in [1, 2048), N (output columns, W has 2N rows) in [1, 4096),
+    K a multiple of 8 in [8, 4096), a random half-precision input and output
+    type, at most 1e9 multiply-adds."""
+    rng = np.random.RandomState(seed)
+    cases = []
+    while len(cases) < count:
+        m = int(np.exp(rng.uniform(0, np.log(2048))))
+        n = int(np.exp(rng.uniform(0, np.log(4096))))
+        k = max(8, int(np.exp(rng.uniform(np.log(8), np.log(4096)))) // 8 * 8)
+        if m * 2 * n * k > 1e9:
+            continue
+        din, dout = SILU_PAIRS[rng.randint(len(SILU_PAIRS))]
+        cases.append(pytest.param(m, n, k, din, dout, id=f"M{m}-N{n}-K{k}-{NAME[din]}-{NAME[dout]}"))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,din,dout", _silu_random_cases())
+def test_silu_mul_selected_random_shapes(m, n, k, din, dout):
+    """nanovllm::gemm_silu_mul (the kernel its selection picks) on seeded
+    random problems, held to the fused op's bar."""
+    gen = torch.Generator().manual_seed(m * 7919 + n * 31 + k)
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((2 * n, k), generator=gen) * 0.1).to(din)
+    ad, wd = a.to(DEV), w.to(DEV)
+    _say(f"silu_mul selected {G.silu_mul_selected_kernel(ad, wd, dout)} {NAME[din]}->{NAME[dout]} M={m} N={n} K={k}")
+    out = G.gemm_silu_mul(ad, wd, dout)
+    torch.cuda.synchronize()
+    assert out.shape == (m, n) and out.dtype == dout
+    _check_silu_mul(out.cpu(), a, w, dout)
+
+
 @pytest.mark.parametrize("m", [1, 4, 32, 48, 2048])
 def test_silu_mul_qwen_mlp_shape(m):
     """Qwen3.5-0.8B gate_up_proj (2 x 3584 rows, K = 1024) + SiluAndMul on
@@ -1112,6 +1145,49 @@ def test_argmax_equals_argmax_of_own_logits(kernel, m, n, din, rank):
         assert cand[np.arange(m), tokens.cpu().numpy()].all()
     else:
         assert orc.greedy_token_admissible(tokens.cpu().numpy(), r, s, k).all()
+
+
+def _argmax_random_cases(count=12, seed=5051):
+    """Seeded random problems for the greedy head's default selection: M
+    log-uniform in [1, 512), N (vocabulary) in [2, 200000), K a multiple of 8
+    in [8, 2048), bf16 or fp16, at most 1e9 multiply-adds and 2e7 logits."""
+    rng = np.random.RandomState(seed)
+    cases = []
+    while len(cases) < count:
+        m = int(np.exp(rng.uniform(0, np.log(512))))
+        n = int(np.exp(rng.uniform(np.log(2), np.log(200000))))
+        k = max(8, int(np.exp(rng.uniform(np.log(8), np.log(2048)))) // 8 * 8)
+        if m * n * k > 1e9 or m * n > 2e7:
+            continue
+        din = (torch.bfloat16, torch.float16)[rng.randint(2)]
+        cases.append(pytest.param(m, n, k, din, id=f"M{m}-N{n}-K{k}-{NAME[din]}"))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,din", _argmax_random_cases())
+def test_argmax_selected_random_shapes(m, n, k, din):
+    """nanovllm::gemm_argmax with its default selection on seeded random
+    problems: every token is one the reference's greedy rule (argmax of the
+    logits rounded to the input type, first index on ties) can return for
+    some fp32 summation order of the float64 logits, and its value lies
+    within the accumulation bound of that token's float64 logit."""
+    gen = torch.Generator().manual_seed(m * 104729 + n * 7 + k)
+    a = torch.randn((m, k), generator=gen).to(din)
+    w = (torch.randn((n, k), generator=gen) * 0.1).to(din)
+    _say(f"argmax selected {NAME[din]} M={m} N={n} K={k}")
+    tokens, values = G.gemm_argmax(a.to(DEV), w.to(DEV))
+    torch.cuda.synchronize()
+    assert tokens.shape == (m,) and tokens.dtype == torch.int64 and values.dtype == torch.float32
+    t = tokens.cpu().numpy()
+    assert ((t >= 0) & (t < n)).all()
+    a64, w64 = a.double().numpy(), w.double().numpy()
+    r = orc.gemm_f64(a64, w64)
+    s = orc.abs_products_f64(a64, w64)
+    cand = orc.rounded_greedy_candidates(r, s, k, NAME[din])
+    assert cand[np.arange(m), t].all()
+    rows = np.arange(m)
+    tol = orc.gemm_tolerance(r[rows, t], s[rows, t], k, NAME[din])
+    assert (np.abs(values.cpu().double().numpy() - r[rows, t]) <= tol).all()
 
 
 @pytest.mark.parametrize("m", [1, 32])
