@@ -194,14 +194,14 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                     const bool in_k = koff + chunk * 8 < k;
 #pragma unroll
                     for (int h = 0; h < IW; ++h)
-                        dma16(koff + 8 * h + r8 < k ? static_cast<const void*>(wsrc[h] + koff * ldb) : zero,
-                              dst + 1024u * h);
+                        dma16_stream(koff + 8 * h + r8 < k ? static_cast<const void*>(wsrc[h] + koff * ldb) : zero,
+                                     dst + 1024u * h);
 #pragma unroll
                     for (int h = 0; h < IA; ++h)
                         dma16(in_k ? static_cast<const void*>(asrc[h] + koff) : zero, dst + 1024u * (IW + h));
                 } else if (koff + kLine <= k) {
 #pragma unroll
-                    for (int h = 0; h < IW; ++h) dma16(wsrc[h] + koff, dst + 1024u * h);
+                    for (int h = 0; h < IW; ++h) dma16_stream(wsrc[h] + koff, dst + 1024u * h);
 #pragma unroll
                     for (int h = 0; h < IA; ++h) dma16(asrc[h] + koff, dst + 1024u * (IW + h));
 #pragma unroll
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                     const bool in_k = koff + chunk * 8 < k;
 #pragma unroll
                     for (int h = 0; h < IW; ++h)
-                        dma16(in_k ? static_cast<const void*>(wsrc[h] + koff) : zero, dst + 1024u * h);
+                        dma16_stream(in_k ? static_cast<const void*>(wsrc[h] + koff) : zero, dst + 1024u * h);
 #pragma unroll
                     for (int h = 0; h < IA; ++h)
                         dma16(in_k ? static_cast<const void*>(asrc[h] + koff) : zero, dst + 1024u * (IW + h));

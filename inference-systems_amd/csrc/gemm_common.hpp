@@ -192,6 +192,20 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(src), "s"(lds) : "memory", "m0");
 }
+
+// dma16 with the non-temporal cache policy (nt), for operands a kernel reads
+// exactly once (the weight stream of the decode kernels): their lines do not
+// push out of L2 what every workgroup re-reads (A and the prologue inputs).
+// Measured on the decode kernel's W copies (bit-identical results, three
+// interleaved runs): bf16 6144 x 1024 at M = 4 / 8 / 16 / 32 4.45-4.50 /
+// 4.51-4.53 / 4.80-4.82 / 5.69-5.70 -> 4.27-4.32 / 4.32-4.38 / 4.64-4.68 /
+// 5.39-5.45 us, the 151936-row LM head at M = 8 / 32 53.8 / 64.9 -> 48.6 /
+// 59.5-59.8 us.  (The same policy on the register loads of gemv_decode moved
+// M = 1 by 1% and made the M = 1 LM head's splitk_regs 6% slower.)
+__device__ __forceinline__ void dma16_stream(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // 16-byte global load.
