@@ -167,6 +167,61 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
 #pragma unroll
             for (int g = 0; g < MG; ++g) acc[q][r][g] = f32x4_t{};
 
+    // EPI_ARGMAX: thread x ranks row x / ETPR of A.  On a sampled head the
+    // noise of its columns (log2 E, which does not depend on the logits) is
+    // drawn while the first lines' copies are in flight, for every row (a
+    // greedy row's draws go unused), so a sampled row costs the epilogue
+    // little more than a greedy one.  With 4 or more columns a thread (QUAD)
+    // it takes groups of 4 adjacent columns, 4 (x % ETPR) + 4 ETPR i + j, one
+    // draw serving 4; with fewer it takes columns x % ETPR + ETPR i, as the
+    // greedy ranking does, one draw each.  The row's temperature is
+    // requested before any copy and first used in the epilogue, when every
+    // copy has landed.
+    constexpr int EROWS = MG * 16;
+    constexpr int ETPR = WAVES * 64 / EROWS;
+    static_assert(EPI != EPI_ARGMAX || (ETPR >= 1 && ETPR <= 64 && (ETPR & (ETPR - 1)) == 0),
+                  "a row's threads share a wave");
+    constexpr int ECOLS = 16 * RG;
+    constexpr bool QUAD = ECOLS >= 4 * ETPR;
+    constexpr int NIT = EPI != EPI_ARGMAX ? 1 : QUAD ? (ECOLS + 4 * ETPR - 1) / (4 * ETPR) : (ECOLS + ETPR - 1) / ETPR;
+    const int erow = threadIdx.x / ETPR, esub = threadIdx.x % ETPR;
+    // One unconditional global load (rows past M read row M - 1; a greedy
+    // head reads the first 4 bytes of A, unused), so no branch joins on the
+    // loaded register before its use, and it is counted on vmcnt alone.
+    float traw = 0.0f;   // the row's temperature as given
+    float nlog[NIT][QUAD ? 4 : 1];
+    if constexpr (EPI == EPI_ARGMAX) {
+        const float* tp = sa.temperature != nullptr ? sa.temperature + min_i64(erow, m - 1)
+                                                    : reinterpret_cast<const float*>(a);
+        traw = *tp;
+    }
+    // The empty asm statements take every draw, so the draws stay ahead of
+    // the wait for the copies that follows them.
+    auto draw_noise = [&]() {
+        if (sa.temperature == nullptr) return;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            if constexpr (QUAD) {
+                const int c4 = 4 * esub + 4 * ETPR * it;
+                const u32x4_t x = sample_words(erow, (n0 + c4) >> 2, sa);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    nlog[it][j] = gumbel_log2e(x[j]);
+                    asm volatile("" : "+v"(nlog[it][j]));
+                }
+            } else {
+                // Column cc's word is word cc % 4 of its quad (n0 is a
+                // multiple of 16).
+                const int cc = esub + ETPR * it;
+                const u32x4_t x = sample_words(erow, (n0 + cc) >> 2, sa);
+                const int j = cc & 3;
+                nlog[it][0] = gumbel_log2e(j == 0 ? x[0] : j == 1 ? x[1] : j == 2 ? x[2] : x[3]);
+                asm volatile("" : "+v"(nlog[it][0]));
+            }
+        }
+    };
+    bool drawn = false;
+
     // Wave w takes lines w + WAVES j, j = 0, 1, ...: line j of a trip goes to
     // partition w + WAVES (j % PW), in batches of LPB copied together.
     for (int64_t l0 = wave; l0 < lines; l0 += int64_t(WAVES) * ROUND) {
@@ -237,6 +292,12 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                                     load16_global(in_k ? static_cast<const void*>(afrag[g] + koff + 32 * st) : zero);
                         }
                     }
+                }
+            }
+            if constexpr (EPI == EPI_ARGMAX) {
+                if (!drawn) {
+                    draw_noise();
+                    drawn = true;
                 }
             }
             wait_vmcnt<0>();
@@ -326,6 +387,9 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
     }
+    if constexpr (EPI == EPI_ARGMAX) {
+        if (!drawn) draw_noise();   // a wave with no line of K
+    }
 
     // acc[q][r][g][v] is D[n = 4*(l/16) + v][m = l%16] of W-row group r,
     // A-row group g, in partition wave + WAVES q.  Each wave writes its
@@ -375,12 +439,10 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
         // adjacent threads per row each take every TPR-th column, then a
         // butterfly over those lanes (keys order by value, then by lowest
         // column, so the result does not depend on the split).
-        constexpr int ROWS = MG * 16;
-        constexpr int TPR = WAVES * 64 / ROWS;
-        static_assert(TPR >= 1 && TPR <= 64 && (TPR & (TPR - 1)) == 0, "a row's threads share a wave");
-        const int row = threadIdx.x / TPR, sub = threadIdx.x % TPR;
+        constexpr int TPR = ETPR;
+        const int row = erow, sub = esub;
         uint64_t best = 0;
-        const float t = row < m ? sample_temperature(row, sa) : 0.0f;
+        const float t = sa.temperature != nullptr && row < m && traw > 1e-10f ? traw : 0.0f;   // 0: greedy
         if (row < m && t == 0.0f) {
             for (int cc = sub; cc < 16 * RG; cc += TPR) {
                 if (n0 + cc >= n) break;
@@ -388,16 +450,27 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
                 best = key > best ? key : best;
             }
         } else if (row < m) {
-            // A sampled row: groups of 4 adjacent columns, so one noise draw
-            // serves 4 scores (n0 is a multiple of 16).
-            for (int c4 = 4 * sub; c4 < 16 * RG; c4 += 4 * TPR) {
-                if (n0 + c4 >= n) break;
-                const u32x4_t x = sample_words(row, (n0 + c4) >> 2, sa);
+            // A sampled row, its columns assigned as the draws made during
+            // the K loop were.
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int cc = c4 + j;
-                    if (n0 + cc >= n) break;
-                    const float v = gumbel_score(ranked_logit(total(cc >> 4, row >> 4, cc & 15, row & 15), sa), t, x[j]);
+            for (int it = 0; it < NIT; ++it) {
+                if constexpr (QUAD) {
+                    const int c4 = 4 * sub + 4 * TPR * it;
+                    if (c4 >= ECOLS || n0 + c4 >= n) break;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int cc = c4 + j;
+                        if (n0 + cc >= n) break;
+                        const float v = gumbel_apply(ranked_logit(total(cc >> 4, row >> 4, cc & 15, row & 15), sa),
+                                                     t, nlog[it][j]);
+                        const uint64_t key = argmax_key(v, n0 + cc);
+                        best = key > best ? key : best;
+                    }
+                } else {
+                    const int cc = sub + TPR * it;
+                    if (cc >= ECOLS || n0 + cc >= n) break;
+                    const float v = gumbel_apply(ranked_logit(total(cc >> 4, row >> 4, cc & 15, row & 15), sa), t,
+                                                 nlog[it][0]);
                     const uint64_t key = argmax_key(v, n0 + cc);
                     best = key > best ? key : best;
                 }
@@ -442,80 +515,6 @@ __global__ __launch_bounds__(WAVES * 64) void splitk_decode_kernel(
             store_elem<DT_OUT>(c, row * ldc + col, total(o, g, nn, mm));
         }
     }
-}
-
-// M = 1 on very wide W (the LM head): 16 W rows per 4-wave workgroup, the
-// MFMA fragments loaded straight into registers, eight 16-byte loads per
-// lane in flight.  Its loads touch 16 half-lines each, but with ~9500
-// workgroups at full occupancy it keeps more bytes in flight than the
-// LDS-staged kernel can (N = 151936: 48.4 us, 80% of HBM, against 50.9 us
-// for the best LDS-staged configuration).  EPI_NONE or EPI_ARGMAX.
-constexpr int kRegWaves = 4, kRegUnroll = 8, kRegStep = 32;
-
-template <int DT, int DT_OUT, int EPI>
-__global__ __launch_bounds__(kRegWaves * 64) void splitk_regs_kernel(
-    const uint16_t* __restrict__ a, const uint16_t* __restrict__ w, void* __restrict__ c,
-    int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, uint64_t* __restrict__ keys,
-    SampleArgs sa) {
-    static_assert(EPI != EPI_SILU_MUL, "gate/up pairs need the LDS-staged kernel");
-    __shared__ float red[kRegWaves][16][16];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int i16 = lane & 15;
-    const int grp = lane >> 4;
-    const int64_t n0 = int64_t(blockIdx.x) * 16;
-    const uint16_t* wp = w + min_i64(n0 + i16, n - 1) * ldb + grp * 8;
-    const bool a_in = i16 < m;
-    const uint16_t* ap = a + (a_in ? i16 : 0) * lda + grp * 8;
-    const int64_t steps = (k + kRegStep - 1) / kRegStep;
-    f32x4_t acc = f32x4_t{};
-    for (int64_t s0 = wave; s0 < steps; s0 += kRegWaves * kRegUnroll) {
-        u32x4_t wf[kRegUnroll], af[kRegUnroll];
-#pragma unroll
-        for (int u = 0; u < kRegUnroll; ++u) {
-            const int64_t ks = (s0 + kRegWaves * u) * kRegStep;
-            const bool in_k = ks + grp * 8 < k;   // K % 8 == 0: a chunk is all in or all out
-            wf[u] = in_k ? load16(wp + ks) : u32x4_t{0u, 0u, 0u, 0u};
-            af[u] = (in_k && a_in) ? load16(ap + ks) : u32x4_t{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int u = 0; u < kRegUnroll; ++u) acc = mfma_16x16x32<DT>(wf[u], af[u], acc);
-    }
-    // acc[v] is D[n = 4 (l / 16) + v][m = l % 16].
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][4 * grp + v][i16] = acc[v];
-    __syncthreads();
-    // One thread per (column nn, row mm) of the 16 x 16 tile.
-    const int nn = threadIdx.x & 15, mm = threadIdx.x >> 4;
-    float sum = red[0][nn][mm];
-#pragma unroll
-    for (int wv = 1; wv < kRegWaves; ++wv) sum += red[wv][nn][mm];
-    if constexpr (EPI == EPI_ARGMAX) {
-        // Per row of A, the best of the workgroup's 16 columns: a 16-lane
-        // max over the keys of one row (lanes 16 mm .. 16 mm + 15).
-        uint64_t best = n0 + nn < n && mm < m ? argmax_key(sample_score(sum, mm, n0 + nn, sa), n0 + nn) : 0;
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) {
-            const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(best >> 32), off))) << 32) |
-                                   uint64_t(uint32_t(__shfl_xor(int(best & 0xFFFFFFFFu), off)));
-            best = other > best ? other : best;
-        }
-        if (nn == 0 && mm < m) keys[mm * int64_t(gridDim.x) + blockIdx.x] = best;
-    } else {
-        if (mm < m && n0 + nn < n) store_elem<DT_OUT>(c, mm * ldc + n0 + nn, sum);
-    }
-}
-
-template <int DT, int DT_OUT, int EPI>
-int launch_regs(const Problem& p, hipStream_t s) {
-    if (p.m > 16) return set_error(NANOVLLM_GEMM_EUNSUPPORTED, "splitk_decode: M above the configuration's rows");
-    const int64_t blocks = (p.n + 15) / 16;
-    if (blocks > INT32_MAX) return set_error(NANOVLLM_GEMM_EINVAL, "splitk_decode: grid too large");
-    if (EPI == EPI_ARGMAX) *p.key_blocks = blocks;
-    hipLaunchKernelGGL((splitk_regs_kernel<DT, DT_OUT, EPI>), dim3(static_cast<uint32_t>(blocks)),
-                       dim3(kRegWaves * 64), 0, s, static_cast<const uint16_t*>(p.a),
-                       static_cast<const uint16_t*>(p.b), p.c, p.m, p.n, p.k, p.lda, p.ldb, p.ldc, p.keys, p.sample);
-    return check_launch("splitk_decode");
 }
 
 template <int DT, int DT_OUT, int AROWS, int RG, int WAVES, int LPB, int PARTS, int EPI, int PRO = PRO_NONE,

@@ -201,7 +201,7 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
 // 4.51-4.53 / 4.80-4.82 / 5.69-5.70 -> 4.27-4.32 / 4.32-4.38 / 4.64-4.68 /
 // 5.39-5.45 us, the 151936-row LM head at M = 8 / 32 53.8 / 64.9 -> 48.6 /
 // 59.5-59.8 us.  (The same policy on the register loads of gemv_decode moved
-// M = 1 by 1% and made the M = 1 LM head's splitk_regs 6% slower.)
+// M = 1 by 1%.)
 __device__ __forceinline__ void dma16_stream(const void* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
                  :: "v"(src), "s"(lds) : "memory", "m0");
@@ -353,12 +353,21 @@ __device__ __forceinline__ u32x4_t sample_words(int64_t row, int64_t q, const Sa
 }
 
 // Score of a sampled column from its logit, the row's temperature and its
-// noise word: v / T - ln E (ln from the hardware log2).
-__device__ __forceinline__ float gumbel_score(float v, float t, uint32_t word) {
+// noise word: v / T - ln E (ln from the hardware log2).  gumbel_log2e is
+// the part that does not depend on the logit (log2 E), so a kernel can draw
+// it before the logit is known; gumbel_apply finishes the score.
+__device__ __forceinline__ float gumbel_log2e(uint32_t word) {
     constexpr float kLn2 = 0.693147180559945309f;
     const float u = float((word >> 8) + 1u) * 0x1p-24f;
     const float e = fmaxf(-__builtin_amdgcn_logf(u) * kLn2, 1e-10f);
-    return v / t - __builtin_amdgcn_logf(e) * kLn2;
+    return __builtin_amdgcn_logf(e);
+}
+__device__ __forceinline__ float gumbel_apply(float v, float t, float log2e) {
+    constexpr float kLn2 = 0.693147180559945309f;
+    return v / t - log2e * kLn2;
+}
+__device__ __forceinline__ float gumbel_score(float v, float t, uint32_t word) {
+    return gumbel_apply(v, t, gumbel_log2e(word));
 }
 
 // The score that ranks column col of row row: the ranked logit v (see

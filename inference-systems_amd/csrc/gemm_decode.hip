@@ -154,8 +154,14 @@ template <int DT, int DT_OUT, int EPI, int AROWS, int PRO>
 int launch_rows(const Problem& p, hipStream_t s) {
     const int64_t rows = EPI == EPI_SILU_MUL ? 2 * p.n : p.n;
     if (rows >= kWideN) {
-        if constexpr (EPI != EPI_SILU_MUL && PRO == PRO_NONE && AROWS == 8)
-            if (p.m == 1) return launch_regs<DT, DT_OUT, EPI>(p, s);
+        // M = 1 takes the configuration of M = 2-8, so rows of M = 1-16 share
+        // one sum order.  A kernel of its own for M = 1 (16 W rows per 4-wave
+        // workgroup, fragments loaded straight into registers, eight loads per
+        // lane in flight) led until W was copied non-temporally; against this
+        // configuration after that (W over two copies, three interleaved runs)
+        // it took 54.8-56.4 against 50.4-51.2 us for fp32 logits, 53.4-55.2
+        // against 52.3-53.0 for the greedy head and 52.0-52.3 against
+        // 50.8-51.2 for the sampled one, and was removed.
         if constexpr (AROWS == 32) return launch_cfg<DT, DT_OUT, 32, 8, 4, 1, 4, EPI, PRO>(p, s);
         else if constexpr (AROWS == 16) return launch_cfg<DT, DT_OUT, 16, 2, 8, 1, 8, EPI, PRO>(p, s);
         else return launch_cfg<DT, DT_OUT, 8, 2, 8, 2, 8, EPI, PRO>(p, s);

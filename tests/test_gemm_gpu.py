@@ -587,10 +587,9 @@ def test_splitk_kn_ragged(m, n, k, din, dout):
 
 @pytest.mark.parametrize("m", [1, 5, 13, 29])
 def test_splitk_wide_n_ragged(m):
-    """splitk_decode on N >= 65536: M = 1 takes the register-loading kernel
-    (16 W rows per workgroup), M <= 16 32 rows and M <= 32 128 rows per
-    workgroup of the LDS-staged kernel; a ragged N leaves the last workgroup
-    partly past N (clamped copies, masked stores)."""
+    """splitk_decode on N >= 65536: M <= 16 32 rows and M <= 32 128 rows per
+    workgroup; a ragged N leaves the last workgroup partly past N (clamped
+    copies, masked stores)."""
     n, k = 70001, 256
     _say(f"splitk wide N={n} M={m} K={k}")
     gen = torch.Generator().manual_seed(m)
@@ -627,20 +626,20 @@ def test_splitk_configs_ragged(n, k, m, din, dout):
 
 # (N, A-row counts that share one K-partition order).  Below 65536 W rows
 # every M from 2 to 32 uses 16 partitions; the LM-head width uses 8
-# partitions for M = 2-16 and 4 for M = 17-32 (M = 1 takes the
-# register-loading kernel, another order again).
-SPLITK_SAME_ORDER = [(6144, (2, 8, 13, 16, 32)), (1000, (2, 8, 13, 16, 32)), (151936, (2, 8, 13, 16)),
+# partitions for M = 1-16 and 4 for M = 17-32.
+SPLITK_SAME_ORDER = [(6144, (2, 8, 13, 16, 32)), (1000, (2, 8, 13, 16, 32)), (151936, (1, 2, 8, 13, 16)),
                      (151936, (17, 24, 32))]
 
 
-@pytest.mark.parametrize("n,ms", SPLITK_SAME_ORDER, ids=["N6144", "N1000", "N151936-M2to16", "N151936-M17to32"])
+@pytest.mark.parametrize("n,ms", SPLITK_SAME_ORDER, ids=["N6144", "N1000", "N151936-M1to16", "N151936-M17to32"])
 def test_splitk_rows_same_bits_across_m(n, ms):
     """A row's output from splitk_decode depends only on the number of K
     partitions, which the configurations fix per family (the partition of
     64-element line L is L % PARTS, lines are added in increasing order
     within a partition and partitions in order, whatever the waves, lines
-    per wave or W rows per workgroup): the first two rows (fp32 outputs) are
-    bit-identical across each listed set of A-row counts, on the decode
+    per wave or W rows per workgroup): the first two rows (fp32 outputs; the
+    one row at M = 1) are bit-identical across each listed set of A-row
+    counts, on the decode
     width, on a narrow W (16-row workgroups) and on the LM-head width in its
     two partition families."""
     k = 1024
@@ -648,17 +647,17 @@ def test_splitk_rows_same_bits_across_m(n, ms):
     a = torch.randn((32, k), generator=gen).to(torch.bfloat16)
     w = (torch.randn((n, k), generator=gen) * 0.1).to(torch.bfloat16)
     a_d, w_d = a.to(DEV), w.to(DEV)
-    first = None
+    heads = {}
     for m in ms:
         _say(f"splitk rows across M: M={m} N={n} K={k} bf16->f32")
         out = G.gemm_with_kernel(a_d[:m], w_d, L.KERNEL_SPLITK_DECODE, torch.float32, L.B_NK)
         torch.cuda.synchronize()
-        head = out[:2].cpu()
-        if first is None:
-            first = head
-            _check_tolerance(head, a[:2], w, L.B_NK, torch.float32)
-        else:
-            assert torch.equal(head, first), f"M={m}: {int((head != first).sum())} of the first two rows' outputs differ"
+        heads[m] = out[:2].cpu()
+    first = heads[max(ms)]
+    _check_tolerance(first, a[:2], w, L.B_NK, torch.float32)
+    for m, head in heads.items():
+        rows = head.shape[0]
+        assert torch.equal(head, first[:rows]), f"M={m}: {int((head != first[:rows]).sum())} of the first rows' outputs differ"
 
 
 @pytest.mark.parametrize("n", [6144, 1000], ids=["N6144", "N1000"])
