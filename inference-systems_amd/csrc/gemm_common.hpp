@@ -200,7 +200,10 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
 // interleaved runs): bf16 6144 x 1024 at M = 4 / 8 / 16 / 32 4.45-4.50 /
 // 4.51-4.53 / 4.80-4.82 / 5.69-5.70 -> 4.27-4.32 / 4.32-4.38 / 4.64-4.68 /
 // 5.39-5.45 us, the 151936-row LM head at M = 8 / 32 53.8 / 64.9 -> 48.6 /
-// 59.5-59.8 us.  (The same policy on the register loads of gemv_decode moved
+// 59.5-59.8 us.  The policy gives up the Infinity Cache: with one W
+// re-read call after call (resident there, which a model's decode step,
+// streaming every layer's weights, never is) M = 32 took 4.68 against
+// 3.94 us.  (The same policy on the register loads of gemv_decode moved
 // M = 1 by 1%.)
 __device__ __forceinline__ void dma16_stream(const void* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
